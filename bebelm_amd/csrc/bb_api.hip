@@ -1,0 +1,888 @@
+// bb_api.hip — the C ABI (include/bebelm_moe.h): contexts, HBM-resident weights, and the
+// host-side sequencing of the kernels in the order the reference's model.rs issues them.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/bebelm_moe.h"
+#include "bb_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Fail {
+  int code;
+};
+
+[[noreturn]] void fail(int code, const std::string& msg) {
+  g_err = msg;
+  throw Fail{code};
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(BB_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class F>
+int guard(F&& f) {
+  try {
+    g_err.clear();
+    f();
+    return BB_OK;
+  } catch (const Fail& x) {
+    return x.code;
+  } catch (const std::bad_alloc&) {
+    g_err = "host allocation failed";
+    return BB_ERR_OOM;
+  } catch (const std::exception& x) {
+    g_err = x.what();
+    return BB_ERR_ARG;
+  } catch (...) {
+    g_err = "unknown error";
+    return BB_ERR_ARG;
+  }
+}
+
+bool block_of(uint32_t dt, size_t& elems, size_t& bytes) {  // tensor.rs:68-93
+  switch (dt) {
+    case BB_F32: elems = 1; bytes = 4; return true;
+    case BB_F16: elems = 1; bytes = 2; return true;
+    case BB_Q4_K: elems = 256; bytes = 144; return true;
+    case BB_Q6_K: elems = 256; bytes = 210; return true;
+    default: return false;
+  }
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Tail padding behind every device allocation: the Q6_K loader reads whole dwords around
+// 2-byte-aligned fields, up to one dword past a block's last byte.
+constexpr size_t PAD = 256;
+
+void* dev_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (hipMalloc(&p, round_up(bytes, 256) + PAD) != hipSuccess) {
+    (void)hipGetLastError();
+    fail(BB_ERR_OOM, "hipMalloc of " + std::to_string(bytes) + " bytes failed");
+  }
+  return p;
+}
+
+constexpr int ROUTE_CTR = 0;        // 1 counter
+constexpr int GATEUP_CTR = 64;      // E * ff/256 counters
+constexpr int DOWN_CTR = 4096;      // hidden/32 counters
+constexpr int N_CTR = 16384;
+
+}  // namespace
+
+struct bb_ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  uint8_t* ws = nullptr;
+  size_t ws_bytes = 0;
+  uint8_t* io = nullptr;  // staging for host-pointer calls
+  size_t io_bytes = 0;
+  uint32_t* counters = nullptr;
+  bool profile = false;
+  struct Pending {
+    int id;
+    hipEvent_t a, b;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> event_pool;
+  double kernel_ms[bb::K_COUNT] = {};
+  int64_t launches[bb::K_COUNT] = {};
+};
+
+struct bb_tensor {
+  bb_ctx* ctx;
+  uint32_t dtype;
+  uint64_t dims[4];
+  int ndims;
+  size_t nbytes;
+  uint8_t* dev;
+};
+
+struct bb_moe {
+  bb_ctx* ctx;
+  const bb_tensor *router, *gate, *up, *down;
+  float* bias_dev;
+  int H, F, E, K;
+  size_t stride_g, stride_u, stride_d;
+};
+
+struct bb_dense {
+  bb_ctx* ctx;
+  const bb_tensor *gate, *up, *down;
+  int H, F;
+};
+
+struct bb_stack {
+  bb_ctx* ctx;
+  std::vector<bb_layer_desc> layers;
+  std::vector<float*> gains;
+  float eps;
+  int H;
+  float* h = nullptr;
+  float* normed = nullptr;
+  float* ffn = nullptr;
+  size_t cap_T = 0;
+};
+
+namespace {
+
+void set_device(bb_ctx* c) { check_hip(hipSetDevice(c->device), "hipSetDevice"); }
+
+hipEvent_t take_event(bb_ctx* c) {
+  if (!c->event_pool.empty()) {
+    hipEvent_t e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  check_hip(hipEventCreate(&e), "hipEventCreate");
+  return e;
+}
+
+// Launch wrapper: brackets the launch with events when profiling is on.
+template <class F>
+void launch(bb_ctx* c, int id, F&& f) {
+  if (!c->profile) {
+    check_hip(f(), bb::kernel_name(id));
+    return;
+  }
+  hipEvent_t a = take_event(c), b = take_event(c);
+  check_hip(hipEventRecord(a, c->stream), "hipEventRecord");
+  check_hip(f(), bb::kernel_name(id));
+  check_hip(hipEventRecord(b, c->stream), "hipEventRecord");
+  c->pending.push_back({id, a, b});
+}
+
+void collect(bb_ctx* c) {
+  if (c->pending.empty()) return;
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  for (auto& p : c->pending) {
+    float ms = 0;
+    check_hip(hipEventElapsedTime(&ms, p.a, p.b), "hipEventElapsedTime");
+    c->kernel_ms[p.id] += ms;
+    c->launches[p.id] += 1;
+    c->event_pool.push_back(p.a);
+    c->event_pool.push_back(p.b);
+  }
+  c->pending.clear();
+}
+
+uint8_t* ensure_ws(bb_ctx* c, size_t bytes) {
+  if (bytes > c->ws_bytes) {
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->ws) (void)hipFree(c->ws);
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+    c->ws = static_cast<uint8_t*>(dev_alloc(bytes));
+    c->ws_bytes = bytes;
+  }
+  return c->ws;
+}
+
+uint8_t* ensure_io(bb_ctx* c, size_t bytes) {
+  if (bytes > c->io_bytes) {
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->io) (void)hipFree(c->io);
+    c->io = nullptr;
+    c->io_bytes = 0;
+    c->io = static_cast<uint8_t*>(dev_alloc(bytes));
+    c->io_bytes = bytes;
+  }
+  return c->io;
+}
+
+// Bump allocator over a byte region, 256-byte aligned slices.
+struct Carve {
+  uint8_t* base;
+  size_t off = 0;
+  template <class T>
+  T* take(size_t n) {
+    T* p = reinterpret_cast<T*>(base ? base + off : nullptr);
+    off = round_up(off + n * sizeof(T), 256);
+    return p;
+  }
+};
+
+void need(bool ok, int code, const std::string& msg) {
+  if (!ok) fail(code, msg);
+}
+
+void need_ctx(bb_ctx* c) { need(c != nullptr, BB_ERR_ARG, "null context"); }
+
+void need_loc(int loc) { need(loc == BB_LOC_HOST || loc == BB_LOC_DEVICE, BB_ERR_ARG, "loc must be BB_LOC_HOST or BB_LOC_DEVICE"); }
+
+void need_aligned(const void* p, const char* what) {
+  need(p != nullptr, BB_ERR_ARG, std::string(what) + " is null");
+  need((reinterpret_cast<uintptr_t>(p) & 15) == 0, BB_ERR_ARG, std::string(what) + " must be 16-byte aligned");
+}
+
+size_t tensor_elems(const bb_tensor* t) {
+  size_t n = 1;
+  for (int i = 0; i < t->ndims; ++i) n *= t->dims[i];
+  return n;
+}
+
+// ---- MoE forward on device pointers -----------------------------------------------------------
+
+struct MoeWs {
+  bb::Q8Bufs xq;
+  bb::RouteBufs rb;
+  float* act;
+  bb::Q8Bufs actq;
+  float* slots;
+};
+
+MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
+  const size_t H = m->H, F = m->F, E = m->E, K = m->K;
+  for (int pass = 0; pass < 2; ++pass) {
+    Carve cv{pass ? c->ws : nullptr};
+    MoeWs w;
+    w.xq.q = cv.take<int8_t>(T * H);
+    w.xq.scales = cv.take<float>(T * H / 256);
+    w.xq.sums = cv.take<int32_t>(T * H / 32);
+    w.rb.logits = cv.take<float>(T * E);
+    w.rb.sel = cv.take<int32_t>(T * K);
+    w.rb.wts = cv.take<float>(T * K);
+    w.rb.counts = cv.take<int32_t>(E);
+    w.rb.offsets = cv.take<int32_t>(E + 1);
+    w.rb.perm = cv.take<int32_t>(T * K);
+    w.rb.hit = cv.take<int32_t>(E + 1);
+    w.rb.ties = cv.take<int32_t>(1);
+    w.rb.margin = cv.take<float>(T);
+    w.rb.counter = c->counters + ROUTE_CTR;
+    w.act = cv.take<float>(T * K * F);
+    w.actq.q = cv.take<int8_t>(T * K * F);
+    w.actq.scales = cv.take<float>(T * K * F / 256);
+    w.actq.sums = cv.take<int32_t>(T * K * F / 32);
+    w.slots = cv.take<float>(T * K * H);
+    if (pass == 0) ensure_ws(c, cv.off);
+    else return w;
+  }
+  return {};
+}
+
+// The small-batch route kernel keeps every (token, slot) entry in LDS: T*k <= 1024.
+constexpr size_t SMALL_ENTRIES_MAX = 1024;
+
+void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr) {
+  need(T >= 1, BB_ERR_ARG, "T must be >= 1");
+  need(T * (size_t)m->K <= SMALL_ENTRIES_MAX, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
+  MoeWs w = carve_moe(c, m, T);
+  const int max_hit = (int)std::min<size_t>((size_t)m->E, T * m->K);
+  const int batch_mode = T > 1;
+  launch(c, bb::K_ROUTE, [&] {
+    return bb::launch_route_small(c->stream, reinterpret_cast<const float*>(m->router->dev), m->bias_dev, x, (int)T,
+                                  m->H, m->E, m->K, w.xq, w.rb);
+  });
+  launch(c, bb::K_GATEUP, [&] {
+    return bb::launch_gateup(c->stream, (int)m->gate->dtype, m->gate->dev, m->up->dev, m->stride_g, m->stride_u, m->H,
+                             m->F, m->K, max_hit, batch_mode, w.rb, w.xq, w.act, w.actq, c->counters + GATEUP_CTR);
+  });
+  launch(c, bb::K_DOWN, [&] {
+    return bb::launch_down(c->stream, (int)m->down->dtype, m->down->dev, m->stride_d, m->H, m->F, m->K, (int)T,
+                           max_hit, batch_mode, w.rb, w.actq, w.slots, out, c->counters + DOWN_CTR);
+  });
+  if (tr) {
+    const size_t E = m->E, K = m->K;
+    auto cp = [&](void* dst, const void* src, size_t bytes) {
+      if (dst) check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "trace copy");
+    };
+    cp(tr->logits, w.rb.logits, T * E * 4);
+    cp(tr->sel, w.rb.sel, T * K * 4);
+    cp(tr->w, w.rb.wts, T * K * 4);
+    cp(tr->counts, w.rb.counts, E * 4);
+    cp(tr->offsets, w.rb.offsets, (E + 1) * 4);
+    cp(tr->perm, w.rb.perm, T * K * 4);
+    cp(tr->ties, w.rb.ties, 4);
+    cp(tr->margin, w.rb.margin, T * 4);
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  }
+}
+
+// ---- dense FFN on device pointers (model.rs:459-469 / :262-278) --------------------------------
+void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* out) {
+  const size_t H = d->H, F = d->F;
+  uint8_t* base = nullptr;
+  for (int pass = 0; pass < 2; ++pass) {
+    Carve cv{base};
+    bb::Q8Bufs xq{cv.take<int8_t>(T * H), cv.take<float>(T * H / 256), cv.take<int32_t>(T * H / 32)};
+    float* gate = cv.take<float>(T * F);
+    float* up = cv.take<float>(T * F);
+    bb::Q8Bufs aq{cv.take<int8_t>(T * F), cv.take<float>(T * F / 256), cv.take<int32_t>(T * F / 32)};
+    if (pass == 0) {
+      base = ensure_ws(c, cv.off);
+      continue;
+    }
+    const int nz = T == 1;  // n_tokens == 1 takes matvec (-0.0-started sum), else matmul
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)d->gate->dtype, d->gate->dev, (H / 256) * (d->gate->dtype == BB_Q4_K ? 144 : 210),
+                                (int)(H / 256), F, xq, H, T, gate, F, nz);
+    });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)d->up->dtype, d->up->dev, (H / 256) * (d->up->dtype == BB_Q4_K ? 144 : 210),
+                                (int)(H / 256), F, xq, H, T, up, F, nz);
+    });
+    launch(c, bb::K_ELEMWISE, [&] { return bb::launch_elementwise(c->stream, bb::EW_SWIGLU, gate, gate, up, 0.f, T * F); });
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, gate, T, F, aq); });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)d->down->dtype, d->down->dev,
+                                (F / 256) * (d->down->dtype == BB_Q4_K ? 144 : 210), (int)(F / 256), H, aq, F, T, out,
+                                H, nz);
+    });
+  }
+}
+
+// Runs `body(ptr_map)` with host arrays staged through the context's io buffer.
+struct Io {
+  const void* host;
+  size_t bytes;
+  bool in, out;
+};
+
+template <class F>
+void with_io(bb_ctx* c, int loc, std::vector<Io> ios, F&& body) {
+  std::vector<void*> dev(ios.size());
+  if (loc == BB_LOC_DEVICE) {
+    for (size_t i = 0; i < ios.size(); ++i) {
+      if (ios[i].bytes) need_aligned(ios[i].host, "device pointer");
+      dev[i] = const_cast<void*>(ios[i].host);
+    }
+    body(dev);
+    return;
+  }
+  size_t total = 0;
+  for (auto& io : ios) total = round_up(total + io.bytes, 256);
+  uint8_t* base = ensure_io(c, total + 256);
+  size_t off = 0;
+  for (size_t i = 0; i < ios.size(); ++i) {
+    if (ios[i].bytes) need(ios[i].host != nullptr, BB_ERR_ARG, "null host pointer");
+    dev[i] = base + off;
+    if (ios[i].in && ios[i].bytes)
+      check_hip(hipMemcpyAsync(dev[i], ios[i].host, ios[i].bytes, hipMemcpyHostToDevice, c->stream), "H2D copy");
+    off = round_up(off + ios[i].bytes, 256);
+  }
+  body(dev);
+  for (size_t i = 0; i < ios.size(); ++i)
+    if (ios[i].out && ios[i].bytes)
+      check_hip(hipMemcpyAsync(const_cast<void*>(ios[i].host), dev[i], ios[i].bytes, hipMemcpyDeviceToHost, c->stream),
+                "D2H copy");
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+void check_weight_range(const bb_tensor* w, uint32_t dtype, size_t byte_off, size_t n_in, size_t n_out,
+                        size_t& row_bytes) {
+  need(w != nullptr, BB_ERR_ARG, "null weight tensor");
+  size_t be, bb_;
+  need(block_of(dtype, be, bb_), BB_ERR_DTYPE, "unsupported weight dtype " + std::to_string(dtype));
+  need(dtype == w->dtype, BB_ERR_DTYPE, "dtype does not match the uploaded tensor's");
+  need(n_in % be == 0, BB_ERR_SHAPE, "n_in (" + std::to_string(n_in) + ") not a multiple of block (" + std::to_string(be) + ")");
+  row_bytes = (n_in / be) * bb_;
+  need(byte_off + row_bytes * n_out <= w->nbytes, BB_ERR_SHAPE, "weight slice exceeds the tensor");
+  if (dtype == BB_Q4_K) need(byte_off % 16 == 0, BB_ERR_ARG, "Q4_K slices must start 16-byte aligned");
+  if (dtype == BB_Q6_K) need(byte_off % 2 == 0, BB_ERR_ARG, "Q6_K slices must start 2-byte aligned");
+  if (dtype == BB_F32) need(byte_off % 4 == 0, BB_ERR_ARG, "F32 slices must start 4-byte aligned");
+  if (dtype == BB_F16) need(byte_off % 2 == 0, BB_ERR_ARG, "F16 slices must start 2-byte aligned");
+}
+
+// matvec / matmul on device pointers.
+void matmul_dev(bb_ctx* c, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
+                const float* x, size_t nt, float* y) {
+  size_t row_bytes;
+  check_weight_range(w, dtype, byte_off, n_in, n_out, row_bytes);
+  const uint8_t* wp = w->dev + byte_off;
+  if (dtype == BB_Q4_K || dtype == BB_Q6_K) {
+    Carve cv{nullptr};
+    cv.take<int8_t>(nt * n_in);
+    cv.take<float>(nt * n_in / 256);
+    cv.take<int32_t>(nt * n_in / 32);
+    uint8_t* base = ensure_ws(c, cv.off);
+    Carve cv2{base};
+    bb::Q8Bufs q{cv2.take<int8_t>(nt * n_in), cv2.take<float>(nt * n_in / 256), cv2.take<int32_t>(nt * n_in / 32)};
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, nt, n_in, q); });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)dtype, wp, row_bytes, (int)(n_in / 256), n_out, q, n_in, nt, y, n_out,
+                                nt == 1);
+    });
+  } else {
+    launch(c, bb::K_ROWS_F32, [&] { return bb::launch_rows_f32(c->stream, (int)dtype, wp, n_in, n_out, x, nt, y); });
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bb_last_error(void) { return g_err.c_str(); }
+const char* bb_version(void) { return "bebelm_moe 0.1.0 (gfx950)"; }
+
+int bb_ctx_create(int device, bb_ctx** out) {
+  return guard([&] {
+    need(out != nullptr, BB_ERR_ARG, "out is null");
+    int n = 0;
+    check_hip(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    need(device >= 0 && device < n, BB_ERR_ARG, "no such device " + std::to_string(device));
+    auto* c = new bb_ctx();
+    c->device = device;
+    try {
+      set_device(c);
+      check_hip(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking), "hipStreamCreate");
+      c->stream = c->own;
+      c->counters = static_cast<uint32_t*>(dev_alloc(N_CTR * sizeof(uint32_t)));
+      check_hip(hipMemset(c->counters, 0, N_CTR * sizeof(uint32_t)), "hipMemset");
+      check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    } catch (...) {
+      if (c->own) (void)hipStreamDestroy(c->own);
+      if (c->counters) (void)hipFree(c->counters);
+      delete c;
+      throw;
+    }
+    *out = c;
+  });
+}
+
+int bb_ctx_destroy(bb_ctx* c) {
+  return guard([&] {
+    if (!c) return;
+    set_device(c);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto& p : c->pending) {
+      (void)hipEventDestroy(p.a);
+      (void)hipEventDestroy(p.b);
+    }
+    for (auto e : c->event_pool) (void)hipEventDestroy(e);
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->io) (void)hipFree(c->io);
+    if (c->counters) (void)hipFree(c->counters);
+    if (c->own) (void)hipStreamDestroy(c->own);
+    delete c;
+  });
+}
+
+int bb_ctx_set_stream(bb_ctx* c, void* s) {
+  return guard([&] {
+    need_ctx(c);
+    c->stream = s ? static_cast<hipStream_t>(s) : c->own;
+  });
+}
+
+int bb_ctx_get_stream(bb_ctx* c, void** s) {
+  return guard([&] {
+    need_ctx(c);
+    need(s != nullptr, BB_ERR_ARG, "out is null");
+    *s = c->stream;
+  });
+}
+
+int bb_ctx_synchronize(bb_ctx* c) {
+  return guard([&] {
+    need_ctx(c);
+    set_device(c);
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int bb_ctx_profile(bb_ctx* c, int enable) {
+  return guard([&] {
+    need_ctx(c);
+    collect(c);
+    c->profile = enable != 0;
+  });
+}
+
+int bb_kernel_count(void) { return bb::K_COUNT; }
+
+int bb_ctx_kernel_stats(bb_ctx* c, int idx, const char** name, double* total_ms, int64_t* launches) {
+  return guard([&] {
+    need_ctx(c);
+    need(idx >= 0 && idx < bb::K_COUNT, BB_ERR_ARG, "kernel index out of range");
+    collect(c);
+    if (name) *name = bb::kernel_name(idx);
+    if (total_ms) *total_ms = c->kernel_ms[idx];
+    if (launches) *launches = c->launches[idx];
+  });
+}
+
+int bb_ctx_reset_stats(bb_ctx* c) {
+  return guard([&] {
+    need_ctx(c);
+    collect(c);
+    for (int i = 0; i < bb::K_COUNT; ++i) {
+      c->kernel_ms[i] = 0;
+      c->launches[i] = 0;
+    }
+  });
+}
+
+int bb_tensor_upload(bb_ctx* c, uint32_t dtype, const void* bytes, size_t nbytes, const uint64_t* dims, int ndims,
+                     bb_tensor** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(out != nullptr && bytes != nullptr && dims != nullptr, BB_ERR_ARG, "null argument");
+    need(ndims >= 1 && ndims <= 4, BB_ERR_ARG, "ndims must be 1..4");
+    size_t be, bb_;
+    need(block_of(dtype, be, bb_), BB_ERR_DTYPE, "unsupported dtype " + std::to_string(dtype));
+    size_t n = 1;
+    for (int i = 0; i < ndims; ++i) n *= dims[i];
+    need(n % be == 0, BB_ERR_SHAPE, "element count is not a whole number of blocks");
+    need((n / be) * bb_ == nbytes, BB_ERR_SHAPE,
+         "nbytes " + std::to_string(nbytes) + " != byte_size " + std::to_string((n / be) * bb_));
+    set_device(c);
+    auto* t = new bb_tensor();
+    t->ctx = c;
+    t->dtype = dtype;
+    t->ndims = ndims;
+    for (int i = 0; i < 4; ++i) t->dims[i] = i < ndims ? dims[i] : 1;
+    t->nbytes = nbytes;
+    try {
+      t->dev = static_cast<uint8_t*>(dev_alloc(nbytes));
+      check_hip(hipMemcpy(t->dev, bytes, nbytes, hipMemcpyHostToDevice), "upload");
+      check_hip(hipMemset(t->dev + nbytes, 0, round_up(nbytes, 256) + PAD - nbytes), "pad clear");
+    } catch (...) {
+      if (t->dev) (void)hipFree(t->dev);
+      delete t;
+      throw;
+    }
+    *out = t;
+  });
+}
+
+int bb_tensor_free(bb_tensor* t) {
+  return guard([&] {
+    if (!t) return;
+    set_device(t->ctx);
+    (void)hipStreamSynchronize(t->ctx->stream);
+    (void)hipFree(t->dev);
+    delete t;
+  });
+}
+
+int bb_tensor_device_ptr(const bb_tensor* t, void** dev) {
+  return guard([&] {
+    need(t != nullptr && dev != nullptr, BB_ERR_ARG, "null argument");
+    *dev = t->dev;
+  });
+}
+
+int bb_quantize_q8(bb_ctx* c, const float* x, size_t n, int8_t* q, float* scales, int32_t* sums, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(n % 256 == 0, BB_ERR_SHAPE, "quantize_q8: n must be a multiple of 256");
+    set_device(c);
+    with_io(c, loc, {{x, n * 4, true, false}, {q, n, false, true}, {scales, n / 256 * 4, false, true}, {sums, n / 32 * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              bb::Q8Bufs qb{static_cast<int8_t*>(d[1]), static_cast<float*>(d[2]), static_cast<int32_t*>(d[3])};
+              launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, static_cast<const float*>(d[0]), 1, n, qb); });
+            });
+  });
+}
+
+int bb_matvec(bb_ctx* c, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
+              const float* x, float* y, int loc) {
+  return bb_matmul(c, dtype, w, byte_off, n_in, n_out, x, 1, y, loc);
+}
+
+int bb_matmul(bb_ctx* c, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
+              const float* x, size_t n_tokens, float* y, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(n_tokens >= 1, BB_ERR_ARG, "n_tokens must be >= 1");
+    size_t rb;
+    check_weight_range(w, dtype, byte_off, n_in, n_out, rb);
+    set_device(c);
+    with_io(c, loc, {{x, n_in * n_tokens * 4, true, false}, {y, n_out * n_tokens * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              matmul_dev(c, dtype, w, byte_off, n_in, n_out, static_cast<const float*>(d[0]), n_tokens,
+                         static_cast<float*>(d[1]));
+            });
+  });
+}
+
+int bb_matvec_fused_batch(bb_ctx* c, const bb_fused_job* jobs, size_t n_jobs, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(jobs != nullptr || n_jobs == 0, BB_ERR_ARG, "jobs is null");
+    size_t total = 0;
+    std::vector<size_t> rbytes(n_jobs);
+    for (size_t j = 0; j < n_jobs; ++j) {
+      need(jobs[j].dtype == BB_Q4_K || jobs[j].dtype == BB_Q6_K, BB_ERR_DTYPE,
+           "matvec_fused_batch: only pre-quantised Q4_K/Q6_K jobs are supported");
+      check_weight_range(jobs[j].w, jobs[j].dtype, jobs[j].byte_off, jobs[j].n_in, jobs[j].n_out, rbytes[j]);
+      total += jobs[j].n_out;
+    }
+    set_device(c);
+    std::vector<Io> ios;
+    for (size_t j = 0; j < n_jobs; ++j) {
+      ios.push_back({jobs[j].qx_q, jobs[j].n_in, true, false});
+      ios.push_back({jobs[j].qx_scales, jobs[j].n_in / 256 * 4, true, false});
+      ios.push_back({jobs[j].qx_sums, jobs[j].n_in / 32 * 4, true, false});
+    }
+    ios.push_back({out, total * 4, false, true});
+    with_io(c, loc, ios, [&](std::vector<void*>& d) {
+      float* o = static_cast<float*>(d.back());
+      size_t start = 0;
+      for (size_t j = 0; j < n_jobs; ++j) {
+        bb::Q8Bufs q{static_cast<int8_t*>(d[3 * j]), static_cast<float*>(d[3 * j + 1]), static_cast<int32_t*>(d[3 * j + 2])};
+        const bb_fused_job& jb = jobs[j];
+        launch(c, bb::K_ROWS_Q8, [&] {
+          return bb::launch_rows_q8(c->stream, (int)jb.dtype, jb.w->dev + jb.byte_off, rbytes[j], (int)(jb.n_in / 256),
+                                    jb.n_out, q, jb.n_in, 1, o + start, jb.n_out, 1);
+        });
+        start += jb.n_out;
+      }
+    });
+  });
+}
+
+static int elementwise(bb_ctx* c, int op, float* out, const float* a, const float* b, float s, size_t n, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    set_device(c);
+    std::vector<Io> ios{{out, n * 4, op != bb::EW_SWIGLU, true}, {a, n * 4, true, false}};
+    if (op == bb::EW_SWIGLU) ios.push_back({b, n * 4, true, false});
+    with_io(c, loc, ios, [&](std::vector<void*>& d) {
+      launch(c, bb::K_ELEMWISE, [&] {
+        return bb::launch_elementwise(c->stream, op, static_cast<float*>(d[0]), static_cast<const float*>(d[1]),
+                                      op == bb::EW_SWIGLU ? static_cast<const float*>(d[2]) : nullptr, s, n);
+      });
+    });
+  });
+}
+
+int bb_swiglu(bb_ctx* c, const float* gate, const float* up, float* out, size_t n, int loc) {
+  return elementwise(c, bb::EW_SWIGLU, out, gate, up, 0.f, n, loc);
+}
+int bb_sigmoid_slice(bb_ctx* c, float* x, size_t n, int loc) { return elementwise(c, bb::EW_SIGMOID, x, x, nullptr, 0.f, n, loc); }
+int bb_add_scaled(bb_ctx* c, float* out, const float* b, float s, size_t n, int loc) {
+  return elementwise(c, bb::EW_ADD_SCALED, out, b, nullptr, s, n, loc);
+}
+int bb_add_assign(bb_ctx* c, float* a, const float* b, size_t n, int loc) {
+  return elementwise(c, bb::EW_ADD_ASSIGN, a, b, nullptr, 0.f, n, loc);
+}
+
+int bb_rmsnorm(bb_ctx* c, const float* x, const float* gain, float eps, size_t n, size_t n_vec, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    set_device(c);
+    with_io(c, loc, {{x, n * n_vec * 4, true, false}, {gain, n * 4, true, false}, {out, n * n_vec * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              launch(c, bb::K_RMSNORM, [&] {
+                return bb::launch_rmsnorm(c->stream, static_cast<const float*>(d[0]), static_cast<const float*>(d[1]), eps,
+                                          n, n_vec, static_cast<float*>(d[2]));
+              });
+            });
+  });
+}
+
+int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const bb_tensor* gate, const bb_tensor* up,
+                  const bb_tensor* down, int n_used, bb_moe** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(router && bias && gate && up && down && out, BB_ERR_ARG, "null argument");
+    need(router->dtype == BB_F32, BB_ERR_DTYPE, "router (ffn_gate_inp) must be F32");
+    need(router->ndims == 2, BB_ERR_SHAPE, "router must be [hidden, E]");
+    const uint64_t H = router->dims[0], E = router->dims[1];
+    need(gate->ndims == 3 && up->ndims == 3 && down->ndims == 3, BB_ERR_SHAPE, "expert tensors must be 3-D");
+    const uint64_t F = gate->dims[1];
+    need(gate->dims[0] == H && gate->dims[2] == E, BB_ERR_SHAPE, "gate_exps must be [hidden, ff, E]");
+    need(up->dims[0] == H && up->dims[1] == F && up->dims[2] == E, BB_ERR_SHAPE, "up_exps must be [hidden, ff, E]");
+    need(down->dims[0] == F && down->dims[1] == H && down->dims[2] == E, BB_ERR_SHAPE, "down_exps must be [ff, hidden, E]");
+    for (const bb_tensor* t : {gate, up, down})
+      need(t->dtype == BB_Q4_K || t->dtype == BB_Q6_K, BB_ERR_DTYPE, "expert tensors must be Q4_K or Q6_K");
+    need(gate->dtype == up->dtype, BB_ERR_DTYPE, "gate_exps and up_exps must share a dtype");
+    need(E >= 1 && E <= 32, BB_ERR_RANGE, "this build supports up to 32 experts");
+    need(n_used >= 1 && n_used <= 8 && (uint64_t)n_used <= E, BB_ERR_RANGE, "n_used must be 1..min(8, E)");
+    need(H % 256 == 0 && F % 256 == 0 && H >= 256 && F >= 256, BB_ERR_SHAPE, "hidden and ff must be multiples of 256");
+    need(H <= 32768 && F <= 32768, BB_ERR_RANGE, "hidden/ff above 32768 are not supported");
+    need(E * (F / 256) <= DOWN_CTR - GATEUP_CTR && H / 32 <= N_CTR - DOWN_CTR, BB_ERR_RANGE, "counter space exceeded");
+    set_device(c);
+    auto* m = new bb_moe();
+    m->ctx = c;
+    m->router = router;
+    m->gate = gate;
+    m->up = up;
+    m->down = down;
+    m->H = (int)H;
+    m->F = (int)F;
+    m->E = (int)E;
+    m->K = n_used;
+    size_t be, bgate, bup, bdown;
+    block_of(gate->dtype, be, bgate);
+    block_of(up->dtype, be, bup);
+    block_of(down->dtype, be, bdown);
+    m->stride_g = F * (H / 256) * bgate;  // model.rs:612-615
+    m->stride_u = F * (H / 256) * bup;
+    m->stride_d = H * (F / 256) * bdown;
+    try {
+      m->bias_dev = static_cast<float*>(dev_alloc(E * 4));
+      check_hip(hipMemcpy(m->bias_dev, bias, E * 4, hipMemcpyHostToDevice), "bias upload");
+    } catch (...) {
+      delete m;
+      throw;
+    }
+    *out = m;
+  });
+}
+
+int bb_moe_destroy(bb_moe* m) {
+  return guard([&] {
+    if (!m) return;
+    set_device(m->ctx);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    (void)hipFree(m->bias_dev);
+    delete m;
+  });
+}
+
+int bb_moe_forward(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, int loc, bb_route_trace* tr) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr, BB_ERR_ARG, "null layer");
+    need(m->ctx == c, BB_ERR_ARG, "layer belongs to another context");
+    need_loc(loc);
+    need(T >= 1, BB_ERR_ARG, "T must be >= 1");
+    set_device(c);
+    with_io(c, loc, {{x, T * m->H * 4, true, false}, {out, T * m->H * 4, false, true}}, [&](std::vector<void*>& d) {
+      moe_forward_dev(c, m, static_cast<const float*>(d[0]), T, static_cast<float*>(d[1]), tr);
+    });
+  });
+}
+
+int bb_dense_create(bb_ctx* c, const bb_tensor* gate, const bb_tensor* up, const bb_tensor* down, bb_dense** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(gate && up && down && out, BB_ERR_ARG, "null argument");
+    need(gate->ndims == 2 && up->ndims == 2 && down->ndims == 2, BB_ERR_SHAPE, "dense weights must be 2-D");
+    const uint64_t H = gate->dims[0], F = gate->dims[1];
+    need(up->dims[0] == H && up->dims[1] == F, BB_ERR_SHAPE, "ffn_up must be [hidden, ff]");
+    need(down->dims[0] == F && down->dims[1] == H, BB_ERR_SHAPE, "ffn_down must be [ff, hidden]");
+    for (const bb_tensor* t : {gate, up, down})
+      need(t->dtype == BB_Q4_K || t->dtype == BB_Q6_K, BB_ERR_DTYPE, "dense weights must be Q4_K or Q6_K");
+    need(H % 256 == 0 && F % 256 == 0, BB_ERR_SHAPE, "hidden and ff must be multiples of 256");
+    auto* d = new bb_dense();
+    d->ctx = c;
+    d->gate = gate;
+    d->up = up;
+    d->down = down;
+    d->H = (int)H;
+    d->F = (int)F;
+    *out = d;
+  });
+}
+
+int bb_dense_destroy(bb_dense* d) {
+  return guard([&] { delete d; });
+}
+
+int bb_dense_forward(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(d != nullptr && d->ctx == c, BB_ERR_ARG, "bad dense layer");
+    need_loc(loc);
+    need(T >= 1, BB_ERR_ARG, "T must be >= 1");
+    set_device(c);
+    with_io(c, loc, {{x, T * d->H * 4, true, false}, {out, T * d->H * 4, false, true}}, [&](std::vector<void*>& dv) {
+      dense_forward_dev(c, d, static_cast<const float*>(dv[0]), T, static_cast<float*>(dv[1]));
+    });
+  });
+}
+
+int bb_stack_create(bb_ctx* c, const bb_layer_desc* layers, size_t n_layers, float eps, bb_stack** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(layers && out && n_layers > 0, BB_ERR_ARG, "null argument");
+    int H = -1;
+    for (size_t i = 0; i < n_layers; ++i) {
+      need((layers[i].moe != nullptr) != (layers[i].dense != nullptr), BB_ERR_ARG, "exactly one of moe/dense per layer");
+      need(layers[i].ffn_norm != nullptr, BB_ERR_ARG, "ffn_norm is null");
+      const int h = layers[i].moe ? layers[i].moe->H : layers[i].dense->H;
+      need(H < 0 || h == H, BB_ERR_SHAPE, "layers disagree on hidden size");
+      H = h;
+    }
+    set_device(c);
+    auto* s = new bb_stack();
+    s->ctx = c;
+    s->eps = eps;
+    s->H = H;
+    try {
+      for (size_t i = 0; i < n_layers; ++i) {
+        bb_layer_desc L = layers[i];
+        float* g = static_cast<float*>(dev_alloc((size_t)H * 4));
+        s->gains.push_back(g);
+        check_hip(hipMemcpy(g, layers[i].ffn_norm, (size_t)H * 4, hipMemcpyHostToDevice), "gain upload");
+        L.ffn_norm = g;
+        s->layers.push_back(L);
+      }
+    } catch (...) {
+      for (float* g : s->gains) (void)hipFree(g);
+      delete s;
+      throw;
+    }
+    *out = s;
+  });
+}
+
+int bb_stack_destroy(bb_stack* s) {
+  return guard([&] {
+    if (!s) return;
+    set_device(s->ctx);
+    (void)hipStreamSynchronize(s->ctx->stream);
+    for (float* g : s->gains) (void)hipFree(g);
+    if (s->h) (void)hipFree(s->h);
+    if (s->normed) (void)hipFree(s->normed);
+    if (s->ffn) (void)hipFree(s->ffn);
+    delete s;
+  });
+}
+
+int bb_stack_forward(bb_ctx* c, bb_stack* s, const float* x, size_t T, float* h_out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(s != nullptr && s->ctx == c, BB_ERR_ARG, "bad stack");
+    need_loc(loc);
+    need(T >= 1, BB_ERR_ARG, "T must be >= 1");
+    set_device(c);
+    const size_t H = s->H;
+    if (T > s->cap_T) {
+      check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+      for (float** p : {&s->h, &s->normed, &s->ffn}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+      }
+      s->cap_T = 0;
+      s->h = static_cast<float*>(dev_alloc(T * H * 4));
+      s->normed = static_cast<float*>(dev_alloc(T * H * 4));
+      s->ffn = static_cast<float*>(dev_alloc(T * H * 4));
+      s->cap_T = T;
+    }
+    with_io(c, loc, {{x, T * H * 4, true, false}, {h_out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
+      check_hip(hipMemcpyAsync(s->h, d[0], T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+      for (const bb_layer_desc& L : s->layers) {
+        launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, s->h, L.ffn_norm, s->eps, H, T, s->normed); });
+        if (L.moe) moe_forward_dev(c, L.moe, s->normed, T, s->ffn, nullptr);
+        else dense_forward_dev(c, L.dense, s->normed, T, s->ffn);
+        launch(c, bb::K_ELEMWISE, [&] { return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, s->h, s->ffn, nullptr, 0.f, T * H); });
+      }
+      check_hip(hipMemcpyAsync(d[1], s->h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+    });
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// bb_internal.h — launcher declarations shared by the kernels TU and the C-ABI TU.
+#ifndef BB_INTERNAL_H
+#define BB_INTERNAL_H
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace bb {
+
+// Device-side routing state for one forward call. All arrays live in the context workspace.
+struct RouteBufs {
+  float* logits;      // [T*E]
+  int32_t* sel;       // [T*K]
+  float* wts;         // [T*K]
+  int32_t* counts;    // [E]
+  int32_t* offsets;   // [E+1]
+  int32_t* perm;      // [T*K]  group position -> entry t*K+k
+  int32_t* hit;       // [E+1]  hit[0] = number of experts with members, hit[1..] ascending ids
+  int32_t* ties;      // [1]
+  float* margin;      // [T]
+  uint32_t* counter;  // grid-completion counter (self-resetting)
+};
+
+struct Q8Bufs {
+  int8_t* q;
+  float* scales;
+  int32_t* sums;
+};
+
+// One launch = one kernel; names are used for the per-kernel profile table.
+enum KernelId : int {
+  K_ROUTE = 0,
+  K_GATEUP,
+  K_DOWN,
+  K_QUANT,
+  K_ROWS_Q8,
+  K_ROWS_F32,
+  K_ELEMWISE,
+  K_RMSNORM,
+  K_ROUTE_LARGE,
+  K_DISPATCH,
+  K_GEMM_GATEUP,
+  K_GEMM_DOWN,
+  K_COMBINE,
+  K_COUNT
+};
+const char* kernel_name(int id);
+
+hipError_t launch_route_small(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H,
+                              int E, int K, Q8Bufs xq, RouteBufs rb);
+
+hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t stride_g,
+                         size_t stride_u, int H, int F, int K, int max_hit, int batch_mode, const RouteBufs& rb,
+                         Q8Bufs xq, float* act, Q8Bufs actq, uint32_t* counters);
+
+hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int H, int F, int K, int T,
+                       int max_hit, int batch_mode, const RouteBufs& rb, Q8Bufs actq, float* slots, float* out,
+                       uint32_t* counters);
+
+hipError_t launch_quantize(hipStream_t s, const float* x, size_t n_vec, size_t n, Q8Bufs q);
+
+hipError_t launch_rows_q8(hipStream_t s, int dtype, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows,
+                          Q8Bufs q, size_t q_stride, size_t n_tok, float* y, size_t y_tok_stride, int neg_zero_start);
+
+hipError_t launch_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t n_in, size_t n_rows, const float* x,
+                           size_t n_tok, float* y);
+
+enum ElemOp : int { EW_SWIGLU = 0, EW_SIGMOID, EW_ADD_SCALED, EW_ADD_ASSIGN };
+hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a, const float* b, float scalar,
+                              size_t n);
+
+hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
+                          float* out);
+
+}  // namespace bb
+#endif

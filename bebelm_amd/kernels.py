@@ -1,0 +1,101 @@
+"""Kernel-level mirror of the reference's src/kernels API over the C ABI.
+
+  quantize_q8(x) -> Q8Vec                  kernels/matmul.rs:141
+  matvec(dtype, w, n_in, n_out, x, y)      kernels/matmul.rs:850
+  matmul(dtype, w, n_in, n_out, x, t, y)   kernels/matmul.rs:908
+  FusedJob / matvec_fused_batch            kernels/matmul.rs:995-1053
+  swiglu / sigmoid_slice                   kernels/activation.rs:16, :25
+  add_scaled / add_assign                  kernels/elementwise.rs:12, :4
+  rmsnorm                                  kernels/rmsnorm.rs:10
+Each function takes the Context first; `w` is an uploaded Tensor (plus a byte offset where the
+reference passes a sub-slice of the weight bytes).
+"""
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import check, lib
+from .model import _ptr, _same_loc
+
+
+@dataclass
+class Q8Vec:
+    q: object       # int8 [n]
+    scales: object  # f32 [n/256]
+    sums: object    # i32 [n/32]
+
+
+def quantize_q8(ctx, x, out=None):
+    n = x.shape[-1] if hasattr(x, "shape") else len(x)
+    if out is None:
+        out = Q8Vec(np.empty(n, np.int8), np.empty(n // 256, np.float32), np.empty(n // 32, np.int32))
+    loc = _same_loc(x, out.q, out.scales, out.sums)
+    check(lib().bb_quantize_q8(ctx.handle, _ptr(x)[0], n, _ptr(out.q)[0], _ptr(out.scales)[0], _ptr(out.sums)[0], loc))
+    return out
+
+
+def matvec(ctx, dtype, w, n_in, n_out, x, y, byte_off=0):
+    loc = _same_loc(x, y)
+    check(lib().bb_matvec(ctx.handle, dtype, w.handle, byte_off, n_in, n_out, _ptr(x)[0], _ptr(y)[0], loc))
+    return y
+
+
+def matmul(ctx, dtype, w, n_in, n_out, x, n_tokens, y, byte_off=0):
+    loc = _same_loc(x, y)
+    check(lib().bb_matmul(ctx.handle, dtype, w.handle, byte_off, n_in, n_out, _ptr(x)[0], n_tokens, _ptr(y)[0], loc))
+    return y
+
+
+@dataclass
+class FusedJob:
+    dtype: int
+    w: object
+    n_in: int
+    n_out: int
+    qx: Q8Vec
+    byte_off: int = 0
+
+
+def matvec_fused_batch(ctx, jobs, out):
+    arr = (_lib.FusedJob * len(jobs))()
+    arrays = [out]
+    for i, j in enumerate(jobs):
+        arr[i] = _lib.FusedJob(j.dtype, j.w.handle, j.byte_off, j.n_in, j.n_out, _ptr(j.qx.q)[0],
+                               _ptr(j.qx.scales)[0], _ptr(j.qx.sums)[0])
+        arrays += [j.qx.q, j.qx.scales, j.qx.sums]
+    loc = _same_loc(*arrays)
+    check(lib().bb_matvec_fused_batch(ctx.handle, arr, len(jobs), _ptr(out)[0], loc))
+    return out
+
+
+def swiglu(ctx, gate, up, out):
+    check(lib().bb_swiglu(ctx.handle, _ptr(gate)[0], _ptr(up)[0], _ptr(out)[0], _n(out), _same_loc(gate, up, out)))
+    return out
+
+
+def sigmoid_slice(ctx, x):
+    check(lib().bb_sigmoid_slice(ctx.handle, _ptr(x)[0], _n(x), _same_loc(x)))
+    return x
+
+
+def add_scaled(ctx, out, b, s):
+    check(lib().bb_add_scaled(ctx.handle, _ptr(out)[0], _ptr(b)[0], ctypes.c_float(s), _n(out), _same_loc(out, b)))
+    return out
+
+
+def add_assign(ctx, a, b):
+    check(lib().bb_add_assign(ctx.handle, _ptr(a)[0], _ptr(b)[0], _n(a), _same_loc(a, b)))
+    return a
+
+
+def rmsnorm(ctx, x, gain, eps, out, n_vec=1):
+    n = _n(gain)
+    check(lib().bb_rmsnorm(ctx.handle, _ptr(x)[0], _ptr(gain)[0], ctypes.c_float(eps), n, n_vec, _ptr(out)[0],
+                           _same_loc(x, gain, out)))
+    return out
+
+
+def _n(a):
+    return a.numel() if hasattr(a, "numel") else a.size

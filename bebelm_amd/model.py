@@ -1,0 +1,242 @@
+"""Host-side mirror of the reference's MoE FFN interface over the C ABI.
+
+Names follow the reference so call sites read alike:
+  Model::moe_ffn / moe_ffn_batch (model.rs:473, :286)  -> MoeLayer.moe_ffn / moe_ffn_batch
+  Model::dense_ffn (model.rs:459)                       -> DenseLayer.dense_ffn
+  run_layers' FFN path (model.rs:105-130)               -> FfnStack.run_layers
+Arrays are numpy (host memory, BB_LOC_HOST) or torch CUDA tensors (device memory,
+BB_LOC_DEVICE). Everything runs on the GPU through libbebelm_moe.so; there is no other path.
+"""
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import LOC_DEVICE, LOC_HOST, check, lib
+
+
+def _ptr(a):
+    """(pointer, loc) for a numpy array or a torch tensor."""
+    if a is None:
+        return None, LOC_HOST
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("arrays must be C-contiguous")
+        return a.ctypes.data, LOC_HOST
+    if hasattr(a, "data_ptr"):
+        if not a.is_contiguous():
+            raise ValueError("tensors must be contiguous")
+        return a.data_ptr(), (LOC_DEVICE if a.is_cuda else LOC_HOST)
+    raise TypeError(f"unsupported array type {type(a)}")
+
+
+def _same_loc(*arrays):
+    locs = {_ptr(a)[1] for a in arrays if a is not None}
+    if len(locs) != 1:
+        raise ValueError("all arrays of one call must be host or all device")
+    return locs.pop()
+
+
+class Context:
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        check(lib().bb_ctx_create(device, ctypes.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_ctx_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        check(lib().bb_ctx_synchronize(self.handle))
+
+    def set_stream(self, stream_ptr):
+        check(lib().bb_ctx_set_stream(self.handle, stream_ptr))
+
+    def stream(self):
+        s = ctypes.c_void_p()
+        check(lib().bb_ctx_get_stream(self.handle, ctypes.byref(s)))
+        return s.value
+
+    def profile(self, enable=True):
+        check(lib().bb_ctx_profile(self.handle, 1 if enable else 0))
+
+    def reset_stats(self):
+        check(lib().bb_ctx_reset_stats(self.handle))
+
+    def kernel_stats(self):
+        """{kernel name: (total ms, launches)} for kernels launched while profiling."""
+        out = {}
+        for i in range(lib().bb_kernel_count()):
+            name = ctypes.c_char_p()
+            ms = ctypes.c_double()
+            n = ctypes.c_int64()
+            check(lib().bb_ctx_kernel_stats(self.handle, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)))
+            if n.value:
+                out[name.value.decode()] = (ms.value, n.value)
+        return out
+
+
+class Tensor:
+    """A weight tensor uploaded once to HBM in its native GGUF block layout."""
+
+    def __init__(self, ctx, dtype, data, dims):
+        data = np.ascontiguousarray(data)
+        raw = data.view(np.uint8).reshape(-1)
+        d = (ctypes.c_uint64 * len(dims))(*dims)
+        h = ctypes.c_void_p()
+        check(lib().bb_tensor_upload(ctx.handle, dtype, raw.ctypes.data, raw.nbytes, d, len(dims), ctypes.byref(h)))
+        self.handle = h
+        self.ctx = ctx
+        self.dtype = dtype
+        self.dims = tuple(dims)
+        self.nbytes = raw.nbytes
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_tensor_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class RouteTrace:
+    """Host copies of one call's routing state (bb_route_trace)."""
+
+    def __init__(self, t, n_experts, k):
+        self.logits = np.zeros(t * n_experts, np.float32)
+        self.sel = np.zeros(t * k, np.int32)
+        self.w = np.zeros(t * k, np.float32)
+        self.counts = np.zeros(n_experts, np.int32)
+        self.offsets = np.zeros(n_experts + 1, np.int32)
+        self.perm = np.zeros(t * k, np.int32)
+        self.ties = np.zeros(1, np.int32)
+        self.margin = np.zeros(t, np.float32)
+
+    def as_struct(self):
+        return _lib.RouteTrace(*(a.ctypes.data for a in (self.logits, self.sel, self.w, self.counts, self.offsets,
+                                                         self.perm, self.ties, self.margin)))
+
+
+class MoeLayer:
+    """One sparse-MoE FFN layer (router, exp_probs_b, stacked gate/up/down experts)."""
+
+    def __init__(self, ctx, weights, n_used=None):
+        w = weights
+        self.ctx = ctx
+        self.hidden, self.moe_ff, self.n_experts = w.hidden, w.moe_ff, w.n_experts
+        self.n_used = n_used or w.n_used
+        E, H, F = w.n_experts, w.hidden, w.moe_ff
+        self.router = Tensor(ctx, 0, w.router, (H, E))
+        self.gate = Tensor(ctx, w.gate_dtype, w.gate_exps, (H, F, E))
+        self.up = Tensor(ctx, w.up_dtype, w.up_exps, (H, F, E))
+        self.down = Tensor(ctx, w.down_dtype, w.down_exps, (F, H, E))
+        bias = np.ascontiguousarray(w.exp_probs_b, np.float32)
+        h = ctypes.c_void_p()
+        check(lib().bb_moe_create(ctx.handle, self.router.handle, bias.ctypes.data, self.gate.handle, self.up.handle,
+                                  self.down.handle, self.n_used, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_moe_destroy(self.handle))
+            self.handle = None
+        for t in (self.router, self.gate, self.up, self.down):
+            t.close()
+
+    def forward(self, x, t, out, trace=None):
+        """x, out: token-major [t, hidden]; numpy (host) or torch CUDA (device, async)."""
+        loc = _same_loc(x, out)
+        tr = trace.as_struct() if trace is not None else None
+        check(lib().bb_moe_forward(self.ctx.handle, self.handle, _ptr(x)[0], t, _ptr(out)[0], loc,
+                                   ctypes.byref(tr) if tr is not None else None))
+        return out
+
+    def moe_ffn(self, x, trace=None):
+        """Model::moe_ffn (model.rs:473-555): one token, host arrays."""
+        x = np.ascontiguousarray(x, np.float32).reshape(self.hidden)
+        out = np.empty(self.hidden, np.float32)
+        return self.forward(x, 1, out, trace)
+
+    def moe_ffn_batch(self, x, t, trace=None):
+        """Model::moe_ffn_batch (model.rs:286-371): t tokens, token-major host arrays."""
+        x = np.ascontiguousarray(x, np.float32).reshape(t * self.hidden)
+        out = np.empty(t * self.hidden, np.float32)
+        return self.forward(x, t, out, trace)
+
+
+class DenseLayer:
+    def __init__(self, ctx, weights):
+        w = weights
+        self.ctx = ctx
+        self.hidden, self.ff = w.hidden, w.ff
+        self.gate = Tensor(ctx, w.gate_dtype, w.gate, (w.hidden, w.ff))
+        self.up = Tensor(ctx, w.up_dtype, w.up, (w.hidden, w.ff))
+        self.down = Tensor(ctx, w.down_dtype, w.down, (w.ff, w.hidden))
+        h = ctypes.c_void_p()
+        check(lib().bb_dense_create(ctx.handle, self.gate.handle, self.up.handle, self.down.handle, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_dense_destroy(self.handle))
+            self.handle = None
+        for t in (self.gate, self.up, self.down):
+            t.close()
+
+    def forward(self, x, t, out):
+        loc = _same_loc(x, out)
+        check(lib().bb_dense_forward(self.ctx.handle, self.handle, _ptr(x)[0], t, _ptr(out)[0], loc))
+        return out
+
+    def dense_ffn(self, x):
+        """Model::dense_ffn (model.rs:459-469)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(self.hidden)
+        out = np.empty(self.hidden, np.float32)
+        return self.forward(x, 1, out)
+
+
+class FfnStack:
+    """run_layers' FFN path with the operator sub-layer contributing nothing (model.rs:105-130)."""
+
+    def __init__(self, ctx, layers, eps=1e-5):
+        """layers: list of (ffn_norm gain f32[hidden], MoeLayer | DenseLayer)."""
+        self.ctx = ctx
+        self.layers = layers
+        self.hidden = layers[0][1].hidden
+        self._gains = [np.ascontiguousarray(g, np.float32) for g, _ in layers]
+        descs = (_lib.LayerDesc * len(layers))()
+        for i, ((_, layer), g) in enumerate(zip(layers, self._gains)):
+            descs[i].ffn_norm = g.ctypes.data
+            descs[i].moe = layer.handle if isinstance(layer, MoeLayer) else None
+            descs[i].dense = layer.handle if isinstance(layer, DenseLayer) else None
+        h = ctypes.c_void_p()
+        check(lib().bb_stack_create(ctx.handle, descs, len(layers), eps, ctypes.byref(h)))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_stack_destroy(self.handle))
+            self.handle = None
+
+    def forward(self, x, t, out):
+        loc = _same_loc(x, out)
+        check(lib().bb_stack_forward(self.ctx.handle, self.handle, _ptr(x)[0], t, _ptr(out)[0], loc))
+        return out
+
+    def run_layers(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty_like(x)
+        return self.forward(x, x.size // self.hidden, out)

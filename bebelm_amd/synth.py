@@ -1,0 +1,202 @@
+"""Deterministic synthetic inputs for the MoE FFN benchmark configurations.
+
+Shapes follow the reference's hard-coded LFM2.5-8B-A1B architecture (src/config.rs:14-32):
+hidden 2048, expert FFN 1792, 32 experts, top-4, dense FFN 7168 (layers 0-1). There is no GGUF
+offline, so weights are random blocks in the native GGUF byte layouts:
+
+  Q4_K (144 B): d, dmin = f16(|N(0, 2e-3)|); 6-bit scales and mins ~ U{0..63} packed as
+                get_scale_min_k4 (dequant.rs:64-72) unpacks them; qs bytes ~ U{0..255}.
+  Q6_K (210 B): ql, qh bytes ~ U{0..255}; i8 scales ~ U{-64..63}; d = f16(|N(0, 2e-3)|).
+  Router (ffn_gate_inp): f32 ~ N(0, 0.02). Hidden states: f32 ~ N(0, 1).
+
+Every tensor draws from its own PCG64 stream keyed by (config seed, tensor id), so any tensor
+can be regenerated alone. Gating follows the reference (sigmoid + selection-only bias,
+model.rs:485-495); the skewed config puts a Zipf(1.2) ranking into that bias (exp_probs_b).
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+
+F32, F16, Q4_K, Q6_K = 0, 1, 12, 14
+BLOCK = {F32: (1, 4), F16: (1, 2), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+HIDDEN = 2048
+MOE_FF = 1792
+DENSE_FF = 7168
+N_EXPERTS = 32
+N_USED = 4
+N_LAYERS = 24
+N_DENSE = 2
+RMS_EPS = 1e-5
+
+
+def rng(seed, *stream):
+    return np.random.Generator(np.random.PCG64([int(seed), *[int(s) for s in stream]]))
+
+
+def byte_size(dtype, n_elements):
+    be, bb = BLOCK[dtype]
+    assert n_elements % be == 0
+    return n_elements // be * bb
+
+
+def _f16_abs_normal(g, n, sigma):
+    return np.abs(g.standard_normal(n) * sigma).astype(np.float16).view(np.uint16)
+
+
+def pack_q4k_scales(sc, m):
+    """Inverse of get_scale_min_k4 (dequant.rs:64-72): (..., 8) 6-bit values -> (..., 12) bytes."""
+    sc = sc.astype(np.uint8)
+    m = m.astype(np.uint8)
+    s = np.zeros(sc.shape[:-1] + (12,), np.uint8)
+    for j in range(4):
+        s[..., j] = sc[..., j] | ((sc[..., j + 4] >> 4) << 6)
+        s[..., j + 4] = m[..., j] | ((m[..., j + 4] >> 4) << 6)
+        s[..., j + 8] = (sc[..., j + 4] & 0xF) | ((m[..., j + 4] & 0xF) << 4)
+    return s
+
+
+def q4k_blocks(g, n_blocks):
+    out = np.empty((n_blocks, 144), np.uint8)
+    d = _f16_abs_normal(g, n_blocks, 2e-3)
+    dmin = _f16_abs_normal(g, n_blocks, 2e-3)
+    out[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+    out[:, 2:4] = dmin.view(np.uint8).reshape(n_blocks, 2)
+    sc = g.integers(0, 64, (n_blocks, 8), dtype=np.uint8)
+    m = g.integers(0, 64, (n_blocks, 8), dtype=np.uint8)
+    out[:, 4:16] = pack_q4k_scales(sc, m)
+    out[:, 16:144] = g.integers(0, 256, (n_blocks, 128), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def q6k_blocks(g, n_blocks):
+    out = np.empty((n_blocks, 210), np.uint8)
+    out[:, 0:192] = g.integers(0, 256, (n_blocks, 192), dtype=np.uint8)
+    out[:, 192:208] = g.integers(-64, 64, (n_blocks, 16), dtype=np.int8).view(np.uint8)
+    d = _f16_abs_normal(g, n_blocks, 2e-3)
+    out[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
+    return out.reshape(-1)
+
+
+def quant_tensor(g, dtype, n_in, n_out, n_mat=1):
+    n_blocks = n_mat * n_out * n_in // 256
+    if dtype == Q4_K:
+        return q4k_blocks(g, n_blocks)
+    if dtype == Q6_K:
+        return q6k_blocks(g, n_blocks)
+    raise ValueError(f"dtype {dtype}")
+
+
+def zipf_bias(seed, n_experts=N_EXPERTS, s=1.2, kappa=0.5):
+    """exp_probs_b[e] = kappa * p_rank(e), p_r ∝ r^-s over a seeded rank permutation."""
+    r = np.arange(1, n_experts + 1, dtype=np.float64)
+    p = r ** -s
+    p /= p.sum()
+    perm = rng(seed, 9001).permutation(n_experts)
+    bias = np.zeros(n_experts, np.float32)
+    bias[perm] = (kappa * p).astype(np.float32)
+    return bias
+
+
+@dataclass
+class MoeWeights:
+    hidden: int
+    moe_ff: int
+    n_experts: int
+    n_used: int
+    router: np.ndarray          # f32 [E, hidden] row-major (GGUF dims [hidden, E])
+    exp_probs_b: np.ndarray     # f32 [E]
+    gate_dtype: int
+    up_dtype: int
+    down_dtype: int
+    gate_exps: np.ndarray       # u8, E experts x ff rows of hidden
+    up_exps: np.ndarray
+    down_exps: np.ndarray       # u8, E experts x hidden rows of ff
+
+    def expert_bytes(self, dtype, n_in, n_out):
+        return byte_size(dtype, n_in * n_out)
+
+    @property
+    def nbytes(self):
+        return self.router.nbytes + self.gate_exps.nbytes + self.up_exps.nbytes + self.down_exps.nbytes
+
+
+@dataclass
+class DenseWeights:
+    hidden: int
+    ff: int
+    gate_dtype: int
+    up_dtype: int
+    down_dtype: int
+    gate: np.ndarray
+    up: np.ndarray
+    down: np.ndarray
+
+    @property
+    def nbytes(self):
+        return self.gate.nbytes + self.up.nbytes + self.down.nbytes
+
+
+def moe_weights(seed, layer=0, hidden=HIDDEN, moe_ff=MOE_FF, n_experts=N_EXPERTS, n_used=N_USED,
+                down_dtype=Q4_K, gate_dtype=Q4_K, bias=None):
+    base = 100 * layer
+    router = (rng(seed, base + 1).standard_normal((n_experts, hidden), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    gate = quant_tensor(rng(seed, base + 2), gate_dtype, hidden, moe_ff, n_experts)
+    up = quant_tensor(rng(seed, base + 3), gate_dtype, hidden, moe_ff, n_experts)
+    down = quant_tensor(rng(seed, base + 4), down_dtype, moe_ff, hidden, n_experts)
+    b = np.zeros(n_experts, np.float32) if bias is None else np.asarray(bias, np.float32)
+    return MoeWeights(hidden, moe_ff, n_experts, n_used, router, b, gate_dtype, gate_dtype, down_dtype, gate, up, down)
+
+
+def dense_weights(seed, layer=0, hidden=HIDDEN, ff=DENSE_FF, dtype=Q4_K):
+    base = 100 * layer
+    gate = quant_tensor(rng(seed, base + 5), dtype, hidden, ff)
+    up = quant_tensor(rng(seed, base + 6), dtype, hidden, ff)
+    down = quant_tensor(rng(seed, base + 7), dtype, ff, hidden)
+    return DenseWeights(hidden, ff, dtype, dtype, dtype, gate, up, down)
+
+
+def hidden_states(seed, t, hidden=HIDDEN, stream=0):
+    return rng(seed, 7000 + stream).standard_normal((t, hidden), dtype=np.float32)
+
+
+@dataclass
+class Config:
+    name: str
+    tokens: int
+    down_dtype: int = Q4_K
+    zipf: bool = False
+    layers: int = 1
+    description: str = ""
+    extra: dict = field(default_factory=dict)
+
+
+CONFIGS = {
+    1: Config("decode_t1", 1, description="decode of 1 token, Q4_K experts, unbiased router"),
+    2: Config("decode_t16", 16, description="decode batch of 16 independent tokens, Q4_K experts"),
+    3: Config("prefill_t512", 512, description="prefill of 512 tokens, Q4_K experts, unbiased router"),
+    4: Config("prefill_t4096_zipf_q6k", 4096, down_dtype=Q6_K, zipf=True,
+              description="prefill of 4096 tokens, Zipf(1.2) selection bias, Q6_K down"),
+    5: Config("ffn_stack_24l_t1", 1, layers=N_LAYERS,
+              description="24-layer FFN path: 2 dense + 22 MoE (down Q4_K on even, Q6_K on odd layers)"),
+}
+
+
+def config_layer(cfg_id, seed=0, layer=0, **kw):
+    cfg = CONFIGS[cfg_id]
+    bias = zipf_bias(seed) if cfg.zipf else None
+    return moe_weights(seed, layer=layer, down_dtype=cfg.down_dtype, bias=bias, **kw)
+
+
+def stack_layers(seed=0, hidden=HIDDEN, moe_ff=MOE_FF, dense_ff=DENSE_FF, n_experts=N_EXPERTS,
+                 n_layers=N_LAYERS, n_dense=N_DENSE):
+    """Config 5: layers < n_dense dense; MoE down in Q4_K on even layers, Q6_K on odd ones."""
+    out = []
+    for layer in range(n_layers):
+        gain = np.ones(hidden, np.float32)
+        if layer < n_dense:
+            out.append((gain, dense_weights(seed, layer, hidden, dense_ff)))
+        else:
+            dd = Q4_K if layer % 2 == 0 else Q6_K
+            out.append((gain, moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=dd)))
+    return out

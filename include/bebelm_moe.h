@@ -1,0 +1,172 @@
+/*
+ * bebelm_moe.h — C ABI of the MI355X (gfx950) MoE FFN library, libbebelm_moe.so.
+ *
+ * This is the drop-in boundary for the reference's (maximecb/bebelm 0.3.6, Rust) sparse-MoE
+ * FFN path. The reference has no FFI of its own; each entry point below names the Rust
+ * function or signature it replaces (paths relative to the reference's src/). A Rust caller
+ * binds these with `extern "C"` declarations (INTEGRATION.md shows the binding).
+ *
+ * Conventions
+ *   - Every entry point returns int: 0 (BB_OK) on success, a BB_ERR_* code otherwise, with a
+ *     message in bb_last_error() (thread-local). No C++ exception or abort crosses the ABI;
+ *     where the reference panics on a shape/dtype violation (matmul.rs:851-857, :909-918,
+ *     :1023-1033) this library returns BB_ERR_ARG / BB_ERR_SHAPE / BB_ERR_DTYPE instead.
+ *   - Dtype codes are ggml's (tensor.rs:41-63): F32=0, F16=1, Q4_K=12, Q6_K=14.
+ *   - Weights are uploaded once (bb_tensor_upload) in their native GGUF block layout (Q4_K:
+ *     144-byte blocks, Q6_K: 210-byte blocks) and are immutable afterwards; a tensor may be
+ *     shared by any number of layers.
+ *   - Activation pointers are host memory when `loc` is BB_LOC_HOST (the call copies in,
+ *     computes and copies out before returning) or device memory of the context's GPU when
+ *     `loc` is BB_LOC_DEVICE (the call only enqueues work on the context's stream; device
+ *     pointers must be 16-byte aligned).
+ *   - A context owns one HIP stream (default priority) and one workspace; calls on one context
+ *     must not overlap. Use one context per calling thread.
+ *   - Results are bit-identical to the reference CPU path on the same inputs (integer dots
+ *     exact, f32 epilogues in the reference's order), except rmsnorm's f64 sum order (see
+ *     bb_rmsnorm).
+ */
+#ifndef BEBELM_MOE_H
+#define BEBELM_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum bb_status {
+  BB_OK = 0,
+  BB_ERR_ARG = 1,    /* null pointer, bad flag, misaligned device pointer            */
+  BB_ERR_DTYPE = 2,  /* dtype not supported on this path                             */
+  BB_ERR_SHAPE = 3,  /* sizes inconsistent (byte_size mismatch, n_in % block != 0)   */
+  BB_ERR_HIP = 4,    /* a HIP runtime call failed                                     */
+  BB_ERR_OOM = 5,    /* device allocation failed                                      */
+  BB_ERR_RANGE = 6   /* size beyond what this build supports                          */
+};
+
+enum bb_dtype { BB_F32 = 0, BB_F16 = 1, BB_Q4_K = 12, BB_Q6_K = 14 };
+enum bb_loc { BB_LOC_HOST = 0, BB_LOC_DEVICE = 1 };
+
+typedef struct bb_ctx bb_ctx;
+typedef struct bb_tensor bb_tensor;
+typedef struct bb_moe bb_moe;
+typedef struct bb_dense bb_dense;
+typedef struct bb_stack bb_stack;
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* bb_last_error(void);
+/* Library version string. */
+const char* bb_version(void);
+
+/* ---- context ---------------------------------------------------------------------------- */
+/* New: there is no device context in the reference (one process, rayon pool, main.rs:155-165). */
+int bb_ctx_create(int device, bb_ctx** out);
+int bb_ctx_destroy(bb_ctx* ctx);
+/* Run subsequent work on a caller-owned hipStream_t (NULL restores the context's own stream). */
+int bb_ctx_set_stream(bb_ctx* ctx, void* hip_stream);
+int bb_ctx_get_stream(bb_ctx* ctx, void** hip_stream);
+int bb_ctx_synchronize(bb_ctx* ctx);
+/* Per-kernel timing with HIP events around every launch (off by default). */
+int bb_ctx_profile(bb_ctx* ctx, int enable);
+/* Accumulated device time of kernel `idx` (0 <= idx < bb_kernel_count()) since the last reset. */
+int bb_kernel_count(void);
+int bb_ctx_kernel_stats(bb_ctx* ctx, int idx, const char** name, double* total_ms, int64_t* launches);
+int bb_ctx_reset_stats(bb_ctx* ctx);
+
+/* ---- weights ------------------------------------------------------------------------------ */
+/* Replaces the zero-copy `GgufFile::tensor_data` view (gguf.rs:191-193) with a one-time copy
+ * into HBM, native block layout kept. `dims` are GGUF dims ([in, out] or [in, out, n_expert]);
+ * nbytes must equal GgmlType::byte_size(prod(dims)) (tensor.rs:99-105). */
+int bb_tensor_upload(bb_ctx* ctx, uint32_t dtype, const void* bytes, size_t nbytes, const uint64_t* dims,
+                     int ndims, bb_tensor** out);
+int bb_tensor_free(bb_tensor* t);
+int bb_tensor_device_ptr(const bb_tensor* t, void** dev);
+
+/* ---- kernel-level mirrors of src/kernels ----------------------------------------------- */
+/* quantize_q8(x: &[f32]) -> Q8Vec (kernels/matmul.rs:141). q[n], scales[n/256], sums[n/32]
+ * live where `loc` says; n % 256 == 0. */
+int bb_quantize_q8(bb_ctx* ctx, const float* x, size_t n, int8_t* q, float* scales, int32_t* sums, int loc);
+
+/* matvec(dtype, w, n_in, n_out, x, y) (kernels/matmul.rs:850). The weight matrix is the
+ * n_out rows starting `byte_off` bytes into tensor `w` (an expert slice is e*expert_bytes,
+ * model.rs:612-615). */
+int bb_matvec(bb_ctx* ctx, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
+              const float* x, float* y, int loc);
+
+/* matmul(dtype, w, n_in, n_out, x, n_tokens, y) with token-major x and y (kernels/matmul.rs:908). */
+int bb_matmul(bb_ctx* ctx, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
+              const float* x, size_t n_tokens, float* y, int loc);
+
+/* FusedJob (kernels/matmul.rs:995-1005). Only the pre-quantised arm (`qx: Some`) is provided:
+ * it is the one every MoE job takes (model.rs:507, :512, :544). */
+typedef struct {
+  uint32_t dtype;           /* Q4_K or Q6_K                         */
+  const bb_tensor* w;
+  size_t byte_off;          /* first row of this job inside w       */
+  size_t n_in, n_out;
+  const int8_t* qx_q;       /* Q8 of this job's x (bb_quantize_q8)  */
+  const float* qx_scales;
+  const int32_t* qx_sums;
+} bb_fused_job;
+/* matvec_fused_batch(jobs, out) (kernels/matmul.rs:1015): out = Σ n_out values, jobs in order. */
+int bb_matvec_fused_batch(bb_ctx* ctx, const bb_fused_job* jobs, size_t n_jobs, float* out, int loc);
+
+/* swiglu(gate, up, out) (kernels/activation.rs:16) and sigmoid_slice(x) (:25). */
+int bb_swiglu(bb_ctx* ctx, const float* gate, const float* up, float* out, size_t n, int loc);
+int bb_sigmoid_slice(bb_ctx* ctx, float* x, size_t n, int loc);
+/* add_scaled(out, b, s) (kernels/elementwise.rs:12) and add_assign(a, b) (:4). */
+int bb_add_scaled(bb_ctx* ctx, float* out, const float* b, float s, size_t n, int loc);
+int bb_add_assign(bb_ctx* ctx, float* a, const float* b, size_t n, int loc);
+/* rmsnorm(x, gain, eps, out) (kernels/rmsnorm.rs:10) over n_vec rows of n. The f64 sum of
+ * squares is a tree, not the reference's left-to-right sum; the f32 result agrees unless the
+ * two f64 sums fall on opposite sides of an f32 rounding boundary. */
+int bb_rmsnorm(bb_ctx* ctx, const float* x, const float* gain, float eps, size_t n, size_t n_vec, float* out,
+               int loc);
+
+/* ---- MoE layer (model.rs:473-555 decode, model.rs:286-371 batched) ----------------------- */
+/* Tensors as Model::moe_ffn resolves them (model.rs:474-478): router `ffn_gate_inp` F32
+ * [hidden, E]; `exp_probs_b` f32[E] (host); stacked experts gate/up [hidden, ff, E] and
+ * down [ff, hidden, E] in Q4_K or Q6_K. Requires E <= 32, k <= 8, hidden and ff multiples
+ * of 256. */
+int bb_moe_create(bb_ctx* ctx, const bb_tensor* router, const float* exp_probs_b, const bb_tensor* gate_exps,
+                  const bb_tensor* up_exps, const bb_tensor* down_exps, int n_used, bb_moe** out);
+int bb_moe_destroy(bb_moe* moe);
+
+/* Routing trace (host arrays; any may be NULL), for bit-exact checks of the route. */
+typedef struct {
+  float* logits;     /* [T*E] router logits                                  */
+  int32_t* sel;      /* [T*k] experts in selection order                     */
+  float* w;          /* [T*k] renormalised weights                           */
+  int32_t* counts;   /* [E]                                                  */
+  int32_t* offsets;  /* [E+1] exclusive prefix sum of counts                 */
+  int32_t* perm;     /* [T*k] entry t*k+slot, grouped by expert, stable      */
+  int32_t* ties;     /* [1] exactly equal keys among the first k+1 sorted   */
+  float* margin;     /* [T] key[k-1] - key[k]                                */
+} bb_route_trace;
+
+/* T == 1: Model::moe_ffn(layer, x) -> Vec<f32>. T > 1: Model::moe_ffn_batch(layer, x, t)
+ * (token-major x[T*hidden], out[T*hidden]); both bit-identical to the reference. */
+int bb_moe_forward(bb_ctx* ctx, bb_moe* moe, const float* x, size_t T, float* out, int loc,
+                   bb_route_trace* trace);
+
+/* ---- dense FFN and the FFN-path layer stack ---------------------------------------------- */
+/* dense_ffn (model.rs:459-469) / dense_ffn_batch (:262-278): gate/up [hidden, ff], down [ff, hidden]. */
+int bb_dense_create(bb_ctx* ctx, const bb_tensor* gate, const bb_tensor* up, const bb_tensor* down, bb_dense** out);
+int bb_dense_destroy(bb_dense* d);
+int bb_dense_forward(bb_ctx* ctx, bb_dense* d, const float* x, size_t T, float* out, int loc);
+
+/* run_layers (model.rs:105-130) with the operator sub-layer contributing nothing:
+ * per layer h += FFN(rmsnorm(h, ffn_norm)). Exactly one of moe / dense is set per layer. */
+typedef struct {
+  const float* ffn_norm; /* host f32[hidden] */
+  bb_moe* moe;
+  bb_dense* dense;
+} bb_layer_desc;
+int bb_stack_create(bb_ctx* ctx, const bb_layer_desc* layers, size_t n_layers, float eps, bb_stack** out);
+int bb_stack_destroy(bb_stack* s);
+int bb_stack_forward(bb_ctx* ctx, bb_stack* s, const float* x, size_t T, float* h_out, int loc);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,320 @@
+"""ctypes wrapper of the CPU restatement (liboracle.so) — TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the
+product package. See bb_oracle.h for what each function restates and how it is pinned.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_K, Q6_K = 0, 1, 12, 14
+c_void_p, c_size_t, c_int, c_float = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+
+
+class Q8(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("scales", c_void_p), ("sums", c_void_p)]
+
+
+class Job(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_uint32), ("w", c_void_p), ("n_in", c_size_t), ("n_out", c_size_t),
+                ("x", c_void_p), ("has_qx", c_int), ("qx", Q8)]
+
+
+class Moe(ctypes.Structure):
+    _fields_ = [("router_dtype", ctypes.c_uint32), ("router", c_void_p), ("exp_probs_b", c_void_p),
+                ("gate_dtype", ctypes.c_uint32), ("up_dtype", ctypes.c_uint32), ("down_dtype", ctypes.c_uint32),
+                ("gate_exps", c_void_p), ("up_exps", c_void_p), ("down_exps", c_void_p),
+                ("hidden", c_int), ("moe_ff", c_int), ("n_experts", c_int), ("n_used", c_int)]
+
+
+class Trace(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("logits", "sel", "w", "counts", "offsets", "perm", "ties", "margin")]
+
+
+class Dense(ctypes.Structure):
+    _fields_ = [("gate_dtype", ctypes.c_uint32), ("up_dtype", ctypes.c_uint32), ("down_dtype", ctypes.c_uint32),
+                ("gate", c_void_p), ("up", c_void_p), ("down", c_void_p), ("hidden", c_int), ("ff", c_int)]
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [("ffn_norm", c_void_p), ("is_moe", c_int), ("dense", Dense), ("moe", Moe)]
+
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.bbo_f16_to_f32.restype = c_float
+        L.bbo_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.bbo_dot.restype = c_float
+        L.bbo_dot.argtypes = [c_void_p, c_void_p, c_size_t]
+        L.bbo_dot_q4k_block_q8.restype = c_float
+        L.bbo_dot_q4k_block_q8.argtypes = [c_void_p, c_void_p, c_float, c_void_p]
+        L.bbo_dot_q6k_block_q8.restype = c_float
+        L.bbo_dot_q6k_block_q8.argtypes = [c_void_p, c_void_p, c_float]
+        for n in ("bbo_q4k_block_sd", "bbo_q6k_block_idot", "bbo_q6k_block_idot_buffered"):
+            getattr(L, n).restype = ctypes.c_int32
+            getattr(L, n).argtypes = [c_void_p, c_void_p]
+        L.bbo_fused_row_dot.restype = c_float
+        L.bbo_fused_row_dot.argtypes = [ctypes.c_uint32, c_void_p, c_void_p, c_size_t]
+        L.bbo_sigmoid.restype = c_float
+        L.bbo_sigmoid.argtypes = [c_float]
+        L.bbo_silu.restype = c_float
+        L.bbo_silu.argtypes = [c_float]
+        L.bbo_get_scale_min_k4.argtypes = [c_int, c_void_p, c_void_p, c_void_p]
+        L.bbo_dequantize.argtypes = [ctypes.c_uint32, c_void_p, c_size_t, c_void_p]
+        L.bbo_quantize_q8.argtypes = [c_void_p, c_size_t, Q8]
+        L.bbo_matvec.argtypes = [ctypes.c_uint32, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p]
+        L.bbo_matmul.argtypes = [ctypes.c_uint32, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p]
+        L.bbo_matvec_fused_batch.argtypes = [ctypes.POINTER(Job), c_size_t, c_void_p]
+        L.bbo_swiglu.argtypes = [c_void_p, c_void_p, c_void_p, c_size_t]
+        L.bbo_add_scaled.argtypes = [c_void_p, c_void_p, c_float, c_size_t]
+        L.bbo_add_assign.argtypes = [c_void_p, c_void_p, c_size_t]
+        L.bbo_rmsnorm.argtypes = [c_void_p, c_void_p, c_float, c_size_t, c_void_p]
+        L.bbo_moe_ffn.argtypes = [ctypes.POINTER(Moe), c_void_p, c_void_p, ctypes.POINTER(Trace)]
+        L.bbo_moe_ffn_batch.argtypes = [ctypes.POINTER(Moe), c_void_p, c_size_t, c_void_p, ctypes.POINTER(Trace)]
+        L.bbo_dense_ffn.argtypes = [ctypes.POINTER(Dense), c_void_p, c_size_t, c_void_p]
+        L.bbo_ffn_stack.argtypes = [ctypes.POINTER(Layer), c_size_t, c_void_p, c_size_t, c_float, c_void_p]
+        L.bbo_set_threads.argtypes = [c_int]
+        L.bbo_get_threads.restype = c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data if a is not None else None
+
+
+def _chk(rc):
+    if rc != 0:
+        raise ValueError(f"oracle call failed ({rc})")
+
+
+def set_threads(n):
+    lib().bbo_set_threads(int(n))
+
+
+def get_threads():
+    return lib().bbo_get_threads()
+
+
+def f16_to_f32(h):
+    return lib().bbo_f16_to_f32(int(h))
+
+
+def get_scale_min_k4(j, scales):
+    s = np.ascontiguousarray(scales, np.uint8)
+    sc, m = np.zeros(1, np.uint8), np.zeros(1, np.uint8)
+    lib().bbo_get_scale_min_k4(j, _p(s), _p(sc), _p(m))
+    return int(sc[0]), int(m[0])
+
+
+def dequantize(dtype, data, n):
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.zeros(n, np.float32)
+    _chk(lib().bbo_dequantize(dtype, _p(data), n, _p(out)))
+    return out
+
+
+class Q8Vec:
+    def __init__(self, n):
+        self.q = np.zeros(n, np.int8)
+        self.scales = np.zeros(n // 256, np.float32)
+        self.sums = np.zeros(n // 32, np.int32)
+
+    def struct(self):
+        return Q8(_p(self.q), _p(self.scales), _p(self.sums))
+
+
+def quantize_q8(x):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    v = Q8Vec(x.size)
+    lib().bbo_quantize_q8(_p(x), x.size, v.struct())
+    return v
+
+
+def dot(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().bbo_dot(_p(a), _p(b), a.size)
+
+
+def dot_q4k_block_q8(block, qx, sx, sums):
+    block, qx, sums = (np.ascontiguousarray(block, np.uint8), np.ascontiguousarray(qx, np.int8),
+                       np.ascontiguousarray(sums, np.int32))
+    return lib().bbo_dot_q4k_block_q8(_p(block), _p(qx), sx, _p(sums))
+
+
+def dot_q6k_block_q8(block, qx, sx):
+    block, qx = np.ascontiguousarray(block, np.uint8), np.ascontiguousarray(qx, np.int8)
+    return lib().bbo_dot_q6k_block_q8(_p(block), _p(qx), sx)
+
+
+def q4k_block_sd(block, qx):
+    block, qx = np.ascontiguousarray(block, np.uint8), np.ascontiguousarray(qx, np.int8)
+    return lib().bbo_q4k_block_sd(_p(block), _p(qx))
+
+
+def q6k_block_idot(block, qx, buffered=False):
+    block, qx = np.ascontiguousarray(block, np.uint8), np.ascontiguousarray(qx, np.int8)
+    f = lib().bbo_q6k_block_idot_buffered if buffered else lib().bbo_q6k_block_idot
+    return f(_p(block), _p(qx))
+
+
+def fused_row_dot(dtype, row, x):
+    row, x = np.ascontiguousarray(row, np.uint8), np.ascontiguousarray(x, np.float32)
+    return lib().bbo_fused_row_dot(dtype, _p(row), _p(x), x.size)
+
+
+def matvec(dtype, w, n_in, n_out, x):
+    w, x = np.ascontiguousarray(w).view(np.uint8).reshape(-1), np.ascontiguousarray(x, np.float32)
+    y = np.zeros(n_out, np.float32)
+    _chk(lib().bbo_matvec(dtype, _p(w), n_in, n_out, _p(x), _p(y)))
+    return y
+
+
+def matmul(dtype, w, n_in, n_out, x, n_tokens):
+    w, x = np.ascontiguousarray(w).view(np.uint8).reshape(-1), np.ascontiguousarray(x, np.float32)
+    y = np.zeros(n_out * n_tokens, np.float32)
+    _chk(lib().bbo_matmul(dtype, _p(w), n_in, n_out, _p(x), n_tokens, _p(y)))
+    return y
+
+
+def matvec_fused_batch(jobs):
+    """jobs: list of (dtype, w bytes, n_in, n_out, x f32, qx Q8Vec | None)."""
+    arr = (Job * len(jobs))()
+    keep = []
+    total = 0
+    for i, (dt, w, n_in, n_out, x, qx) in enumerate(jobs):
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        keep += [w, x]
+        arr[i] = Job(dt, _p(w), n_in, n_out, _p(x), 1 if qx is not None else 0,
+                     qx.struct() if qx is not None else Q8(None, None, None))
+        total += n_out
+    out = np.zeros(total, np.float32)
+    _chk(lib().bbo_matvec_fused_batch(arr, len(jobs), _p(out)))
+    return out
+
+
+def sigmoid(x):
+    return lib().bbo_sigmoid(float(x))
+
+
+def silu(x):
+    return lib().bbo_silu(float(x))
+
+
+def swiglu(gate, up):
+    gate, up = np.ascontiguousarray(gate, np.float32), np.ascontiguousarray(up, np.float32)
+    out = np.zeros_like(gate)
+    lib().bbo_swiglu(_p(gate), _p(up), _p(out), gate.size)
+    return out
+
+
+def add_scaled(out, b, s):
+    out = np.array(out, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    lib().bbo_add_scaled(_p(out), _p(b), s, out.size)
+    return out
+
+
+def add_assign(a, b):
+    a = np.array(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    lib().bbo_add_assign(_p(a), _p(b), a.size)
+    return a
+
+
+def rmsnorm(x, gain, eps):
+    x, gain = np.ascontiguousarray(x, np.float32), np.ascontiguousarray(gain, np.float32)
+    out = np.zeros_like(x)
+    lib().bbo_rmsnorm(_p(x), _p(gain), eps, x.size, _p(out))
+    return out
+
+
+def _moe_struct(w):
+    return Moe(0, _p(w.router), _p(w.exp_probs_b), w.gate_dtype, w.up_dtype, w.down_dtype, _p(w.gate_exps),
+               _p(w.up_exps), _p(w.down_exps), w.hidden, w.moe_ff, w.n_experts, w.n_used)
+
+
+class TraceArrays:
+    def __init__(self, t, E, k):
+        self.logits = np.zeros(t * E, np.float32)
+        self.sel = np.zeros(t * k, np.int32)
+        self.w = np.zeros(t * k, np.float32)
+        self.counts = np.zeros(E, np.int32)
+        self.offsets = np.zeros(E + 1, np.int32)
+        self.perm = np.zeros(t * k, np.int32)
+        self.ties = np.zeros(1, np.int32)
+        self.margin = np.zeros(t, np.float32)
+
+    def struct(self):
+        return Trace(*(_p(a) for a in (self.logits, self.sel, self.w, self.counts, self.offsets, self.perm,
+                                       self.ties, self.margin)))
+
+
+def moe_ffn(w, x, trace=False):
+    """Model::moe_ffn (one token). Returns out or (out, TraceArrays)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(w.hidden, np.float32)
+    m = _moe_struct(w)
+    tr = TraceArrays(1, w.n_experts, w.n_used) if trace else None
+    ts = tr.struct() if tr else None
+    _chk(lib().bbo_moe_ffn(ctypes.byref(m), _p(x), _p(out), ctypes.byref(ts) if ts else None))
+    return (out, tr) if trace else out
+
+
+def moe_ffn_batch(w, x, t, trace=False):
+    """Model::moe_ffn_batch (t tokens, token-major)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(t * w.hidden, np.float32)
+    m = _moe_struct(w)
+    tr = TraceArrays(t, w.n_experts, w.n_used) if trace else None
+    ts = tr.struct() if tr else None
+    _chk(lib().bbo_moe_ffn_batch(ctypes.byref(m), _p(x), t, _p(out), ctypes.byref(ts) if ts else None))
+    return (out, tr) if trace else out
+
+
+def _dense_struct(d):
+    return Dense(d.gate_dtype, d.up_dtype, d.down_dtype, _p(d.gate), _p(d.up), _p(d.down), d.hidden, d.ff)
+
+
+def dense_ffn(d, x, t=1):
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(t * d.hidden, np.float32)
+    s = _dense_struct(d)
+    _chk(lib().bbo_dense_ffn(ctypes.byref(s), _p(x), t, _p(out)))
+    return out
+
+
+def ffn_stack(layers, x, t=1, eps=1e-5):
+    """layers: list of (gain, MoeWeights | DenseWeights) as bebelm_amd.synth.stack_layers makes."""
+    arr = (Layer * len(layers))()
+    keep = []
+    for i, (gain, w) in enumerate(layers):
+        gain = np.ascontiguousarray(gain, np.float32)
+        keep.append(gain)
+        if hasattr(w, "router"):
+            arr[i] = Layer(_p(gain), 1, Dense(), _moe_struct(w))
+        else:
+            arr[i] = Layer(_p(gain), 0, _dense_struct(w), Moe())
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    h = np.zeros_like(x)
+    _chk(lib().bbo_ffn_stack(arr, len(layers), _p(x), t, eps, _p(h)))
+    return h
