@@ -74,10 +74,6 @@ void* dev_alloc(size_t bytes) {
   return p;
 }
 
-constexpr int ROUTE_CTR = 0;        // 1 counter
-constexpr int GATEUP_CTR = 64;      // E * ff/256 counters
-constexpr int DOWN_CTR = 4096;      // hidden/32 counters
-constexpr int N_CTR = 16384;
 
 }  // namespace
 
@@ -89,7 +85,6 @@ struct bb_ctx {
   size_t ws_bytes = 0;
   uint8_t* io = nullptr;  // staging for host-pointer calls
   size_t io_bytes = 0;
-  uint32_t* counters = nullptr;
   bool profile = false;
   struct Pending {
     int id;
@@ -114,6 +109,7 @@ struct bb_moe {
   bb_ctx* ctx;
   const bb_tensor *router, *gate, *up, *down;
   float* bias_dev;
+  float* router_cm;  // router regrouped by dot chain (layout of k_route's loads)
   int H, F, E, K;
   size_t stride_g, stride_u, stride_d;
 };
@@ -237,10 +233,9 @@ size_t tensor_elems(const bb_tensor* t) {
 // ---- MoE forward on device pointers -----------------------------------------------------------
 
 struct MoeWs {
-  bb::Q8Bufs xq;
+  bb::XQBufs xq;
   bb::RouteBufs rb;
   float* act;
-  bb::Q8Bufs actq;
   float* slots;
 };
 
@@ -250,8 +245,8 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
     Carve cv{pass ? c->ws : nullptr};
     MoeWs w;
     w.xq.q = cv.take<int8_t>(T * H);
-    w.xq.scales = cv.take<float>(T * H / 256);
-    w.xq.sums = cv.take<int32_t>(T * H / 32);
+    w.xq.sx = cv.take<float>(T * H / 256);
+    w.xq.pairs = cv.take<uint32_t>(T * H / 256 * 12);
     w.rb.logits = cv.take<float>(T * E);
     w.rb.sel = cv.take<int32_t>(T * K);
     w.rb.wts = cv.take<float>(T * K);
@@ -259,13 +254,9 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
     w.rb.offsets = cv.take<int32_t>(E + 1);
     w.rb.perm = cv.take<int32_t>(T * K);
     w.rb.hit = cv.take<int32_t>(E + 1);
-    w.rb.ties = cv.take<int32_t>(1);
+    w.rb.ties = cv.take<int32_t>(T);
     w.rb.margin = cv.take<float>(T);
-    w.rb.counter = c->counters + ROUTE_CTR;
     w.act = cv.take<float>(T * K * F);
-    w.actq.q = cv.take<int8_t>(T * K * F);
-    w.actq.scales = cv.take<float>(T * K * F / 256);
-    w.actq.sums = cv.take<int32_t>(T * K * F / 32);
     w.slots = cv.take<float>(T * K * H);
     if (pass == 0) ensure_ws(c, cv.off);
     else return w;
@@ -273,27 +264,25 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
   return {};
 }
 
-// The small-batch route kernel keeps every (token, slot) entry in LDS: T*k <= 1024.
-constexpr size_t SMALL_ENTRIES_MAX = 1024;
 
 void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr) {
   need(T >= 1, BB_ERR_ARG, "T must be >= 1");
-  need(T * (size_t)m->K <= SMALL_ENTRIES_MAX, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
+  need(T * (size_t)m->K <= (size_t)bb::MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
   MoeWs w = carve_moe(c, m, T);
-  const int max_hit = (int)std::min<size_t>((size_t)m->E, T * m->K);
   const int batch_mode = T > 1;
+  const int max_hit = (int)std::min<size_t>((size_t)m->E, T * m->K);
   launch(c, bb::K_ROUTE, [&] {
-    return bb::launch_route_small(c->stream, reinterpret_cast<const float*>(m->router->dev), m->bias_dev, x, (int)T,
-                                  m->H, m->E, m->K, w.xq, w.rb);
+    return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, w.xq, w.rb);
   });
   launch(c, bb::K_GATEUP, [&] {
-    return bb::launch_gateup(c->stream, (int)m->gate->dtype, m->gate->dev, m->up->dev, m->stride_g, m->stride_u, m->H,
-                             m->F, m->K, max_hit, batch_mode, w.rb, w.xq, w.act, w.actq, c->counters + GATEUP_CTR);
+    return bb::launch_gateup(c->stream, (int)m->gate->dtype, m->gate->dev, m->up->dev, m->stride_g, m->stride_u,
+                             (int)T, m->H, m->F, m->E, m->K, max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
   });
   launch(c, bb::K_DOWN, [&] {
-    return bb::launch_down(c->stream, (int)m->down->dtype, m->down->dev, m->stride_d, m->H, m->F, m->K, (int)T,
-                           max_hit, batch_mode, w.rb, w.actq, w.slots, out, c->counters + DOWN_CTR);
+    return bb::launch_down(c->stream, (int)m->down->dtype, m->down->dev, m->stride_d, (int)T, m->H, m->F, m->K, max_hit,
+                           batch_mode, w.rb, w.act, w.slots);
   });
+  launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
   if (tr) {
     const size_t E = m->E, K = m->K;
     auto cp = [&](void* dst, const void* src, size_t bytes) {
@@ -305,9 +294,15 @@ void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out,
     cp(tr->counts, w.rb.counts, E * 4);
     cp(tr->offsets, w.rb.offsets, (E + 1) * 4);
     cp(tr->perm, w.rb.perm, T * K * 4);
-    cp(tr->ties, w.rb.ties, 4);
+    std::vector<int32_t> ties(T);
+    cp(ties.data(), w.rb.ties, T * 4);
     cp(tr->margin, w.rb.margin, T * 4);
     check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (tr->ties) {
+      int32_t tot = 0;
+      for (int32_t v : ties) tot += v;
+      *tr->ties = tot;
+    }
   }
 }
 
@@ -440,12 +435,9 @@ int bb_ctx_create(int device, bb_ctx** out) {
       set_device(c);
       check_hip(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking), "hipStreamCreate");
       c->stream = c->own;
-      c->counters = static_cast<uint32_t*>(dev_alloc(N_CTR * sizeof(uint32_t)));
-      check_hip(hipMemset(c->counters, 0, N_CTR * sizeof(uint32_t)), "hipMemset");
       check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
     } catch (...) {
       if (c->own) (void)hipStreamDestroy(c->own);
-      if (c->counters) (void)hipFree(c->counters);
       delete c;
       throw;
     }
@@ -465,7 +457,6 @@ int bb_ctx_destroy(bb_ctx* c) {
     for (auto e : c->event_pool) (void)hipEventDestroy(e);
     if (c->ws) (void)hipFree(c->ws);
     if (c->io) (void)hipFree(c->io);
-    if (c->counters) (void)hipFree(c->counters);
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
   });
@@ -710,8 +701,8 @@ int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const b
     need(E >= 1 && E <= 32, BB_ERR_RANGE, "this build supports up to 32 experts");
     need(n_used >= 1 && n_used <= 8 && (uint64_t)n_used <= E, BB_ERR_RANGE, "n_used must be 1..min(8, E)");
     need(H % 256 == 0 && F % 256 == 0 && H >= 256 && F >= 256, BB_ERR_SHAPE, "hidden and ff must be multiples of 256");
-    need(H <= 32768 && F <= 32768, BB_ERR_RANGE, "hidden/ff above 32768 are not supported");
-    need(E * (F / 256) <= DOWN_CTR - GATEUP_CTR && H / 32 <= N_CTR - DOWN_CTR, BB_ERR_RANGE, "counter space exceeded");
+    need(H <= (uint64_t)bb::GU_H_MAX && F <= (uint64_t)bb::DN_F_MAX, BB_ERR_RANGE,
+         "hidden and ff above 2048 are not supported by the LDS-staged GEMV kernels");
     set_device(c);
     auto* m = new bb_moe();
     m->ctx = c;
@@ -733,7 +724,14 @@ int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const b
     try {
       m->bias_dev = static_cast<float*>(dev_alloc(E * 4));
       check_hip(hipMemcpy(m->bias_dev, bias, E * 4, hipMemcpyHostToDevice), "bias upload");
+      m->router_cm = static_cast<float*>(dev_alloc(E * H * 4));
+      check_hip(bb::launch_router_chain_major(c->stream, reinterpret_cast<const float*>(router->dev), (int)H, (int)E,
+                                              m->router_cm),
+                "router layout");
+      check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     } catch (...) {
+      if (m->bias_dev) (void)hipFree(m->bias_dev);
+      if (m->router_cm) (void)hipFree(m->router_cm);
       delete m;
       throw;
     }
@@ -747,6 +745,7 @@ int bb_moe_destroy(bb_moe* m) {
     set_device(m->ctx);
     (void)hipStreamSynchronize(m->ctx->stream);
     (void)hipFree(m->bias_dev);
+    (void)hipFree(m->router_cm);
     delete m;
   });
 }

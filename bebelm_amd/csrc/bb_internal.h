@@ -16,9 +16,8 @@ struct RouteBufs {
   int32_t* offsets;   // [E+1]
   int32_t* perm;      // [T*K]  group position -> entry t*K+k
   int32_t* hit;       // [E+1]  hit[0] = number of experts with members, hit[1..] ascending ids
-  int32_t* ties;      // [1]
+  int32_t* ties;      // [T]  exactly equal keys among the first k+1 of each token
   float* margin;      // [T]
-  uint32_t* counter;  // grid-completion counter (self-resetting)
 };
 
 struct Q8Bufs {
@@ -46,16 +45,37 @@ enum KernelId : int {
 };
 const char* kernel_name(int id);
 
-hipError_t launch_route_small(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H,
-                              int E, int K, Q8Bufs xq, RouteBufs rb);
+// Q8 activation record used by the decode GEMV kernels: quants, per-256 scales and the int16
+// sum pairs consumed by v_dot2 (12 dwords per 256-block; see bb_rowlane.h).
+struct XQBufs {
+  int8_t* q;
+  float* sx;
+  uint32_t* pairs;
+};
+
+// Decode / small-batch path limits: T*k (token, slot) entries per call; members of one expert
+// staged in LDS at a time (MCH); largest hidden / ff (8 super-blocks, one per wave).
+constexpr int MAX_ENTRIES = 1024;
+constexpr int MCH = 8;
+constexpr int GU_H_MAX = 2048;
+constexpr int DN_F_MAX = 2048;
+// Target number of blocks of one decode GEMV launch (one 8-wave block per CU at the VGPR
+// budget of the double-buffered rows); each block walks enough row tiles to cover the work.
+constexpr int GEMV_BLOCKS = 256;
+
+hipError_t launch_route(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H, int E,
+                        int K, XQBufs xq, RouteBufs rb);
+
+hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc);
 
 hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t stride_g,
-                         size_t stride_u, int H, int F, int K, int max_hit, int batch_mode, const RouteBufs& rb,
-                         Q8Bufs xq, float* act, Q8Bufs actq, uint32_t* counters);
+                         size_t stride_u, int T, int H, int F, int E, int K, int max_hit, int batch_mode, int publish,
+                         const RouteBufs& rb, XQBufs xq, float* act);
 
-hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int H, int F, int K, int T,
-                       int max_hit, int batch_mode, const RouteBufs& rb, Q8Bufs actq, float* slots, float* out,
-                       uint32_t* counters);
+hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int T, int H, int F, int K,
+                       int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots);
+
+hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out);
 
 hipError_t launch_quantize(hipStream_t s, const float* x, size_t n_vec, size_t n, Q8Bufs q);
 

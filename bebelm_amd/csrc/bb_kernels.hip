@@ -13,7 +13,7 @@
 namespace bb {
 
 const char* kernel_name(int id) {
-  static const char* names[K_COUNT] = {"route_small",  "gateup_swiglu", "down_combine", "quantize_q8",
+  static const char* names[K_COUNT] = {"route_gating",  "gateup_swiglu", "down_combine", "quantize_q8",
                                        "rows_q8",      "rows_f32",      "elementwise",  "rmsnorm",
                                        "route_large",  "dispatch",      "gemm_gateup",  "gemm_down",
                                        "combine"};
@@ -46,260 +46,6 @@ __device__ __forceinline__ float dot32_half(const uint8_t* __restrict__ a, const
   float r = y + __shfl_down(y, 1, 32);
   for (; i < n; ++i) r = r + ld_w<DT>(a, i) * b[i];
   return r;
-}
-
-// ---------------------------------------------------------------------------------------------
-// Router + gating + dispatch for a small token batch (model.rs:483-495 per token, :316-322).
-// Blocks [0, E): router row e for every token. Blocks [E, ...): Q8 quantisation of x, one
-// 256-block per wave (model.rs:501). The last block to finish (grid-completion counter) runs
-// sigmoid / top-k / renormalisation per token on 32-lane half-waves and the stable counting
-// sort by expert.
-__global__ void __launch_bounds__(256) k_route_small(const float* __restrict__ W, const float* __restrict__ bias,
-                                                     const float* __restrict__ x, int T, int H, int E, int K,
-                                                     Q8Bufs xq, RouteBufs rb) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, c = lane & 31;
-  const int nbx = H / QK;
-  if ((int)blockIdx.x < E) {
-    const int e = blockIdx.x;
-    const uint8_t* wr = reinterpret_cast<const uint8_t*>(W + (size_t)e * H);
-    for (int base = wave * 2; base < T; base += 8) {
-      const int t = base + half;
-      const int tc = t < T ? t : T - 1;
-      const float r = dot32_half<DT_F32>(wr, x + (size_t)tc * H, H, c);
-      if (c == 0 && t < T) rb.logits[(size_t)t * E + e] = r;
-    }
-  } else {
-    const int qi = ((int)blockIdx.x - E) * 4 + wave;
-    if (qi < T * nbx) {
-      const int t = qi / nbx, b = qi % nbx;
-      const float4 v = *reinterpret_cast<const float4*>(x + (size_t)t * H + b * QK + 4 * lane);
-      wave_quantize_block(v, xq.q + (size_t)t * H + b * QK, xq.scales + (size_t)t * nbx + b,
-                          xq.sums + (size_t)t * (H / 32) + b * 8);
-    }
-  }
-
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(rb.counter, 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  __shared__ int32_t s_sel[1024];
-  __shared__ int32_t s_cnt[64];
-  __shared__ int32_t s_off[65];
-  __shared__ int32_t s_ties;
-  if (tid == 0) s_ties = 0;
-  if (tid < 64) s_cnt[tid] = 0;
-  __syncthreads();
-
-  for (int base = wave * 2; base < T; base += 8) {
-    const int t = base + half;
-    const int tc = t < T ? t : T - 1;
-    const bool live = c < E;
-    const float s = live ? sigmoid(rb.logits[(size_t)tc * E + c]) : 0.0f;
-    const float key = live ? s + bias[c] : 0.0f;
-    const int32_t kk = total_key(key);
-    // (key, -index) packed so a plain max picks the highest key, lowest index first.
-    long long cand = live ? (((long long)kk << 8) | (long long)(255 - c)) : (long long)(-0x7fffffffffffffffLL - 1);
-    int32_t prev_kk = 0;
-    float prev_key = 0.0f, denom = -0.0f;
-    int sel_r[8];
-    float s_r[8];
-    int ties = 0;
-    float margin = __builtin_inff();
-    const int rounds = K < E ? K + 1 : K;
-    for (int r = 0; r < rounds; ++r) {
-      long long m = cand;
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) {
-        const int lo = __shfl_xor((int)(m & 0xffffffffLL), o, 32);
-        const int hi = __shfl_xor((int)(m >> 32), o, 32);
-        const long long other = ((long long)hi << 32) | (unsigned)lo;
-        m = other > m ? other : m;
-      }
-      const int ew = 255 - (int)(m & 0xff);
-      const int32_t kw = (int32_t)(m >> 8);
-      const float kwf = __shfl(key, ew, 32);
-      if (c == ew) cand = (long long)(-0x7fffffffffffffffLL - 1);
-      if (r > 0 && kw == prev_kk) ++ties;
-      if (r == K) margin = prev_key - kwf;
-      if (r < K) {
-        sel_r[r] = ew;
-        s_r[r] = __shfl(s, ew, 32);
-      }
-      prev_kk = kw;
-      prev_key = kwf;
-    }
-    for (int r = 0; r < K; ++r) denom += s_r[r];
-    denom = denom + 1e-6f;
-    if (c == 0 && t < T) {
-      for (int r = 0; r < K; ++r) {
-        rb.sel[(size_t)t * K + r] = sel_r[r];
-        rb.wts[(size_t)t * K + r] = s_r[r] / denom;
-        s_sel[t * K + r] = sel_r[r];
-      }
-      rb.margin[t] = margin;
-      if (ties) atomicAdd(&s_ties, ties);
-    }
-  }
-  __syncthreads();
-  const int n_ent = T * K;
-  for (int i = tid; i < n_ent; i += 256) atomicAdd(&s_cnt[s_sel[i]], 1);
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0, nh = 0;
-    s_off[0] = 0;
-    for (int e = 0; e < E; ++e) {
-      rb.counts[e] = s_cnt[e];
-      if (s_cnt[e] > 0) rb.hit[1 + nh++] = e;
-      acc += s_cnt[e];
-      s_off[e + 1] = acc;
-      rb.offsets[e + 1] = acc;
-    }
-    rb.offsets[0] = 0;
-    rb.hit[0] = nh;
-    rb.ties[0] = s_ties;
-    *rb.counter = 0u;
-  }
-  __syncthreads();
-  // model.rs:317-322: within an expert, entries keep (token, slot) order.
-  for (int i = tid; i < n_ent; i += 256) {
-    const int e = s_sel[i];
-    int rank = 0;
-    for (int j = 0; j < i; ++j) rank += s_sel[j] == e;
-    rb.perm[s_off[e] + rank] = i;
-  }
-}
-
-hipError_t launch_route_small(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H,
-                              int E, int K, Q8Bufs xq, RouteBufs rb) {
-  const int nq = (T * (H / QK) + 3) / 4;
-  hipLaunchKernelGGL(k_route_small, dim3(E + nq), dim3(256), 0, s, router, bias, x, T, H, E, K, xq, rb);
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------------------------
-// Gate/up GEMV + SwiGLU for every (hit expert, member token) (model.rs:497-524, :340-351).
-// Block (rt, u): 4 waves x 8 groups; groups 0-3 take gate rows o, groups 4-7 the matching up
-// rows, so silu(gate)*up is formed in registers. The last block of each 256-row slice of an
-// expert quantises that slice of act for all its members (model.rs:530-534, matmul.rs:933).
-constexpr int GU_ROWS = 16;
-
-template <int DT>
-__global__ void __launch_bounds__(256) k_gateup(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
-                                                size_t stride_g, size_t stride_u, int H, int F, int K, int batch_mode,
-                                                RouteBufs rb, Q8Bufs xq, float* __restrict__ act, Q8Bufs actq,
-                                                uint32_t* __restrict__ counters) {
-  const int u = blockIdx.y;
-  if (u >= rb.hit[0]) return;
-  const int e = rb.hit[1 + u];
-  const int p0 = rb.offsets[e], p1 = rb.offsets[e + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 3, p = lane & 7;
-  const int o = blockIdx.x * GU_ROWS + wave * 4 + (g & 3);
-  const int nb = H / QK;
-  const size_t row_bytes = (size_t)nb * RowDot<DT>::BLOCK_BYTES;
-  const uint8_t* row = (g < 4 ? gate + (size_t)e * stride_g : up + (size_t)e * stride_u) + (size_t)o * row_bytes;
-  const float start = (batch_mode && p1 - p0 > 1) ? 0.0f : -0.0f;
-  for (int j = p0; j < p1; ++j) {
-    const int t = rb.perm[j] / K;
-    const float acc = row_dot_q8<DT>(row, nb, p, xq.q + (size_t)t * H, xq.scales + (size_t)t * nb,
-                                     xq.sums + (size_t)t * (H / 32), start);
-    const float upv = __shfl(acc, (lane + 32) & 63);
-    if (g < 4 && p == 0) act[(size_t)j * F + o] = silu(acc) * upv;
-  }
-
-  __shared__ int s_last;
-  const int nbf = F / QK;
-  const int blk = (blockIdx.x * GU_ROWS) / QK;
-  uint32_t* ctr = counters + (size_t)u * nbf + blk;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(ctr, 1u) == (uint32_t)(QK / GU_ROWS - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int j = p0 + wave; j < p1; j += 4) {
-    const float4 v = *reinterpret_cast<const float4*>(act + (size_t)j * F + blk * QK + 4 * lane);
-    wave_quantize_block(v, actq.q + (size_t)j * F + blk * QK, actq.scales + (size_t)j * nbf + blk,
-                        actq.sums + (size_t)j * (F / 32) + blk * 8);
-  }
-  if (tid == 0) *ctr = 0u;
-}
-
-hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t stride_g,
-                         size_t stride_u, int H, int F, int K, int max_hit, int batch_mode, const RouteBufs& rb,
-                         Q8Bufs xq, float* act, Q8Bufs actq, uint32_t* counters) {
-  dim3 grid(F / GU_ROWS, max_hit);
-  if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_gateup<DT_Q4_K>, grid, dim3(256), 0, s, gate, up, stride_g, stride_u, H, F, K, batch_mode,
-                       rb, xq, act, actq, counters);
-  else
-    hipLaunchKernelGGL(k_gateup<DT_Q6_K>, grid, dim3(256), 0, s, gate, up, stride_g, stride_u, H, F, K, batch_mode,
-                       rb, xq, act, actq, counters);
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------------------------
-// Down GEMV per (hit expert, member) into its (token, slot) row, then the ordered combine
-// out[t] = Σ_k w[t,k]·down[t,k] in selection order (model.rs:547-553, :361-369), run by the
-// last expert block to finish each 32-row tile.
-constexpr int DN_ROWS = 32;
-
-template <int DT>
-__global__ void __launch_bounds__(256) k_down(const uint8_t* __restrict__ down, size_t stride_d, int H, int F, int K,
-                                              int T, int batch_mode, RouteBufs rb, Q8Bufs actq,
-                                              float* __restrict__ slots, float* __restrict__ out,
-                                              uint32_t* __restrict__ counters) {
-  const int u = blockIdx.y;
-  const int n_hit = rb.hit[0];
-  if (u >= n_hit) return;
-  const int e = rb.hit[1 + u];
-  const int p0 = rb.offsets[e], p1 = rb.offsets[e + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 3, p = lane & 7;
-  const int o = blockIdx.x * DN_ROWS + wave * 8 + g;
-  const int nb = F / QK;
-  const size_t row_bytes = (size_t)nb * RowDot<DT>::BLOCK_BYTES;
-  const uint8_t* row = down + (size_t)e * stride_d + (size_t)o * row_bytes;
-  const float start = (batch_mode && p1 - p0 > 1) ? 0.0f : -0.0f;
-  for (int j = p0; j < p1; ++j) {
-    const int i = rb.perm[j];
-    const float acc = row_dot_q8<DT>(row, nb, p, actq.q + (size_t)j * F, actq.scales + (size_t)j * nb,
-                                     actq.sums + (size_t)j * (F / 32), start);
-    if (p == 0) slots[(size_t)i * H + o] = acc;
-  }
-
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = atomicAdd(&counters[blockIdx.x], 1u) == (uint32_t)(n_hit - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int idx = tid; idx < T * DN_ROWS; idx += 256) {
-    const int t = idx / DN_ROWS, oo = blockIdx.x * DN_ROWS + idx % DN_ROWS;
-    float acc = 0.0f;
-    for (int k = 0; k < K; ++k) acc = acc + rb.wts[(size_t)t * K + k] * slots[((size_t)t * K + k) * H + oo];
-    out[(size_t)t * H + oo] = acc;
-  }
-  if (tid == 0) counters[blockIdx.x] = 0u;
-}
-
-hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int H, int F, int K, int T,
-                       int max_hit, int batch_mode, const RouteBufs& rb, Q8Bufs actq, float* slots, float* out,
-                       uint32_t* counters) {
-  dim3 grid(H / DN_ROWS, max_hit);
-  if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_down<DT_Q4_K>, grid, dim3(256), 0, s, down, stride_d, H, F, K, T, batch_mode, rb, actq,
-                       slots, out, counters);
-  else
-    hipLaunchKernelGGL(k_down<DT_Q6_K>, grid, dim3(256), 0, s, down, stride_d, H, F, K, T, batch_mode, rb, actq,
-                       slots, out, counters);
-  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------------------
