@@ -107,11 +107,13 @@ struct bb_tensor {
 
 struct bb_moe {
   bb_ctx* ctx;
-  const bb_tensor *router, *gate, *up, *down;
   float* bias_dev;
-  float* router_cm;  // router regrouped by dot chain (layout of k_route's loads)
+  float* router_cm;    // router regrouped by dot chain (layout of k_route's loads)
+  uint8_t* gu_packed;  // gate/up experts, tile-packed and interleaved
+  uint8_t* dn_packed;  // down experts, tile-packed
   int H, F, E, K;
-  size_t stride_g, stride_u, stride_d;
+  int gu_dtype, dn_dtype;
+  size_t stride_gu, stride_dn;  // packed bytes per expert
 };
 
 struct bb_dense {
@@ -275,11 +277,11 @@ void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out,
     return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, w.xq, w.rb);
   });
   launch(c, bb::K_GATEUP, [&] {
-    return bb::launch_gateup(c->stream, (int)m->gate->dtype, m->gate->dev, m->up->dev, m->stride_g, m->stride_u,
-                             (int)T, m->H, m->F, m->E, m->K, max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
+    return bb::launch_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
+                             max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
   });
   launch(c, bb::K_DOWN, [&] {
-    return bb::launch_down(c->stream, (int)m->down->dtype, m->down->dev, m->stride_d, (int)T, m->H, m->F, m->K, max_hit,
+    return bb::launch_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->K, max_hit,
                            batch_mode, w.rb, w.act, w.slots);
   });
   launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
@@ -706,10 +708,6 @@ int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const b
     set_device(c);
     auto* m = new bb_moe();
     m->ctx = c;
-    m->router = router;
-    m->gate = gate;
-    m->up = up;
-    m->down = down;
     m->H = (int)H;
     m->F = (int)F;
     m->E = (int)E;
@@ -718,20 +716,32 @@ int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const b
     block_of(gate->dtype, be, bgate);
     block_of(up->dtype, be, bup);
     block_of(down->dtype, be, bdown);
-    m->stride_g = F * (H / 256) * bgate;  // model.rs:612-615
-    m->stride_u = F * (H / 256) * bup;
-    m->stride_d = H * (F / 256) * bdown;
+    const size_t stride_g = F * (H / 256) * bgate;  // model.rs:612-615
+    const size_t stride_u = F * (H / 256) * bup;
+    const size_t stride_d = H * (F / 256) * bdown;
+    m->gu_dtype = (int)gate->dtype;
+    m->dn_dtype = (int)down->dtype;
+    m->stride_gu = (F / 32) * (H / 256) * bb::pack_tile_block_bytes(m->gu_dtype);
+    m->stride_dn = (H / 64) * (F / 256) * bb::pack_tile_block_bytes(m->dn_dtype);
     try {
       m->bias_dev = static_cast<float*>(dev_alloc(E * 4));
       check_hip(hipMemcpy(m->bias_dev, bias, E * 4, hipMemcpyHostToDevice), "bias upload");
       m->router_cm = static_cast<float*>(dev_alloc(E * H * 4));
+      m->gu_packed = static_cast<uint8_t*>(dev_alloc(E * m->stride_gu));
+      m->dn_packed = static_cast<uint8_t*>(dev_alloc(E * m->stride_dn));
       check_hip(bb::launch_router_chain_major(c->stream, reinterpret_cast<const float*>(router->dev), (int)H, (int)E,
                                               m->router_cm),
                 "router layout");
+      check_hip(bb::launch_pack_rows(c->stream, m->gu_dtype, gate->dev, up->dev, stride_g, stride_u, (int)F,
+                                     (int)(H / 256), (int)E, m->gu_packed),
+                "gate/up packing");
+      check_hip(bb::launch_pack_rows(c->stream, m->dn_dtype, down->dev, nullptr, stride_d, 0, (int)H, (int)(F / 256),
+                                     (int)E, m->dn_packed),
+                "down packing");
       check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     } catch (...) {
-      if (m->bias_dev) (void)hipFree(m->bias_dev);
-      if (m->router_cm) (void)hipFree(m->router_cm);
+      for (void* p : {(void*)m->bias_dev, (void*)m->router_cm, (void*)m->gu_packed, (void*)m->dn_packed})
+        if (p) (void)hipFree(p);
       delete m;
       throw;
     }
@@ -744,8 +754,8 @@ int bb_moe_destroy(bb_moe* m) {
     if (!m) return;
     set_device(m->ctx);
     (void)hipStreamSynchronize(m->ctx->stream);
-    (void)hipFree(m->bias_dev);
-    (void)hipFree(m->router_cm);
+    for (void* p : {(void*)m->bias_dev, (void*)m->router_cm, (void*)m->gu_packed, (void*)m->dn_packed})
+      (void)hipFree(p);
     delete m;
   });
 }

@@ -4,14 +4,16 @@
 // fence writes back and invalidates the whole L2), so kernel boundaries are the only hand-offs:
 //   k_route         router logits, gating (sigmoid, top-k, renormalisation) and the XQ record
 //                   of x, one block per token                                     (model.rs:484-501)
-//   k_gateup        gate and up rows of one expert, SwiGLU, for the entries that selected
-//                   the expert                                                     (model.rs:504-524)
-//   k_down          Q8 of the expert's act rows, then its down rows               (model.rs:529-548)
+//   k_experts       gate and up rows of the hit experts, SwiGLU, for the entries that
+//     <GATEUP>      selected each expert                                           (model.rs:504-524)
+//   k_experts       Q8 of the experts' act rows, then their down rows             (model.rs:529-548)
+//     <DOWN>
 //   k_combine       out[t] = Σ_k w[t,k]·down[t,k] in selection order              (model.rs:550-553)
 // The GEMV kernels run one weight row per lane: each of the 8 waves of a block owns one
 // 256-weight super-block of the tile's 64 rows, computes its exact value for every member,
-// and lanes sum the per-block values left to right through LDS. Blocks walk several tiles of
-// one expert with the next tile's weights in flight, so HBM streams while the SIMDs compute.
+// and lanes sum the per-block values left to right through LDS. Blocks walk an equal share of
+// (expert, tile) units with the next unit's weights in flight, so HBM streams while the SIMDs
+// compute.
 #include "bb_internal.h"
 #include "bb_rowlane.h"
 
@@ -40,10 +42,10 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
   const int nm = H / 32;
   // issue this lane's chain operands first; they are independent of everything below
   float4 wv[GU_H_MAX / 32 / 4];
-  const float4* wr = reinterpret_cast<const float4*>(Wc + ((size_t)(e < E ? e : 0) * 32 + c) * nm);
+  const float4* wr = reinterpret_cast<const float4*>(Wc) + (size_t)(e < E ? e : 0) * nm / 4 * 32 + c;
 #pragma unroll
   for (int k = 0; k < GU_H_MAX / 32 / 4; ++k)
-    if (k < nm / 4) wv[k] = wr[k];
+    if (k < nm / 4) wv[k] = wr[32 * k];
   const float* xr = x + (size_t)t * H;
   for (int i = tid; i < H / 4; i += 1024) reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(xr)[i];
   __syncthreads();
@@ -112,12 +114,14 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
   }
 }
 
-// Wc[e][c][m] = W[e][32m + c]: the router rows regrouped by dot chain (layout only).
+// Wc[e][k][c][j] = W[e][32(4k + j) + c]: the router rows regrouped so that float4 k of dot chain
+// c (elements 128k + c, +32, +64, +96) sits at float4 index 32k + c of the expert's rows, and
+// the 32 chains of an expert load 512 contiguous bytes per step (layout only).
 __global__ void k_router_chain_major(const float* __restrict__ W, int H, int E, float* __restrict__ Wc) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (size_t)E * H) return;
   const size_t e = i / H, r = i % H, c = r % 32, m = r / 32;
-  Wc[(e * 32 + c) * (H / 32) + m] = W[i];
+  Wc[((e * (H / 128) + m / 4) * 32 + c) * 4 + m % 4] = W[i];
 }
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc) {
@@ -131,28 +135,32 @@ hipError_t launch_route(hipStream_t s, const float* router, const float* bias, c
   return hipGetLastError();
 }
 
-// The u-th expert (ascending id) that some entry selected, and its members: the entries
-// i (= token*K + slot) with sel[i] == e, ascending — the order model.rs:317-322 groups them in.
-// One ballot per 64 entries and a prefix over the per-chunk counts. Returns the member count
-// (0 when fewer than u+1 experts were selected); uniform across the block.
+// ---- dispatch: hit experts and their members ---------------------------------------------------
+// Each block reads the T*K selections once into registers (entry i = token*K + slot lives on
+// lane i%64 of wave (i/64)%8, slot k = i/512), forms the mask of selected experts, and builds
+// member lists on demand: the entries with sel == e in ascending order, the order
+// model.rs:316-322 groups them in (one ballot per 64 entries and a prefix over chunk counts).
+constexpr int SEL_REGS = MAX_ENTRIES / 512;
+
+struct SelRegs {
+  int32_t v[SEL_REGS];
+};
+
 struct SmemMembers {
   int32_t list[MAX_ENTRIES];
   int32_t chunk[MAX_ENTRIES / 64 + 1];
   uint32_t mask;
-  int32_t e;
 };
 
-__device__ int members_of(const int32_t* __restrict__ sel, int n_ent, int u, SmemMembers& sm) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int n_chunks = (n_ent + 63) >> 6;
-  constexpr int KMAX = MAX_ENTRIES / 64 / 8 + 1;
-  int sv[KMAX];
+// Uniform across the block; needs blockDim.x == 512.
+__device__ uint32_t read_selection(const int32_t* __restrict__ sel, int n_ent, SelRegs& sr, SmemMembers& sm) {
+  const int tid = threadIdx.x, lane = tid & 63;
   uint32_t present = 0;
 #pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    const int i = (wave + k * nw) * 64 + lane;
-    sv[k] = i < n_ent ? sel[i] : -1;
-    if (sv[k] >= 0) present |= 1u << sv[k];
+  for (int k = 0; k < SEL_REGS; ++k) {
+    const int i = k * 512 + tid;
+    sr.v[k] = i < n_ent ? sel[i] : -1;
+    if (sr.v[k] >= 0) present |= 1u << sr.v[k];
   }
   if (tid == 0) sm.mask = 0;
   __syncthreads();
@@ -160,15 +168,18 @@ __device__ int members_of(const int32_t* __restrict__ sel, int n_ent, int u, Sme
   for (int o = 32; o >= 1; o >>= 1) present |= (uint32_t)__shfl_xor((int)present, o);
   if (lane == 0) atomicOr(&sm.mask, present);
   __syncthreads();
-  uint32_t mask = sm.mask;
-  for (int k = 0; k < u && mask; ++k) mask &= mask - 1;  // drop the u lowest experts
-  const int e = mask ? __builtin_ctz(mask) : -1;
-  if (e < 0) return 0;
-  unsigned long long masks[KMAX];
+  return sm.mask;
+}
+
+// Fills sm.list with the members of expert e; returns their count (uniform).
+__device__ int member_list(const SelRegs& sr, int n_ent, int e, SmemMembers& sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_chunks = (n_ent + 63) >> 6;
+  unsigned long long masks[SEL_REGS];
 #pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    const int ch = wave + k * nw;
-    masks[k] = __ballot(sv[k] == e);
+  for (int k = 0; k < SEL_REGS; ++k) {
+    const int ch = k * 8 + wave;
+    masks[k] = __ballot(sr.v[k] == e);
     if (ch < n_chunks && lane == 0) sm.chunk[ch] = __popcll(masks[k]);
   }
   __syncthreads();
@@ -180,18 +191,23 @@ __device__ int members_of(const int32_t* __restrict__ sel, int n_ent, int u, Sme
       acc += v;
     }
     sm.chunk[n_chunks] = acc;
-    sm.e = e;
   }
   __syncthreads();
   const unsigned long long lt = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int k = 0; k < KMAX; ++k) {
-    const int ch = wave + k * nw;
+  for (int k = 0; k < SEL_REGS; ++k) {
+    const int ch = k * 8 + wave;
     if (ch < n_chunks && ((masks[k] >> lane) & 1ull)) sm.list[sm.chunk[ch] + __popcll(masks[k] & lt)] = ch * 64 + lane;
   }
   const int cnt = sm.chunk[n_chunks];
   __syncthreads();
   return cnt;
+}
+
+// Id of the u-th set bit of mask (ascending).
+__device__ __forceinline__ int nth_expert(uint32_t mask, int u) {
+  for (int k = 0; k < u; ++k) mask &= mask - 1;
+  return __builtin_ctz(mask);
 }
 
 // The dispatch of model.rs:316-322 for the route trace (counts, offsets, grouped entries).
@@ -223,171 +239,213 @@ __device__ void publish_dispatch(const int32_t* __restrict__ sel, int n_ent, int
   }
 }
 
-// XQ records of up to MCH members in LDS.
+// Members' XQ records in LDS (up to MST at a time) and the per-(member, block, row) values
+// waiting for the left-to-right block sum (MCH members at a time).
+constexpr int MST = 16;
 struct SmemXQ {
-  int8_t q[MCH][GU_H_MAX];
-  uint32_t pairs[MCH][GU_H_MAX / QK][12];
-  float sx[MCH][GU_H_MAX / QK];
+  int8_t q[MST][GU_H_MAX];
+  uint32_t pairs[MST][GU_H_MAX / QK][12];
+  float sx[MST][GU_H_MAX / QK];
 };
 
-// Per-(member, block, row) values waiting for the left-to-right block sum.
 struct SmemT {
   float v[MCH][GU_H_MAX / QK][64];
 };
 
-// Stages the XQ records of members [c0, c0+cnt) into LDS; row_of(m) is the record index.
-template <class RowOf>
-__device__ __forceinline__ void stage_xq(SmemXQ& xs, XQBufs src, int n, int cnt, RowOf row_of) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  const int nq16 = n / 16, nb = n / QK;
-  for (int idx = tid; idx < cnt * nq16; idx += nthr) {
-    const int m = idx / nq16, k = idx % nq16;
-    reinterpret_cast<uint4*>(xs.q[m])[k] = reinterpret_cast<const uint4*>(src.q + row_of(m) * n)[k];
-  }
-  for (int idx = tid; idx < cnt * nb * 12; idx += nthr) {
-    const int m = idx / (nb * 12), k = idx % (nb * 12);
-    xs.pairs[m][k / 12][k % 12] = src.pairs[row_of(m) * nb * 12 + k];
-  }
-  for (int idx = tid; idx < cnt * nb; idx += nthr) {
-    const int m = idx / nb, k = idx % nb;
-    xs.sx[m][k] = src.sx[row_of(m) * nb + k];
-  }
-}
+// ---- expert GEMV (gate/up + SwiGLU, or down) ---------------------------------------------------
+// Work units are (hit expert u, row tile) pairs in u-major order; block b of G takes units
+// [b*U/G, (b+1)*U/G), so every block streams the same number of tiles whatever the expert
+// load. A tile is 64 rows in the tile-packed layout: for gate/up, lanes 0-31 the gate rows and
+// lanes 32-63 the up rows of 32 outputs (model.rs:504-524); for down, 64 outputs of the down
+// rows (model.rs:529-548). Wave w owns super-block w of the tile. A tile's weights are
+// unpacked into registers, the next unit's loads are issued, and only then are the current
+// tile's values computed, so one tile per block is always in flight.
+//
+// Members' activations: for gate/up the route kernel's XQ record of the member's token; for
+// down the member's act row, quantised here (quantize_q8 per member, model.rs:530-534).
+enum : int { GEMV_GATEUP = 0, GEMV_DOWN = 1 };
 
-// ---- gate/up + SwiGLU --------------------------------------------------------------------------
-// Block (g, u): tiles g*ntile .. of hit expert u; a tile is 32 outputs, lanes 0-31 holding the
-// gate rows and lanes 32-63 the up rows of the same outputs; wave w owns super-block w of all
-// 64 rows. The next tile's weights are in flight while the current one is computed; the
-// members' x records are staged once per block.
-template <int DT>
-__global__ void __launch_bounds__(512) k_gateup(const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up,
-                                                size_t stride_g, size_t stride_u, int T, int H, int F, int K,
-                                                int batch_mode, int ntile, int publish, int E, RouteBufs rb, XQBufs xq,
-                                                float* __restrict__ act) {
+template <int DT, int KIND>
+__global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk, size_t stride_e, int T, int H,
+                                                 int F, int K, int batch_mode, int publish, int E, RouteBufs rb,
+                                                 XQBufs xq, const float* __restrict__ act_in,
+                                                 float* __restrict__ out) {
   using R = LaneRow<DT>;
   __shared__ SmemMembers mem;
   __shared__ __align__(16) SmemXQ xs;
   __shared__ SmemT tv;
   const int n_ent = T * K;
-  if (publish && blockIdx.x == 0 && blockIdx.y == 0) publish_dispatch(rb.sel, n_ent, E, rb);
-  const int n_mem = members_of(rb.sel, n_ent, blockIdx.y, mem);
-  if (n_mem == 0) return;
-  const int e = mem.e;
+  const int n_in = KIND == GEMV_GATEUP ? H : F;  // row length
+  const int nb = n_in / QK;
+  const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
+  const int out_w = KIND == GEMV_GATEUP ? F : H;  // output row stride
+  if (publish && blockIdx.x == 0) publish_dispatch(rb.sel, n_ent, E, rb);
+  SelRegs sr;
+  const uint32_t mask = read_selection(rb.sel, n_ent, sr, mem);
+  const int n_units = __popc(mask) * tiles;
+  const int lo = (int)((long long)blockIdx.x * n_units / gridDim.x);
+  const int hi = (int)((long long)(blockIdx.x + 1) * n_units / gridDim.x);
+  if (lo >= hi) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nb = H / QK;
-  const int tile0 = blockIdx.x * ntile, tile1 = min(tile0 + ntile, F / 32);
-  const size_t row_bytes = (size_t)nb * R::BLOCK_BYTES;
-  const uint8_t* base = lane < 32 ? gate + (size_t)e * stride_g + (size_t)lane * row_bytes
-                                  : up + (size_t)e * stride_u + (size_t)(lane - 32) * row_bytes;
-  base += (size_t)w * R::BLOCK_BYTES;
   const bool has_blk = w < nb;
-  const float start = (batch_mode && n_mem > 1) ? 0.0f : -0.0f;
-  typename R::Loaded cur, nxt;
-  if (has_blk) R::load(cur, base + (size_t)tile0 * 32 * row_bytes);
-  const int n_chunks = (n_mem + MCH - 1) / MCH;
-  for (int tile = tile0; tile < tile1; ++tile) {
-    if (has_blk && tile + 1 < tile1) R::load(nxt, base + (size_t)(tile + 1) * 32 * row_bytes);
+  const size_t tile_bytes = (size_t)nb * R::TB_BYTES;
+  auto tile_addr = [&](int e, int tile) {
+    return wpk + (size_t)e * stride_e + (size_t)tile * tile_bytes + (size_t)w * R::TB_BYTES;
+  };
+  // stage the XQ records of members [c0, c0 + cnt) of the current list
+  auto stage = [&](int c0, int cnt) {
+    if constexpr (KIND == GEMV_GATEUP) {
+      const int nq16 = H / 16;
+      for (int idx = tid; idx < cnt * nq16; idx += 512) {
+        const int m = idx / nq16, k = idx % nq16;
+        const size_t row = mem.list[c0 + m] / K;
+        reinterpret_cast<uint4*>(xs.q[m])[k] = reinterpret_cast<const uint4*>(xq.q + row * H)[k];
+      }
+      for (int idx = tid; idx < cnt * nb * 12; idx += 512) {
+        const int m = idx / (nb * 12), k = idx % (nb * 12);
+        xs.pairs[m][k / 12][k % 12] = xq.pairs[(size_t)(mem.list[c0 + m] / K) * nb * 12 + k];
+      }
+      for (int idx = tid; idx < cnt * nb; idx += 512) {
+        const int m = idx / nb, k = idx % nb;
+        xs.sx[m][k] = xq.sx[(size_t)(mem.list[c0 + m] / K) * nb + k];
+      }
+    } else {
+      for (int task = w; task < cnt * nb; task += 8) {
+        const int m = task / nb, b = task % nb;
+        const float4 v = *reinterpret_cast<const float4*>(act_in + (size_t)mem.list[c0 + m] * F + b * QK + 4 * lane);
+        wave_quantize_xq(v, xs.q[m] + b * QK, &xs.sx[m][b], xs.pairs[m][b]);
+      }
+    }
+  };
+
+  int u = lo / tiles, tile = lo % tiles;
+  int e = nth_expert(mask, u);
+  int n_mem = member_list(sr, n_ent, e, mem);
+  typename R::Loaded L;
+  if (has_blk) R::load(L, tile_addr(e, tile));
+  if (n_mem <= MST) stage(0, n_mem);
+  __syncthreads();
+  for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
-    if (has_blk) R::prep(B, cur);
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      const int c0 = ch * MCH, cnt = min(n_mem - c0, MCH);
-      if (tile == tile0 || n_chunks > 1) {
-        stage_xq(xs, xq, H, cnt, [&](int m) { return (size_t)(mem.list[c0 + m] / K); });
+    if (has_blk) R::prep(B, L);
+    // the next unit's weights go in flight before this tile is computed
+    const bool more = unit + 1 < hi;
+    const int tile_n = tile + 1 == tiles ? 0 : tile + 1;
+    const int u_n = tile + 1 == tiles ? u + 1 : u;
+    const int e_n = u_n == u ? e : nth_expert(mask, u_n);
+    if (has_blk && more) R::load(L, tile_addr(e_n, tile_n));
+    const float start = (batch_mode && n_mem > 1) ? 0.0f : -0.0f;
+    for (int c0 = 0; c0 < n_mem; c0 += MCH) {
+      const int cnt = min(n_mem - c0, MCH);
+      int sb = c0;  // index of member c0 in xs
+      if (n_mem > MST) {
+        stage(c0, cnt);
         __syncthreads();
+        sb = 0;
       }
       if (has_blk)
-        for (int m = 0; m < cnt; ++m) tv.v[m][w][lane] = R::value(B, xs.q[m] + w * QK, xs.pairs[m][w], xs.sx[m][w]);
+        for (int m = 0; m < cnt; ++m)
+          tv.v[m][w][lane] = R::value(B, xs.q[sb + m] + w * QK, xs.pairs[sb + m][w], xs.sx[sb + m][w]);
       __syncthreads();
       for (int m = w; m < cnt; m += 8) {
         float acc = start;
         for (int b = 0; b < nb; ++b) acc += tv.v[m][b][lane];
-        const float upv = __shfl(acc, (lane + 32) & 63);
-        if (lane < 32) act[(size_t)mem.list[c0 + m] * F + tile * 32 + lane] = silu(acc) * upv;
+        const int ent = mem.list[c0 + m];
+        if constexpr (KIND == GEMV_GATEUP) {
+          const float upv = __shfl(acc, (lane + 32) & 63);
+          if (lane < 32) out[(size_t)ent * out_w + tile * 32 + lane] = silu(acc) * upv;
+        } else {
+          out[(size_t)ent * out_w + tile * 64 + lane] = acc;
+        }
       }
       __syncthreads();
     }
-    if (has_blk) cur = nxt;
+    if (more && u_n != u) {
+      e = e_n;
+      n_mem = member_list(sr, n_ent, e, mem);
+      if (n_mem <= MST) stage(0, n_mem);
+      __syncthreads();
+    }
+    u = u_n;
+    tile = tile_n;
   }
 }
 
-hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t stride_g,
-                         size_t stride_u, int T, int H, int F, int E, int K, int max_hit, int batch_mode, int publish,
-                         const RouteBufs& rb, XQBufs xq, float* act) {
-  const int tiles = F / 32;
-  const int ntile = max(1, (tiles * max_hit + GEMV_BLOCKS - 1) / GEMV_BLOCKS);
-  dim3 grid((tiles + ntile - 1) / ntile, max_hit);
+template <int KIND>
+static hipError_t launch_experts(hipStream_t s, int dtype, const uint8_t* wpk, size_t stride_e, int T, int H, int F,
+                                 int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
+                                 XQBufs xq, const float* act_in, float* out) {
+  const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
+  const int grid = min(GEMV_BLOCKS, max_hit * tiles);
   if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_gateup<DT_Q4_K>, grid, dim3(512), 0, s, gate, up, stride_g, stride_u, T, H, F, K, batch_mode,
-                       ntile, publish, E, rb, xq, act);
+    hipLaunchKernelGGL((k_experts<DT_Q4_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+                       publish, E, rb, xq, act_in, out);
   else
-    hipLaunchKernelGGL(k_gateup<DT_Q6_K>, grid, dim3(512), 0, s, gate, up, stride_g, stride_u, T, H, F, K, batch_mode,
-                       ntile, publish, E, rb, xq, act);
+    hipLaunchKernelGGL((k_experts<DT_Q6_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+                       publish, E, rb, xq, act_in, out);
   return hipGetLastError();
 }
 
-// ---- down --------------------------------------------------------------------------------------
-// Block (g, u): 64-row tiles g*ntile .. of hit expert u. The prologue quantises the members'
-// act rows (quantize_q8 per member, model.rs:530-534) straight into LDS.
-template <int DT>
-__global__ void __launch_bounds__(512) k_down(const uint8_t* __restrict__ down, size_t stride_d, int T, int H, int F,
-                                              int K, int batch_mode, int ntile, RouteBufs rb,
-                                              const float* __restrict__ act, float* __restrict__ slots) {
-  using R = LaneRow<DT>;
-  __shared__ SmemMembers mem;
-  __shared__ __align__(16) SmemXQ xs;
-  __shared__ SmemT tv;
-  const int n_mem = members_of(rb.sel, T * K, blockIdx.y, mem);
-  if (n_mem == 0) return;
-  const int e = mem.e;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nb = F / QK;
-  const int tile0 = blockIdx.x * ntile, tile1 = min(tile0 + ntile, H / 64);
-  const size_t row_bytes = (size_t)nb * R::BLOCK_BYTES;
-  const uint8_t* base = down + (size_t)e * stride_d + (size_t)lane * row_bytes + (size_t)w * R::BLOCK_BYTES;
-  const bool has_blk = w < nb;
-  const float start = (batch_mode && n_mem > 1) ? 0.0f : -0.0f;
-  typename R::Loaded cur, nxt;
-  if (has_blk) R::load(cur, base + (size_t)tile0 * 64 * row_bytes);
-  const int n_chunks = (n_mem + MCH - 1) / MCH;
-  for (int tile = tile0; tile < tile1; ++tile) {
-    if (has_blk && tile + 1 < tile1) R::load(nxt, base + (size_t)(tile + 1) * 64 * row_bytes);
-    typename R::Blk B;
-    if (has_blk) R::prep(B, cur);
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      const int c0 = ch * MCH, cnt = min(n_mem - c0, MCH);
-      if (tile == tile0 || n_chunks > 1) {
-        for (int task = w; task < cnt * nb; task += 8) {
-          const int m = task / nb, b = task % nb;
-          const float4 v = *reinterpret_cast<const float4*>(act + (size_t)mem.list[c0 + m] * F + b * QK + 4 * lane);
-          wave_quantize_xq(v, xs.q[m] + b * QK, &xs.sx[m][b], xs.pairs[m][b]);
-        }
-        __syncthreads();
-      }
-      if (has_blk)
-        for (int m = 0; m < cnt; ++m) tv.v[m][w][lane] = R::value(B, xs.q[m] + w * QK, xs.pairs[m][w], xs.sx[m][w]);
-      __syncthreads();
-      for (int m = w; m < cnt; m += 8) {
-        float acc = start;
-        for (int b = 0; b < nb; ++b) acc += tv.v[m][b][lane];
-        slots[(size_t)mem.list[c0 + m] * H + tile * 64 + lane] = acc;
-      }
-      __syncthreads();
-    }
-    if (has_blk) cur = nxt;
+hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F, int E,
+                         int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb, XQBufs xq, float* act) {
+  return launch_experts<GEMV_GATEUP>(s, dtype, gu, stride_gu, T, H, F, E, K, max_hit, batch_mode, publish, rb, xq,
+                                     nullptr, act);
+}
+
+hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,
+                       int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots) {
+  return launch_experts<GEMV_DOWN>(s, dtype, dn, stride_dn, T, H, F, 0, K, max_hit, batch_mode, 0, rb, XQBufs{}, act,
+                                   slots);
+}
+
+// ---- tile packing ------------------------------------------------------------------------------
+// One thread per 16-byte chunk (and per tail u16) of the packed output; raw blocks are only
+// 2-byte aligned (Q6_K), so the chunk is read as eight u16.
+__global__ void k_pack_rows(int dtype, const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, size_t stride_a,
+                            size_t stride_b, int rows_a, int nb, int n_exp, uint8_t* __restrict__ dst) {
+  const int NC = pack_chunks(dtype), TAIL = pack_tail(dtype);
+  const size_t TB = pack_tile_block_bytes(dtype);
+  const int blk_bytes = dtype == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+  const int tile_rows = b ? 32 : 64;
+  const int n_tiles = rows_a / tile_rows;
+  const size_t units_per_tb = (size_t)(NC + 1) * 64;  // chunk slots plus tail slots
+  const size_t total = (size_t)n_exp * n_tiles * nb * units_per_tb;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const size_t tbi = i / units_per_tb;
+  const int u = (int)(i % units_per_tb), c = u / 64, lane = u % 64;
+  const int blk = (int)(tbi % nb);
+  const size_t et = tbi / nb;
+  const int t = (int)(et % n_tiles), e = (int)(et / n_tiles);
+  const uint8_t* src;
+  if (b) src = lane < 32 ? a + (size_t)e * stride_a + (size_t)(32 * t + lane) * nb * blk_bytes
+                         : b + (size_t)e * stride_b + (size_t)(32 * t + lane - 32) * nb * blk_bytes;
+  else src = a + (size_t)e * stride_a + (size_t)(64 * t + lane) * nb * blk_bytes;
+  src += (size_t)blk * blk_bytes;
+  uint8_t* o = dst + tbi * TB;
+  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+  if (c < NC) {
+    uint16_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = s16[8 * c + k];
+    uint4 q;
+    q.x = v[0] | ((uint32_t)v[1] << 16);
+    q.y = v[2] | ((uint32_t)v[3] << 16);
+    q.z = v[4] | ((uint32_t)v[5] << 16);
+    q.w = v[6] | ((uint32_t)v[7] << 16);
+    *reinterpret_cast<uint4*>(o + 1024 * c + 16 * lane) = q;
+  } else if (TAIL) {
+    reinterpret_cast<uint16_t*>(o + 1024 * NC)[lane] = s16[8 * NC];
   }
 }
 
-hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int T, int H, int F, int K,
-                       int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots) {
-  const int tiles = H / 64;
-  const int ntile = max(1, (tiles * max_hit + GEMV_BLOCKS - 1) / GEMV_BLOCKS);
-  dim3 grid((tiles + ntile - 1) / ntile, max_hit);
-  if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_down<DT_Q4_K>, grid, dim3(512), 0, s, down, stride_d, T, H, F, K, batch_mode, ntile, rb, act,
-                       slots);
-  else
-    hipLaunchKernelGGL(k_down<DT_Q6_K>, grid, dim3(512), 0, s, down, stride_d, T, H, F, K, batch_mode, ntile, rb, act,
-                       slots);
+hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const uint8_t* b, size_t stride_a,
+                            size_t stride_b, int rows_a, int nb, int n_exp, uint8_t* dst) {
+  const int n_tiles = rows_a / (b ? 32 : 64);
+  const size_t total = (size_t)n_exp * n_tiles * nb * (pack_chunks(dtype) + 1) * 64;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_pack_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, dtype, a, b, stride_a,
+                     stride_b, rows_a, nb, n_exp, dst);
   return hipGetLastError();
 }
 

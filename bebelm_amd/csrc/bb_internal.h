@@ -63,16 +63,35 @@ constexpr int DN_F_MAX = 2048;
 // budget of the double-buffered rows); each block walks enough row tiles to cover the work.
 constexpr int GEMV_BLOCKS = 256;
 
+// Tile-packed expert rows (built once per layer by launch_pack_rows): the 64 rows of a tile and
+// one 256-weight super-block form a tile-block of NC chunks of 64 x 16 bytes, chunk c holding
+// bytes 16c..16c+15 of the block of each row (row r of the tile at lane r), followed for Q6_K
+// by the 64 rows' trailing 2 bytes (the f16 d). One 16-byte load per lane of a wave then reads
+// 1 KB of contiguous memory. Layout: [expert][tile][block][chunk][lane][16 B] (+ tail).
+// Gate/up tiles interleave the two tensors: lanes 0-31 gate rows 32t.., lanes 32-63 up rows.
+constexpr int TILE_ROWS = 64;
+__host__ __device__ constexpr int pack_chunks(int dt) { return dt == 12 ? 9 : 13; }
+__host__ __device__ constexpr int pack_tail(int dt) { return dt == 12 ? 0 : 2; }
+__host__ __device__ constexpr size_t pack_tile_block_bytes(int dt) {
+  return (size_t)pack_chunks(dt) * 1024 + (size_t)pack_tail(dt) * TILE_ROWS;
+}
+
+// Packs n_exp experts of raw GGUF rows (a, and b for the interleaved gate/up form; b null for
+// plain tiles of 64 rows of a) into dst. stride_a/b: raw bytes per expert; rows_a: rows per
+// expert of a; nb: super-blocks per row.
+hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const uint8_t* b, size_t stride_a,
+                            size_t stride_b, int rows_a, int nb, int n_exp, uint8_t* dst);
+
 hipError_t launch_route(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H, int E,
                         int K, XQBufs xq, RouteBufs rb);
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc);
 
-hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t stride_g,
-                         size_t stride_u, int T, int H, int F, int E, int K, int max_hit, int batch_mode, int publish,
-                         const RouteBufs& rb, XQBufs xq, float* act);
+// gu / dn: tile-packed gate+up and down tensors; stride_*: packed bytes per expert.
+hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F, int E,
+                         int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb, XQBufs xq, float* act);
 
-hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* down, size_t stride_d, int T, int H, int F, int K,
+hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,
                        int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots);
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out);

@@ -18,11 +18,11 @@
 #ifndef BB_ROWLANE_H
 #define BB_ROWLANE_H
 #include "bb_device.h"
+#include "bb_internal.h"
 
 namespace bb {
 
 typedef short v2s __attribute__((ext_vector_type(2)));
-typedef uint4 uint4_a4 __attribute__((aligned(4)));
 
 __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, a), __builtin_bit_cast(v2s, b), c, false);
@@ -71,9 +71,12 @@ struct Q4Blk {
   float d, dmin;
 };
 
-__device__ __forceinline__ void q4_load(uint4 (&w)[9], const uint8_t* __restrict__ blk) {
+// tb: the tile-block (tile-packed layout); chunk k of this lane's row block is at
+// tb + 1024k + 16·lane, so each load of the wave reads 1 KB of contiguous memory.
+__device__ __forceinline__ void q4_load(uint4 (&w)[9], const uint8_t* __restrict__ tb) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 0; k < 9; ++k) w[k] = reinterpret_cast<const uint4*>(blk)[k];
+  for (int k = 0; k < 9; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * lane);
 }
 
 // get_scale_min_k4 (dequant.rs:64-72) on four bytes at a time, then the nibble unpack
@@ -138,39 +141,32 @@ __device__ __forceinline__ float q4_value(const Q4Blk& B, const int8_t* __restri
 }
 
 // ---- Q6_K row block ----------------------------------------------------------------------------
-// Blocks are 2-byte aligned (210 B): 14 dword-aligned 16-byte loads, then a funnel shift.
 struct Q6Blk {
-  uint32_t q[64];  // 6-bit quants 0..63 in element order (dword i = elements 4i..4i+3)
-  int sc[16];
+  uint32_t q[64];   // 6-bit quants 0..63 in element order (dword i = elements 4i..4i+3)
+  uint32_t sc4[4];  // the 16 i8 scales, four per dword
   uint32_t scp[8];  // i8 scales as int16 pairs (sc4i, sc4i+2), (sc4i+1, sc4i+3)
   float d;
 };
 
-__device__ __forceinline__ void q6_load(uint4 (&w)[14], const uint8_t* __restrict__ blk, uint32_t& shift) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(blk);
-  const uint4_a4* p = reinterpret_cast<const uint4_a4*>(a & ~uintptr_t(3));
-  shift = (uint32_t)(a & 3);
+// Bytes 0..207 of the block (ql, qh, scales) in 13 chunks, then the f16 d from the tail.
+__device__ __forceinline__ void q6_load(uint4 (&w)[13], uint32_t& dbits, const uint8_t* __restrict__ tb) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int k = 0; k < 14; ++k) {
-    const uint4_a4 v = p[k];
-    w[k] = make_uint4(v.x, v.y, v.z, v.w);
-  }
+  for (int k = 0; k < 13; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * lane);
+  dbits = *reinterpret_cast<const uint16_t*>(tb + 13 * 1024 + 2 * lane);
 }
 
 // dequant.rs:122-138 / matmul.rs:496-525: element 128n + 32g + l takes the low (g<2) or high
 // nibble of ql[64n + 32(g&1) + l] and bits 2g..2g+1 of qh[32n + l].
-__device__ __forceinline__ void q6_prep(Q6Blk& B, const uint4 (&w)[14], uint32_t shift) {
-  uint32_t raw[56];
+__device__ __forceinline__ void q6_prep(Q6Blk& B, const uint4 (&w)[13], uint32_t dbits) {
+  uint32_t bd[52];  // block dwords
 #pragma unroll
-  for (int k = 0; k < 14; ++k) {
-    raw[4 * k] = w[k].x;
-    raw[4 * k + 1] = w[k].y;
-    raw[4 * k + 2] = w[k].z;
-    raw[4 * k + 3] = w[k].w;
+  for (int k = 0; k < 13; ++k) {
+    bd[4 * k] = w[k].x;
+    bd[4 * k + 1] = w[k].y;
+    bd[4 * k + 2] = w[k].z;
+    bd[4 * k + 3] = w[k].w;
   }
-  uint32_t bd[53];  // block dwords
-#pragma unroll
-  for (int j = 0; j < 53; ++j) bd[j] = __builtin_amdgcn_alignbyte(raw[j + 1], raw[j], shift);
 #pragma unroll
   for (int i = 0; i < 64; ++i) {
     const int n = i >> 5, g = (i & 31) >> 3, k = i & 7;
@@ -182,16 +178,13 @@ __device__ __forceinline__ void q6_prep(Q6Blk& B, const uint4 (&w)[14], uint32_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t s = bd[48 + i];
+    B.sc4[i] = s;
     const int s0 = (int)(int8_t)(s & 0xff), s1 = (int)(int8_t)((s >> 8) & 0xff);
     const int s2 = (int)(int8_t)((s >> 16) & 0xff), s3 = (int)(int8_t)(s >> 24);
-    B.sc[4 * i] = s0;
-    B.sc[4 * i + 1] = s1;
-    B.sc[4 * i + 2] = s2;
-    B.sc[4 * i + 3] = s3;
     B.scp[2 * i] = pack16(s0, s2);
     B.scp[2 * i + 1] = pack16(s1, s3);
   }
-  B.d = f16_bits_to_f32(bd[52] & 0xffff);
+  B.d = f16_bits_to_f32(dbits);
 }
 
 // s = Σ_k sc_k·Σ_{i∈k}(q_i − 32)·x_i = Σ_k sc_k·D_k − 32·Σ_k sc_k·T_k (exact; matmul.rs:692-742).
@@ -205,7 +198,7 @@ __device__ __forceinline__ float q6_value(const Q6Blk& B, const int8_t* __restri
     dk = __builtin_amdgcn_sdot4((int)B.q[4 * k + 1], (int)x.y, dk, false);
     dk = __builtin_amdgcn_sdot4((int)B.q[4 * k + 2], (int)x.z, dk, false);
     dk = __builtin_amdgcn_sdot4((int)B.q[4 * k + 3], (int)x.w, dk, false);
-    s += B.sc[k] * dk;
+    s += (int)(int8_t)(B.sc4[k >> 2] >> (8 * (k & 3))) * dk;
   }
   int corr = 0;
 #pragma unroll
@@ -214,14 +207,13 @@ __device__ __forceinline__ float q6_value(const Q6Blk& B, const int8_t* __restri
   return sx * (B.d * (float)s);
 }
 
-// Policy wrappers used by the kernels.
+// Policy wrappers used by the kernels; load() takes the tile-block address.
 template <int DT>
 struct LaneRow;
 
 template <>
 struct LaneRow<DT_Q4_K> {
-  static constexpr int BLOCK_BYTES = Q4K_BYTES;
-  using Raw = uint4[9];
+  static constexpr size_t TB_BYTES = pack_tile_block_bytes(DT_Q4_K);
   using Blk = Q4Blk;
   struct Loaded {
     uint4 w[9];
@@ -235,14 +227,14 @@ struct LaneRow<DT_Q4_K> {
 
 template <>
 struct LaneRow<DT_Q6_K> {
-  static constexpr int BLOCK_BYTES = Q6K_BYTES;
+  static constexpr size_t TB_BYTES = pack_tile_block_bytes(DT_Q6_K);
   using Blk = Q6Blk;
   struct Loaded {
-    uint4 w[14];
-    uint32_t shift;
+    uint4 w[13];
+    uint32_t dbits;
   };
-  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* blk) { q6_load(L.w, blk, L.shift); }
-  static __device__ __forceinline__ void prep(Blk& B, const Loaded& L) { q6_prep(B, L.w, L.shift); }
+  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* tb) { q6_load(L.w, L.dbits, tb); }
+  static __device__ __forceinline__ void prep(Blk& B, const Loaded& L) { q6_prep(B, L.w, L.dbits); }
   static __device__ __forceinline__ float value(const Blk& B, const int8_t* xq, const uint32_t* pairs, float sx) {
     return q6_value(B, xq, pairs, sx);
   }

@@ -127,7 +127,8 @@ int bb_rmsnorm(bb_ctx* ctx, const float* x, const float* gain, float eps, size_t
 /* Tensors as Model::moe_ffn resolves them (model.rs:474-478): router `ffn_gate_inp` F32
  * [hidden, E]; `exp_probs_b` f32[E] (host); stacked experts gate/up [hidden, ff, E] and
  * down [ff, hidden, E] in Q4_K or Q6_K. Requires E <= 32, k <= 8, hidden and ff multiples
- * of 256. */
+ * of 256. The layer keeps its own device copies of the router and experts, regrouped for
+ * coalesced loads (same bytes, other order); the tensors may be freed after this call. */
 int bb_moe_create(bb_ctx* ctx, const bb_tensor* router, const float* exp_probs_b, const bb_tensor* gate_exps,
                   const bb_tensor* up_exps, const bb_tensor* down_exps, int n_used, bb_moe** out);
 int bb_moe_destroy(bb_moe* moe);
