@@ -54,6 +54,7 @@ _SIGS = {
     "bb_kernel_count": (c_int, []),
     "bb_ctx_kernel_stats": (c_int, [c_void_p, c_int, P(ctypes.c_char_p), P(ctypes.c_double), P(ctypes.c_int64)]),
     "bb_ctx_reset_stats": (c_int, [c_void_p]),
+    "bb_ctx_set_batched_min_entries": (c_int, [c_void_p, c_size_t]),
     "bb_tensor_upload": (c_int, [c_void_p, c_uint32, c_void_p, c_size_t, P(ctypes.c_uint64), c_int, P(c_void_p)]),
     "bb_tensor_free": (c_int, [c_void_p]),
     "bb_tensor_device_ptr": (c_int, [c_void_p, P(c_void_p)]),

@@ -5,6 +5,8 @@ The library is the product: a C-ABI shared object (include/bebelm_moe.h). Flags:
                                             reference's rounding sequence
   -fhip-fp32-correctly-rounded-divide-sqrt  IEEE f32 divide / sqrt (sigmoid, renorm, rmsnorm)
   -target-feature -packed-fp32-ops          no packed-FP32 instructions on this hardware pool
+  -amdgpu-mfma-vgpr-form                    MFMA results in VGPRs (the GEMM epilogues read them
+                                            with VALU; no accumulator-register copies)
 """
 import os
 import subprocess
@@ -13,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbebelm_moe.so")
-SOURCES = ["bb_kernels.hip", "bb_decode.hip", "bb_gemm.hip", "bb_api.hip"]
+SOURCES = ["bb_kernels.hip", "bb_decode.hip", "bb_prefill.hip", "bb_api.hip"]
 ARCH = os.environ.get("BB_OFFLOAD_ARCH", "gfx950")
 
 
@@ -34,6 +36,7 @@ def flags():
         "-ffp-contract=off",
         "-fhip-fp32-correctly-rounded-divide-sqrt",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-Wall",
         "-Wno-unused-function",
     ]

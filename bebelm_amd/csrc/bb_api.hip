@@ -94,6 +94,7 @@ struct bb_ctx {
   std::vector<hipEvent_t> event_pool;
   double kernel_ms[bb::K_COUNT] = {};
   int64_t launches[bb::K_COUNT] = {};
+  size_t batched_min_entries = 129;  // T*k from which MoE calls take the grouped-GEMM path
 };
 
 struct bb_tensor {
@@ -239,16 +240,18 @@ struct MoeWs {
   bb::RouteBufs rb;
   float* act;
   float* slots;
+  int8_t* aq;     // Q8 of act (batched path)
+  float* aq_sx;
 };
 
-MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
+MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched) {
   const size_t H = m->H, F = m->F, E = m->E, K = m->K;
   for (int pass = 0; pass < 2; ++pass) {
     Carve cv{pass ? c->ws : nullptr};
-    MoeWs w;
+    MoeWs w{};
     w.xq.q = cv.take<int8_t>(T * H);
     w.xq.sx = cv.take<float>(T * H / 256);
-    w.xq.pairs = cv.take<uint32_t>(T * H / 256 * 12);
+    w.xq.pairs = batched ? nullptr : cv.take<uint32_t>(T * H / 256 * 12);
     w.rb.logits = cv.take<float>(T * E);
     w.rb.sel = cv.take<int32_t>(T * K);
     w.rb.wts = cv.take<float>(T * K);
@@ -260,30 +263,55 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T) {
     w.rb.margin = cv.take<float>(T);
     w.act = cv.take<float>(T * K * F);
     w.slots = cv.take<float>(T * K * H);
+    if (batched) {
+      w.aq = cv.take<int8_t>(T * K * F);
+      w.aq_sx = cv.take<float>(T * K * F / 256);
+    }
     if (pass == 0) ensure_ws(c, cv.off);
     else return w;
   }
   return {};
 }
 
-
 void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr) {
   need(T >= 1, BB_ERR_ARG, "T must be >= 1");
-  need(T * (size_t)m->K <= (size_t)bb::MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
-  MoeWs w = carve_moe(c, m, T);
-  const int batch_mode = T > 1;
-  const int max_hit = (int)std::min<size_t>((size_t)m->E, T * m->K);
-  launch(c, bb::K_ROUTE, [&] {
-    return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, w.xq, w.rb);
-  });
-  launch(c, bb::K_GATEUP, [&] {
-    return bb::launch_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
-                             max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
-  });
-  launch(c, bb::K_DOWN, [&] {
-    return bb::launch_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->K, max_hit,
-                           batch_mode, w.rb, w.act, w.slots);
-  });
+  const size_t n_ent = T * (size_t)m->K;
+  const bool batched = n_ent >= c->batched_min_entries;
+  if (batched)
+    need(n_ent <= (size_t)bb::PF_MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 32768 (token, slot) entries per call");
+  else
+    need(n_ent <= (size_t)bb::MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
+  MoeWs w = carve_moe(c, m, T, batched);
+  if (batched) {
+    // model.rs:286-371: route all tokens, group entries by expert, grouped GEMMs, combine
+    launch(c, bb::K_ROUTE_LARGE, [&] {
+      return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 16, w.xq, w.rb);
+    });
+    launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
+    launch(c, bb::K_GEMM_GATEUP, [&] {
+      return bb::launch_gemm_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
+                                    w.rb, bb::GemmX{w.xq.q, w.xq.sx}, w.act);
+    });
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, w.act, n_ent, m->F, w.aq, w.aq_sx); });
+    launch(c, bb::K_GEMM_DOWN, [&] {
+      return bb::launch_gemm_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->E, m->K,
+                                  w.rb, bb::GemmX{w.aq, w.aq_sx}, w.slots);
+    });
+  } else {
+    const int batch_mode = T > 1;
+    const int max_hit = (int)std::min<size_t>((size_t)m->E, n_ent);
+    launch(c, bb::K_ROUTE, [&] {
+      return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 1, w.xq, w.rb);
+    });
+    launch(c, bb::K_GATEUP, [&] {
+      return bb::launch_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
+                               max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
+    });
+    launch(c, bb::K_DOWN, [&] {
+      return bb::launch_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->K, max_hit,
+                             batch_mode, w.rb, w.act, w.slots);
+    });
+  }
   launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
   if (tr) {
     const size_t E = m->E, K = m->K;
@@ -516,6 +544,13 @@ int bb_ctx_reset_stats(bb_ctx* c) {
       c->kernel_ms[i] = 0;
       c->launches[i] = 0;
     }
+  });
+}
+
+int bb_ctx_set_batched_min_entries(bb_ctx* c, size_t min_entries) {
+  return guard([&] {
+    need_ctx(c);
+    c->batched_min_entries = min_entries;
   });
 }
 

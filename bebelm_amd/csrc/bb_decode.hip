@@ -19,97 +19,109 @@
 
 namespace bb {
 
-// ---- router + gating + XQ of x, one block per token -------------------------------------------
-// Block t (1024 threads): lane (e = tid/32, c = tid%32) runs fmaf chain c of router row e
-// (matmul.rs:36-66: chains i = c mod 32, lane combine (acc0+acc1)+(acc2+acc3), reduce_add
-// ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7))). The router is held chain-major (Wc[e][c][m] =
-// W[e][32m+c], built once per layer) so each lane reads its chain as contiguous float4s; x is
-// staged in LDS. Then one half-wave does the gating of model.rs:485-495 (sigmoid, rank of
-// score+bias by total_cmp with lower index first on exact ties, renormalisation), and waves
-// quantise x into its XQ record (model.rs:501).
+// ---- router + gating + XQ of x ------------------------------------------------------------------
+// Block of 1024 threads for tpb consecutive tokens: lane (e = tid/32, c = tid%32) runs fmaf
+// chain c of router row e (matmul.rs:36-66: chains i = c mod 32, lane combine
+// (acc0+acc1)+(acc2+acc3), reduce_add ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7))). The router is held
+// regrouped by chain (built once per layer) and read once per block into registers; each
+// token's x is staged in LDS (the next one prefetched) and quantised into its XQ record
+// (model.rs:501; the pair dwords only when xq.pairs is set). Then half-wave i gates token i
+// (model.rs:485-495): sigmoid, rank of score+bias by total_cmp with the lower index first on
+// exact ties, renormalisation.
+constexpr int ROUTE_TPB_MAX = 16;
+
 __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, const float* __restrict__ bias,
-                                                const float* __restrict__ x, int H, int E, int K, XQBufs xq,
-                                                RouteBufs rb) {
+                                                const float* __restrict__ x, int T, int H, int E, int K, int tpb,
+                                                XQBufs xq, RouteBufs rb) {
   __shared__ __align__(16) float xs[GU_H_MAX];
-  __shared__ float lg[32];
-  __shared__ int32_t s_key[32];
-  __shared__ float s_rank_s[8];
-  __shared__ int32_t s_rank_e[8];
-  __shared__ float s_rank_key[9];
-  const int t = blockIdx.x;
+  __shared__ float lg[ROUTE_TPB_MAX][32];
+  __shared__ int32_t s_key[ROUTE_TPB_MAX][32];
+  __shared__ float s_rank_s[ROUTE_TPB_MAX][8];
+  __shared__ int32_t s_rank_e[ROUTE_TPB_MAX][8];
+  __shared__ float s_rank_key[ROUTE_TPB_MAX][9];
+  const int t0 = blockIdx.x * tpb, nt = min(tpb, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int e = tid >> 5, c = tid & 31;
   const int nm = H / 32;
-  // issue this lane's chain operands first; they are independent of everything below
+  // this lane's chain operands, independent of everything below
   float4 wv[GU_H_MAX / 32 / 4];
   const float4* wr = reinterpret_cast<const float4*>(Wc) + (size_t)(e < E ? e : 0) * nm / 4 * 32 + c;
 #pragma unroll
   for (int k = 0; k < GU_H_MAX / 32 / 4; ++k)
     if (k < nm / 4) wv[k] = wr[32 * k];
-  const float* xr = x + (size_t)t * H;
-  for (int i = tid; i < H / 4; i += 1024) reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(xr)[i];
-  __syncthreads();
+  const int nq = H / 4;  // float4 per token (<= 512 < 1024 threads)
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4 xr = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tid < nq) xr = x4[(size_t)t0 * nq + tid];
   const int nbx = H / QK;
-  if (wave < nbx) {
-    const float4 v = reinterpret_cast<const float4*>(xs + wave * QK)[lane];
-    wave_quantize_xq(v, xq.q + (size_t)t * H + wave * QK, xq.sx + (size_t)t * nbx + wave,
-                     xq.pairs + ((size_t)t * nbx + wave) * 12);
-  }
-  float acc = 0.0f;
-#pragma unroll
-  for (int k = 0; k < GU_H_MAX / 32 / 4; ++k) {
-    if (k < nm / 4) {
-      acc = fmaf(wv[k].x, xs[32 * (4 * k + 0) + c], acc);
-      acc = fmaf(wv[k].y, xs[32 * (4 * k + 1) + c], acc);
-      acc = fmaf(wv[k].z, xs[32 * (4 * k + 2) + c], acc);
-      acc = fmaf(wv[k].w, xs[32 * (4 * k + 3) + c], acc);
+  for (int i = 0; i < nt; ++i) {
+    const int t = t0 + i;
+    if (tid < nq) reinterpret_cast<float4*>(xs)[tid] = xr;
+    __syncthreads();
+    if (i + 1 < nt && tid < nq) xr = x4[(size_t)(t + 1) * nq + tid];
+    if (wave < nbx) {
+      const float4 v = reinterpret_cast<const float4*>(xs + wave * QK)[lane];
+      wave_quantize_xq(v, xq.q + (size_t)t * H + wave * QK, xq.sx + (size_t)t * nbx + wave,
+                       xq.pairs ? xq.pairs + ((size_t)t * nbx + wave) * 12 : nullptr);
     }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < GU_H_MAX / 32 / 4; ++k) {
+      if (k < nm / 4) {
+        acc = fmaf(wv[k].x, xs[32 * (4 * k + 0) + c], acc);
+        acc = fmaf(wv[k].y, xs[32 * (4 * k + 1) + c], acc);
+        acc = fmaf(wv[k].z, xs[32 * (4 * k + 2) + c], acc);
+        acc = fmaf(wv[k].w, xs[32 * (4 * k + 3) + c], acc);
+      }
+    }
+    const float A = acc + __shfl_down(acc, 8, 32);
+    const float v = A + __shfl_down(A, 16, 32);
+    const float u = v + __shfl_down(v, 4, 32);
+    const float y = u + __shfl_down(u, 2, 32);
+    const float r = y + __shfl_down(y, 1, 32);
+    if (c == 0 && e < E) {
+      lg[i][e] = r;
+      rb.logits[(size_t)t * E + e] = r;
+    }
+    __syncthreads();
   }
-  const float A = acc + __shfl_down(acc, 8, 32);
-  const float v = A + __shfl_down(A, 16, 32);
-  const float u = v + __shfl_down(v, 4, 32);
-  const float y = u + __shfl_down(u, 2, 32);
-  const float r = y + __shfl_down(y, 1, 32);
-  if (c == 0 && e < E) {
-    lg[e] = r;
-    rb.logits[(size_t)t * E + e] = r;
-  }
-  __syncthreads();
-  if (tid < 32) {
+  const int i = tid >> 5;  // half-wave i gates token t0 + i
+  if (i < nt) {
+    const int t = t0 + i;
     const bool live = c < E;
-    const float s = live ? sigmoid(lg[c]) : 0.0f;
+    const float s = live ? sigmoid(lg[i][c]) : 0.0f;
     const float key = live ? s + bias[c] : 0.0f;
     const int32_t kk = total_key(key);
-    if (live) s_key[c] = kk;
+    if (live) s_key[i][c] = kk;
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     int rank = 0, eq_after = 0;
     if (live) {
       for (int j = 0; j < E; ++j) {
-        const int32_t kj = s_key[j];
+        const int32_t kj = s_key[i][j];
         rank += (kj > kk) || (kj == kk && j < c);
         eq_after += (kj == kk && j > c);
       }
     }
     if (live && rank < K) {
-      s_rank_s[rank] = s;
-      s_rank_e[rank] = c;
+      s_rank_s[i][rank] = s;
+      s_rank_e[i][rank] = c;
     }
-    if (live && rank <= K) s_rank_key[rank] = key;
+    if (live && rank <= K) s_rank_key[i][rank] = key;
     const int tie = (live && rank < K && eq_after > 0) ? 1 : 0;
-    const unsigned long long tm = __ballot(tie);
+    const uint32_t tm = (uint32_t)(__ballot(tie) >> (lane & 32));
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
     if (c == 0) {
       float denom = -0.0f;
-      for (int k = 0; k < K; ++k) denom += s_rank_s[k];
+      for (int k = 0; k < K; ++k) denom += s_rank_s[i][k];
       denom = denom + 1e-6f;
       for (int k = 0; k < K; ++k) {
-        rb.sel[(size_t)t * K + k] = s_rank_e[k];
-        rb.wts[(size_t)t * K + k] = s_rank_s[k] / denom;
+        rb.sel[(size_t)t * K + k] = s_rank_e[i][k];
+        rb.wts[(size_t)t * K + k] = s_rank_s[i][k] / denom;
       }
-      rb.margin[t] = K < E ? s_rank_key[K - 1] - s_rank_key[K] : __builtin_inff();
-      rb.ties[t] = __popcll(tm);
+      rb.margin[t] = K < E ? s_rank_key[i][K - 1] - s_rank_key[i][K] : __builtin_inff();
+      rb.ties[t] = __popc(tm);
     }
   }
 }
@@ -130,8 +142,9 @@ hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E
 }
 
 hipError_t launch_route(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H, int E,
-                        int K, XQBufs xq, RouteBufs rb) {
-  hipLaunchKernelGGL(k_route, dim3(T), dim3(1024), 0, s, router, bias, x, H, E, K, xq, rb);
+                        int K, int tpb, XQBufs xq, RouteBufs rb) {
+  tpb = max(1, min(tpb, ROUTE_TPB_MAX));
+  hipLaunchKernelGGL(k_route, dim3((T + tpb - 1) / tpb), dim3(1024), 0, s, router, bias, x, T, H, E, K, tpb, xq, rb);
   return hipGetLastError();
 }
 

@@ -82,8 +82,9 @@ __host__ __device__ constexpr size_t pack_tile_block_bytes(int dt) {
 hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const uint8_t* b, size_t stride_a,
                             size_t stride_b, int rows_a, int nb, int n_exp, uint8_t* dst);
 
+// tpb tokens per block (the router is read once per block); xq.pairs may be null.
 hipError_t launch_route(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H, int E,
-                        int K, XQBufs xq, RouteBufs rb);
+                        int K, int tpb, XQBufs xq, RouteBufs rb);
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc);
 
@@ -93,6 +94,29 @@ hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t str
 
 hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,
                        int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots);
+
+// ---- batched (prefill) path ----------------------------------------------------------------------
+// Largest T*k of one call on this path (the dispatch keeps per-64-entry counts in LDS).
+constexpr int PF_MAX_ENTRIES = 32768;
+
+// counts/offsets/perm/hit of rb from sel (stable grouping, model.rs:316-322).
+hipError_t launch_dispatch(hipStream_t s, int n_ent, int E, const RouteBufs& rb);
+
+// Grouped expert GEMM over the members of each expert (int8 MFMA with exact integer
+// sub-dots and the reference's f32 per-block epilogue).
+//   gate/up: x = XQ records of the members' tokens, out = act in group order [pos][F].
+//   down:    x = Q8 of act in group order, out = slots[entry][H].
+struct GemmX {
+  const int8_t* q;  // Q8 rows
+  const float* sx;  // per-256 scales of the rows
+};
+hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
+                              int E, int K, const RouteBufs& rb, GemmX x, float* act);
+hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
+                            int K, const RouteBufs& rb, GemmX x, float* slots);
+
+// Q8 rows (quants and per-256 scales only) of n_rows vectors of n floats.
+hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx);
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out);
 

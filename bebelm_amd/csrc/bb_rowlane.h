@@ -59,7 +59,7 @@ __device__ __forceinline__ void wave_quantize_xq(float4 v, int8_t* __restrict__ 
   }
   const int a32 = __shfl(s32, srcA), b32 = __shfl(s32, srcB);
   const int a16 = __shfl(t16, srcA), b16 = __shfl(t16, srcB);
-  if (lane < 12) pairs[lane] = wide ? pack16(a32, b32) : pack16(a16, b16);
+  if (pairs && lane < 12) pairs[lane] = wide ? pack16(a32, b32) : pack16(a16, b16);
   if (lane == 0) *sx = amax / 127.0f;
 }
 

@@ -72,6 +72,10 @@ class Context:
     def reset_stats(self):
         check(lib().bb_ctx_reset_stats(self.handle))
 
+    def set_batched_min_entries(self, n):
+        """MoE calls with T*k >= n take the grouped-GEMM (batched) kernels."""
+        check(lib().bb_ctx_set_batched_min_entries(self.handle, int(n)))
+
     def kernel_stats(self):
         """{kernel name: (total ms, launches)} for kernels launched while profiling."""
         out = {}

@@ -3,15 +3,19 @@
 Default workload: BASELINE.json config 2. That is a decode batch of 16 independent tokens
 through one sparse-MoE block of LFM2.5-8B-A1B's shape (hidden 2048, expert FFN 1792, 32
 experts, top-4, Q4_K experts with Q8 activations). A step is one pass of the hot path over one
-batch: router, gating, dispatch, gate/up + SwiGLU, down + combine.
+batch: router, gating, dispatch, gate/up + SwiGLU, down, combine. `--config 1|3|4` runs the
+other single-block configurations (3 and 4 take the batched path: dispatch and grouped int8-MFMA
+GEMMs), `--config 5` the 24-layer FFN stack at one token.
 
-The 256 MB Infinity Cache would hold one layer's 198 MB of experts, so step i runs layer
-i mod L of L independently generated layers (L = 12 by default, 2.4 GB), as successive layers
-of a real model would. Inputs are resident in HBM before the timed region.
+The 256 MB Infinity Cache would hold one layer's 198-228 MB of experts, so for configs 1-4 step
+i runs layer i mod L of L independently generated layers (L = 12 by default, 2.4-2.7 GB), as
+successive layers of a real model would; config 5 holds its ~5 GB of layers resident. Inputs are
+resident in HBM before the timed region.
 
 The output is one JSON line with `value` in tok/s. It also carries:
-  roofline      the dominant kernel's algorithmic bytes per launch divided by its mean launch
-                time, measured with HIP events on the stream it runs on
+  roofline      the dominant kernel's algorithmic bytes (decode, config 3) or operations
+                (config 4) per launch divided by its mean launch time, measured with HIP events
+                on the stream the kernels run on, against MI355X's 8 TB/s or int8 MFMA peak
   cpu_baseline  the reference path (its C++ restatement, OpenMP over output rows as the
                 reference's rayon does) timed on this host on a bounded sample
 """
@@ -27,14 +31,18 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (the north-star prefill target's yardstick)
+
+DECODE_KERNELS = ("gateup_swiglu", "down_combine")
+GEMM_KERNELS = ("gemm_gateup", "gemm_down")
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--layers", type=int, default=12, help="distinct weight sets rotated across steps")
     ap.add_argument("--seed", type=int, default=0)
@@ -43,23 +51,37 @@ def parse():
     return ap.parse_args()
 
 
-def algorithmic_bytes(w, counts, T):
-    """Per-kernel and per-step algorithmic bytes for one MoE layer (no intermediates/re-reads)."""
+def q8_bytes(n):
+    return n + n // 256 * 4
+
+
+def layer_work(w, counts, T, batched):
+    """Algorithmic bytes and int8 operations per kernel launch of one MoE layer.
+
+    Bytes: weights of the hit experts (each read once), activations in, results out; no
+    intermediates re-read. Operations: 2 per multiply-add of the expert GEMMs."""
     from bebelm_amd import synth
 
     H, F, K = w.hidden, w.moe_ff, w.n_used
+    n_ent = T * K
     u_hit = int(np.count_nonzero(counts))
     gu = synth.byte_size(w.gate_dtype, H * F) + synth.byte_size(w.up_dtype, H * F)
     dn = synth.byte_size(w.down_dtype, F * H)
-    q8 = lambda n: n + n // 256 * 4 + n // 32 * 4  # noqa: E731
-    gateup = u_hit * gu + T * q8(H) + T * K * (F * 4 + q8(F))      # weights + x_q8 in, act (+q8) out
-    down = u_hit * dn + T * K * q8(F) + T * H * 4 + T * K * H * 4  # weights + act_q8 in, out + slots
-    route = w.router.nbytes + T * H * 4 + T * q8(H)
-    step = u_hit * (gu + dn) + w.router.nbytes + T * H * 4 * 2      # SURVEY 8(d) block figure
-    return {"gateup_swiglu": gateup, "down_combine": down, "route_small": route, "step": step, "u_hit": u_hit}
+    gate_b = u_hit * gu + T * q8_bytes(H) + n_ent * F * 4
+    down_b = u_hit * dn + n_ent * (F * 4 if not batched else q8_bytes(F)) + n_ent * H * 4
+    gate_ops = 2.0 * n_ent * 2 * F * H
+    down_ops = 2.0 * n_ent * F * H
+    names = GEMM_KERNELS if batched else DECODE_KERNELS
+    return {
+        names[0]: (gate_b, gate_ops),
+        names[1]: (down_b, down_ops),
+        "step_bytes": u_hit * (gu + dn) + w.router.nbytes + T * H * 4 * 2,
+        "u_hit": u_hit,
+        "ops": gate_ops + down_ops,
+    }
 
 
-def cpu_baseline(layers, x, T, seconds):
+def cpu_baseline(run_one, T, seconds, what):
     from oracle import bbo
 
     try:
@@ -68,22 +90,16 @@ def cpu_baseline(layers, x, T, seconds):
         cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     bbo.set_threads(cores)
-    xs = x.reshape(-1)
     calls = 0
     t0 = time.perf_counter()
     while True:
-        w = layers[calls % len(layers)]
-        if T == 1:
-            bbo.moe_ffn(w, xs)
-        else:
-            bbo.moe_ffn_batch(w, xs, T)
+        run_one(calls)
         calls += 1
         el = time.perf_counter() - t0
         if el >= seconds or calls >= 1000:
             break
     return {"value": calls * T / el, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{calls} calls of the C++ restatement of moe_ffn{'_batch' if T > 1 else ''} "
-                      f"(T={T}, {len(layers)} rotated layers) in {el:.1f} s, OpenMP over output rows"}
+            "sample": f"{calls} calls of the C++ restatement of {what} in {el:.1f} s, OpenMP over output rows"}
 
 
 def main():
@@ -94,93 +110,171 @@ def main():
     import torch
 
     from bebelm_amd import synth
-    from bebelm_amd.model import Context, MoeLayer, RouteTrace
+    from bebelm_amd.model import Context, DenseLayer, FfnStack, MoeLayer, RouteTrace
 
     cfg = synth.CONFIGS[args.config]
-    if args.config == 5:
-        print("config 5 is measured by bench_stack in DESIGN notes; use --config 1..4 here", file=sys.stderr)
-        sys.exit(2)
     T = cfg.tokens
-    L = max(1, args.layers)
+    prefill = args.config in (3, 4)
+    steps = args.steps if args.steps is not None else (20 if args.config == 4 else 200)
+    warmup = args.warmup if args.warmup is not None else (3 if args.config == 4 else 20)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     ctx = Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    batched = T * 4 >= 129
 
     t_gen = time.perf_counter()
-    weights = [synth.config_layer(args.config, seed=args.seed, layer=l) for l in range(L)]
-    layers = [MoeLayer(ctx, w) for w in weights]
     x_host = synth.hidden_states(args.seed, T)
     x = torch.from_numpy(x_host).to(dev)
     out = torch.empty_like(x)
+    if args.config == 5:
+        spec = synth.stack_layers(seed=args.seed)
+        built = [(g, MoeLayer(ctx, w) if isinstance(w, synth.MoeWeights) else DenseLayer(ctx, w)) for g, w in spec]
+        stack = FfnStack(ctx, built)
+        moe_w = [w for _, w in spec if isinstance(w, synth.MoeWeights)]
+        dense_w = [w for _, w in spec if not isinstance(w, synth.MoeWeights)]
+        units = [stack]
+        weight_bytes = int(sum(w.nbytes for _, w in spec))
+        L = 1
+    else:
+        L = max(1, args.layers)
+        weights = [synth.config_layer(args.config, seed=args.seed, layer=l) for l in range(L)]
+        units = [MoeLayer(ctx, w) for w in weights]
+        weight_bytes = int(sum(w.nbytes for w in weights))
     t_gen = time.perf_counter() - t_gen
 
-    # data-dependent hit counts per layer (for the algorithmic byte counts)
-    per_layer = []
-    for w, layer in zip(weights, layers):
-        tr = RouteTrace(T, w.n_experts, w.n_used)
-        layer.forward(np.ascontiguousarray(x_host.reshape(-1)), T, np.empty(T * w.hidden, np.float32), tr)
-        per_layer.append(algorithmic_bytes(w, tr.counts, T))
+    # data-dependent hit counts (for the algorithmic byte counts)
+    if args.config == 5:
+        per_layer = [None]
+        xs = x_host.reshape(-1).copy()
+        from oracle import bbo
+        # routing of every MoE layer of the stack for this token, from the CPU restatement's trace
+        layers_work = []
+        h = xs.copy()
+        for g, w in spec:
+            normed = bbo.rmsnorm(h, g, 1e-5)
+            if isinstance(w, synth.MoeWeights):
+                y, tr = bbo.moe_ffn(w, normed, trace=True)
+                layers_work.append(layer_work(w, tr.counts, 1, False))
+            else:
+                y = bbo.dense_ffn(w, normed, 1)
+            h = (h + y).astype(np.float32)
+        dense_bytes = sum(synth.byte_size(w.gate_dtype, w.hidden * w.ff) * 3 for w in dense_w)
+        step_bytes = sum(l["step_bytes"] for l in layers_work) + dense_bytes
+    else:
+        per_layer = []
+        for w, layer in zip(weights, units):
+            tr = RouteTrace(T, w.n_experts, w.n_used)
+            layer.forward(np.ascontiguousarray(x_host.reshape(-1)), T, np.empty(T * w.hidden, np.float32), tr)
+            per_layer.append(layer_work(w, tr.counts, T, batched))
 
-    for i in range(args.warmup):
-        layers[i % L].forward(x, T, out)
+    def step(i):
+        units[i % len(units)].forward(x, T, out)
+
+    for i in range(warmup):
+        step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        layers[i % L].forward(x, T, out)
+    for i in range(steps):
+        step(i)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    ms = el * 1e3 / args.steps
+    ms = el * 1e3 / steps
 
-    # second pass with HIP events around every launch, for per-kernel mean durations
+    # second pass with HIP events around every launch on the same stream: mean kernel durations
     ctx.profile(True)
     ctx.reset_stats()
-    for i in range(args.steps):
-        layers[i % L].forward(x, T, out)
+    for i in range(steps):
+        step(i)
     stats = ctx.kernel_stats()
     ctx.profile(False)
-
-    used = [per_layer[i % L] for i in range(args.steps)]
-    avg = {k: float(np.mean([u[k] for u in used])) for k in used[0]}
     kern_us = {n: v[0] * 1e3 / v[1] for n, v in stats.items()}
-    dominant = max(("gateup_swiglu", "down_combine"), key=lambda n: stats.get(n, (0, 1))[0])
+
+    if args.config == 5:
+        names = DECODE_KERNELS
+        avg = {n: float(np.mean([lw[n][0] for lw in layers_work])) for n in names}
+        avg_ops = {n: float(np.mean([lw[n][1] for lw in layers_work])) for n in names}
+        u_hit = float(np.mean([lw["u_hit"] for lw in layers_work]))
+    else:
+        names = GEMM_KERNELS if batched else DECODE_KERNELS
+        used = [per_layer[i % L] for i in range(steps)]
+        avg = {n: float(np.mean([u[n][0] for u in used])) for n in names}
+        avg_ops = {n: float(np.mean([u[n][1] for u in used])) for n in names}
+        step_bytes = float(np.mean([u["step_bytes"] for u in used]))
+        u_hit = float(np.mean([u["u_hit"] for u in used]))
+    dominant = max(names, key=lambda n: stats.get(n, (0, 1))[0])
     dom_us = kern_us[dominant]
-    achieved = avg[dominant] / (dom_us * 1e-6) / 1e9
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{dominant}_{cfg.name}.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
+    if args.config == 4:
+        achieved = avg_ops[dominant] / (dom_us * 1e-6) / 1e12
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS,
+                    "unit": "TFLOP/s", "frac": achieved / INT8_PEAK_TOPS, "traffic": traffic,
+                    "ops_per_launch": avg_ops[dominant], "op_type": "int8 multiply-adds x2",
+                    "frac_of_bf16_peak": achieved / BF16_PEAK_TFLOPS}
+    else:
+        achieved = avg[dominant] / (dom_us * 1e-6) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                    "algorithmic_bytes_per_launch": avg[dominant]}
 
+    kind = "prefill" if prefill else ("FFN-stack decode" if args.config == 5 else "decode")
     result = {
-        "metric": "MoE-block decode tok/s (config 2: 16 tokens, one MoE FFN block)",
+        "metric": f"MoE-block {kind} tok/s (config {args.config}: {T} token{'s' if T > 1 else ''}"
+                  f"{', 24-layer FFN stack' if args.config == 5 else ', one MoE FFN block'})",
         "value": T / (ms * 1e-3),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded Q4_K experts, N(0,1) hidden states; no GGUF offline)",
+        "data": "synthetic (seeded Q4_K/Q6_K experts, N(0,1) hidden states; no GGUF offline)",
         "config": {"workload": f"config {args.config}: {cfg.description}", "tokens": T, "hidden": 2048,
-                   "moe_ff": 1792, "experts": 32, "top_k": 4, "down": "Q6_K" if cfg.down_dtype == 14 else "Q4_K",
-                   "weight_sets_rotated": L, "weight_bytes_resident": int(sum(w.nbytes for w in weights))},
-        "block_hbm_gbps": avg["step"] / (ms * 1e-3) / 1e9,
-        "block_frac_of_8tbs": avg["step"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-        "mean_hit_experts": avg["u_hit"],
+                   "moe_ff": 1792, "experts": 32, "top_k": 4,
+                   "down": "Q4_K/Q6_K alternating" if args.config == 5 else
+                           ("Q6_K" if cfg.down_dtype == 14 else "Q4_K"),
+                   "path": "batched (grouped int8-MFMA GEMM)" if batched else "per-expert GEMV",
+                   "weight_sets_rotated": L, "weight_bytes_resident": weight_bytes},
+        "block_hbm_gbps": step_bytes / (ms * 1e-3) / 1e9,
+        "block_frac_of_8tbs": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "mean_hit_experts": u_hit,
         "kernel_us": {k: round(v, 3) for k, v in kern_us.items()},
-        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "algorithmic_bytes_per_launch": avg[dominant]},
+        "roofline": roofline,
         "cpu_baseline": None,
         "setup_s": round(t_gen, 1),
     }
+    if prefill:
+        ops = float(np.mean([per_layer[i % L]["ops"] for i in range(steps)]))
+        result["block_tflops"] = ops / (ms * 1e-3) / 1e12
+        result["block_frac_of_bf16_peak"] = result["block_tflops"] / BF16_PEAK_TFLOPS
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(weights[: min(L, 4)], x_host, T, args.cpu_seconds)
-    for l in layers:
-        l.close()
+        from oracle import bbo
+
+        if args.config == 5:
+            from oracle import bbo as _b
+            layers_o = [(g, w) for g, w in spec]
+            result["cpu_baseline"] = cpu_baseline(lambda i: _b.ffn_stack(layers_o, x_host.reshape(-1), 1, 1e-5), T,
+                                                  args.cpu_seconds, "the 24-layer FFN stack (T=1)")
+        else:
+            sample = weights[: min(L, 4)]
+            xs = x_host.reshape(-1)
+            fn = (lambda i: bbo.moe_ffn(sample[i % len(sample)], xs)) if T == 1 else \
+                (lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T))
+            result["cpu_baseline"] = cpu_baseline(fn, T, args.cpu_seconds,
+                                                  f"moe_ffn{'_batch' if T > 1 else ''} (T={T}, {len(sample)} rotated layers)")
+    if args.config == 5:
+        stack.close()
+        for _, l in built:
+            l.close()
+    else:
+        for l in units:
+            l.close()
     ctx.close()
     print(json.dumps(result), flush=True)
 

@@ -1,0 +1,113 @@
+"""GPU parity of the batched MoE path (routing of many tokens, dispatch, grouped int8-MFMA GEMMs)
+against the CPU restatement of Model::moe_ffn_batch (model.rs:286-371).
+
+Bit-exact, like the per-token path: the GEMMs compute the reference's exact integer sub-dots and
+its f32 per-block epilogue in order, so block outputs, routing, weights and the dispatch
+permutation must equal the oracle's bit for bit. Config 3 (512 tokens) and config 4 (4096 tokens,
+Zipf selection bias, Q6_K down) run at full size; reduced shapes force the batched kernels onto
+small batches and edge cases.
+"""
+import numpy as np
+import pytest
+
+from bebelm_amd import synth
+from bebelm_amd.model import MoeLayer, RouteTrace
+
+from test_gpu_parity import Q4_K, Q6_K, assert_bits, check_moe, log
+
+pytestmark = pytest.mark.gpu
+
+DEFAULT_MIN_ENTRIES = 129
+
+
+@pytest.fixture
+def batched(gpu_ctx):
+    gpu_ctx.set_batched_min_entries(1)
+    yield gpu_ctx
+    gpu_ctx.set_batched_min_entries(DEFAULT_MIN_ENTRIES)
+
+
+@pytest.fixture
+def gemv_only(gpu_ctx):
+    gpu_ctx.set_batched_min_entries(1 << 40)
+    yield gpu_ctx
+    gpu_ctx.set_batched_min_entries(DEFAULT_MIN_ENTRIES)
+
+
+@pytest.mark.parametrize("t", [1, 2, 3, 7, 33, 64, 200])
+@pytest.mark.parametrize("down", [Q4_K, Q6_K])
+def test_batched_small_dims(batched, oracle, t, down):
+    w = synth.moe_weights(31, hidden=512, moe_ff=512, n_experts=8, down_dtype=down)
+    x = synth.hidden_states(32, t, hidden=512)
+    check_moe(batched, oracle, w, x, t, f"batched t={t}")
+
+
+@pytest.mark.parametrize("t", [5, 70])
+def test_batched_q6k_gate_up(batched, oracle, t):
+    w = synth.moe_weights(33, hidden=512, moe_ff=256, n_experts=8, down_dtype=Q6_K, gate_dtype=Q6_K)
+    x = synth.hidden_states(34, t, hidden=512)
+    check_moe(batched, oracle, w, x, t, f"q6k gate/up t={t}")
+
+
+def test_batched_other_shape(batched, oracle):
+    # k = 3 of 16 experts, hidden 768 (3 blocks), ff 1024
+    w = synth.moe_weights(35, hidden=768, moe_ff=1024, n_experts=16, n_used=3)
+    x = synth.hidden_states(36, 50, hidden=768)
+    check_moe(batched, oracle, w, x, 50, "k=3 E=16")
+
+
+def test_batched_one_dominant_expert_group(batched, oracle):
+    # every token picks the same 4 experts: groups of 300 members, several member tiles each
+    bias = np.zeros(32, np.float32)
+    bias[[3, 9, 17, 30]] = [4.0, 3.0, 2.0, 1.0]
+    w = synth.moe_weights(37, hidden=512, moe_ff=256, n_experts=32, bias=bias)
+    x = synth.hidden_states(38, 300, hidden=512)
+    _, tr = check_moe(batched, oracle, w, x, 300, "dominant group")
+    assert sorted(np.nonzero(tr.counts)[0].tolist()) == [3, 9, 17, 30]
+
+
+def test_batched_zero_inputs(batched, oracle):
+    w = synth.moe_weights(39, hidden=512, moe_ff=256, n_experts=8)
+    x = synth.hidden_states(40, 40, hidden=512)
+    x[0] = 0.0
+    x[5, :256] = 0.0
+    x[7] *= np.float32(1e3)
+    check_moe(batched, oracle, w, x, 40, "batched zero/scaled")
+
+
+@pytest.mark.parametrize("t", [33, 64])
+def test_gemv_path_many_members(gemv_only, oracle, t):
+    # the per-expert GEMV kernels with more members than they stage at once
+    w = synth.moe_weights(41, hidden=512, moe_ff=512, n_experts=8)
+    x = synth.hidden_states(42, t, hidden=512)
+    check_moe(gemv_only, oracle, w, x, t, f"gemv t={t}")
+
+
+def test_config3_prefill512_full_size(gpu_ctx, oracle):
+    w = synth.config_layer(3, seed=0)
+    x = synth.hidden_states(0, 512)
+    _, tr = check_moe(gpu_ctx, oracle, w, x, 512, "config3")
+    assert tr.counts.sum() == 2048
+
+
+def test_config4_prefill4096_zipf_q6k_full_size(gpu_ctx, oracle):
+    w = synth.config_layer(4, seed=0)
+    x = synth.hidden_states(0, 4096)
+    _, tr = check_moe(gpu_ctx, oracle, w, x, 4096, "config4")
+    share = np.sort(tr.counts)[::-1][:3].sum() / tr.counts.sum()
+    log(f"config4 top-3 expert share {share:.3f}")
+    assert share > 0.30
+
+
+def test_batched_rejects_too_many_entries(gpu_ctx):
+    from bebelm_amd import BBError
+
+    w = synth.moe_weights(43, hidden=256, moe_ff=256, n_experts=8)
+    layer = MoeLayer(gpu_ctx, w)
+    try:
+        t = 32768 // 4 + 1
+        x = np.zeros(t * 256, np.float32)
+        with pytest.raises(BBError):
+            layer.forward(x, t, np.empty_like(x))
+    finally:
+        layer.close()
