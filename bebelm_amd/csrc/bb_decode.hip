@@ -29,11 +29,12 @@ namespace bb {
 // (model.rs:485-495): sigmoid, rank of score+bias by total_cmp with the lower index first on
 // exact ties, renormalisation.
 constexpr int ROUTE_TPB_MAX = 16;
+constexpr int ROUTE_G = 2;  // tokens staged in LDS together (one float4 per thread)
 
 __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, const float* __restrict__ bias,
                                                 const float* __restrict__ x, int T, int H, int E, int K, int tpb,
                                                 XQBufs xq, RouteBufs rb) {
-  __shared__ __align__(16) float xs[GU_H_MAX];
+  __shared__ __align__(16) float xs[ROUTE_G][GU_H_MAX];
   __shared__ float lg[ROUTE_TPB_MAX][32];
   __shared__ int32_t s_key[ROUTE_TPB_MAX][32];
   __shared__ float s_rank_s[ROUTE_TPB_MAX][8];
@@ -49,39 +50,49 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
 #pragma unroll
   for (int k = 0; k < GU_H_MAX / 32 / 4; ++k)
     if (k < nm / 4) wv[k] = wr[32 * k];
-  const int nq = H / 4;  // float4 per token (<= 512 < 1024 threads)
+  const int nq = H / 4;  // float4 per token (<= 512)
   const float4* x4 = reinterpret_cast<const float4*>(x);
-  float4 xr = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (tid < nq) xr = x4[(size_t)t0 * nq + tid];
   const int nbx = H / QK;
-  for (int i = 0; i < nt; ++i) {
-    const int t = t0 + i;
-    if (tid < nq) reinterpret_cast<float4*>(xs)[tid] = xr;
+  // stage s covers tokens t0 + ROUTE_G*s .. ; each thread carries one float4 of the next stage
+  const int my_tk = tid / nq, my_q = tid % nq;
+  auto fetch = [&](int i0) {
+    return (my_tk < ROUTE_G && i0 + my_tk < nt) ? x4[(size_t)(t0 + i0 + my_tk) * nq + my_q]
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 xr = fetch(0);
+  for (int i0 = 0; i0 < nt; i0 += ROUTE_G) {
+    const int g = min(ROUTE_G, nt - i0);
+    if (my_tk < ROUTE_G) reinterpret_cast<float4*>(xs[my_tk])[my_q] = xr;
     __syncthreads();
-    if (i + 1 < nt && tid < nq) xr = x4[(size_t)(t + 1) * nq + tid];
-    if (wave < nbx) {
-      const float4 v = reinterpret_cast<const float4*>(xs + wave * QK)[lane];
-      wave_quantize_xq(v, xq.q + (size_t)t * H + wave * QK, xq.sx + (size_t)t * nbx + wave,
-                       xq.pairs ? xq.pairs + ((size_t)t * nbx + wave) * 12 : nullptr);
+    if (i0 + ROUTE_G < nt) xr = fetch(i0 + ROUTE_G);
+    // XQ records of the staged tokens: one wave per 256-block
+    for (int task = wave; task < g * nbx; task += 16) {
+      const int tk = task / nbx, bk = task % nbx, t = t0 + i0 + tk;
+      const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
+      wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                       xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
     }
-    float acc = 0.0f;
+    for (int tk = 0; tk < g; ++tk) {
+      const float* xt = xs[tk];
+      float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < GU_H_MAX / 32 / 4; ++k) {
-      if (k < nm / 4) {
-        acc = fmaf(wv[k].x, xs[32 * (4 * k + 0) + c], acc);
-        acc = fmaf(wv[k].y, xs[32 * (4 * k + 1) + c], acc);
-        acc = fmaf(wv[k].z, xs[32 * (4 * k + 2) + c], acc);
-        acc = fmaf(wv[k].w, xs[32 * (4 * k + 3) + c], acc);
+      for (int k = 0; k < GU_H_MAX / 32 / 4; ++k) {
+        if (k < nm / 4) {
+          acc = fmaf(wv[k].x, xt[32 * (4 * k + 0) + c], acc);
+          acc = fmaf(wv[k].y, xt[32 * (4 * k + 1) + c], acc);
+          acc = fmaf(wv[k].z, xt[32 * (4 * k + 2) + c], acc);
+          acc = fmaf(wv[k].w, xt[32 * (4 * k + 3) + c], acc);
+        }
       }
-    }
-    const float A = acc + __shfl_down(acc, 8, 32);
-    const float v = A + __shfl_down(A, 16, 32);
-    const float u = v + __shfl_down(v, 4, 32);
-    const float y = u + __shfl_down(u, 2, 32);
-    const float r = y + __shfl_down(y, 1, 32);
-    if (c == 0 && e < E) {
-      lg[i][e] = r;
-      rb.logits[(size_t)t * E + e] = r;
+      const float A = acc + __shfl_down(acc, 8, 32);
+      const float v = A + __shfl_down(A, 16, 32);
+      const float u = v + __shfl_down(v, 4, 32);
+      const float y = u + __shfl_down(u, 2, 32);
+      const float r = y + __shfl_down(y, 1, 32);
+      if (c == 0 && e < E) {
+        lg[i0 + tk][e] = r;
+        rb.logits[(size_t)(t0 + i0 + tk) * E + e] = r;
+      }
     }
     __syncthreads();
   }

@@ -30,8 +30,6 @@ typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
 enum : int { GEMM_GATEUP = 0, GEMM_DOWN = 1 };
 
-constexpr int BN = 64;                 // members per tile
-constexpr int PSTRIDE = BN * 8 + 128;  // bytes per row of 8-byte activation pieces in LDS
 constexpr size_t TB4 = pack_tile_block_bytes(DT_Q4_K);
 constexpr size_t TB6 = pack_tile_block_bytes(DT_Q6_K);
 
@@ -40,17 +38,26 @@ constexpr size_t TB6 = pack_tile_block_bytes(DT_Q6_K);
 // exclusive scan over chunks per expert gives each chunk's first group position; an entry's
 // position is that plus its rank among the chunk's entries of the same expert.
 __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ sel, int n_ent, int E, RouteBufs rb) {
+  constexpr int CPW = PF_MAX_ENTRIES / 64 / 16;  // chunks per wave
   __shared__ int32_t cc[PF_MAX_ENTRIES / 64][32];
   __shared__ int32_t part[32][33];
   __shared__ int32_t off[33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_chunks = (n_ent + 63) >> 6;
-  for (int ch = wave; ch < n_chunks; ch += 16) {
-    const int i = ch * 64 + lane;
-    const int v = i < n_ent ? sel[i] : -1;
+  // every selection this lane needs, loaded once up front (chunk wave + 16k, entry lane)
+  int v[CPW];
+#pragma unroll
+  for (int k = 0; k < CPW; ++k) {
+    const int i = (wave + 16 * k) * 64 + lane;
+    v[k] = i < n_ent ? sel[i] : -1;
+  }
+#pragma unroll
+  for (int k = 0; k < CPW; ++k) {
+    const int ch = wave + 16 * k;
+    if (ch >= n_chunks) break;
     int mine = 0;
     for (int x = 0; x < E; ++x) {
-      const int c = __popcll(__ballot(v == x));
+      const int c = __popcll(__ballot(v[k] == x));
       if (lane == x) mine = c;
     }
     if (lane < 32) cc[ch][lane] = mine;
@@ -67,9 +74,9 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ s
   if (tid < 32) {
     int acc = 0;
     for (int q = 0; q < 32; ++q) {
-      const int v = part[tid][q];
+      const int x = part[tid][q];
       part[tid][q] = acc;
-      acc += v;
+      acc += x;
     }
     part[tid][32] = acc;
   }
@@ -91,22 +98,23 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ s
   {
     int acc = part[e][p] + off[e];
     for (int ch = c0; ch < c1; ++ch) {
-      const int v = cc[ch][e];
+      const int x = cc[ch][e];
       cc[ch][e] = acc;
-      acc += v;
+      acc += x;
     }
   }
   __syncthreads();
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int ch = wave; ch < n_chunks; ch += 16) {
-    const int i = ch * 64 + lane;
-    const int v = i < n_ent ? sel[i] : -1;
+#pragma unroll
+  for (int k = 0; k < CPW; ++k) {
+    const int ch = wave + 16 * k;
+    if (ch >= n_chunks) break;
     unsigned long long mb = 0;
     for (int x = 0; x < E; ++x) {
-      const unsigned long long b = __ballot(v == x);
-      if (v == x) mb = b;
+      const unsigned long long b = __ballot(v[k] == x);
+      if (v[k] == x) mb = b;
     }
-    if (v >= 0) rb.perm[cc[ch][v] + __popcll(mb & lt)] = i;
+    if (v[k] >= 0) rb.perm[cc[ch][v[k]] + __popcll(mb & lt)] = ch * 64 + lane;
   }
 }
 
@@ -116,16 +124,16 @@ hipError_t launch_dispatch(hipStream_t s, int n_ent, int E, const RouteBufs& rb)
 }
 
 // ---- member tiles --------------------------------------------------------------------------------
-// Tiles are enumerated expert by expert, BN members each (an expert's last tile partial).
+// Tiles are enumerated expert by expert, bn members each (an expert's last tile partial).
 struct TileInfo {
   int e, m0, cnt, base, g;
 };
 
-__device__ bool find_tile(const RouteBufs& rb, int E, int tile, TileInfo& ti, int32_t* sh) {
+__device__ bool find_tile(const RouteBufs& rb, int E, int bn, int tile, TileInfo& ti, int32_t* sh) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const int c = lane < E ? rb.counts[lane] : 0;
-    const int nt = (c + BN - 1) / BN;
+    const int nt = (c + bn - 1) / bn;
     int incl = nt;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -135,7 +143,7 @@ __device__ bool find_tile(const RouteBufs& rb, int E, int tile, TileInfo& ti, in
     const int excl = incl - nt;
     if (lane < E && tile >= excl && tile < incl) {
       sh[0] = lane;
-      sh[1] = (tile - excl) * BN;
+      sh[1] = (tile - excl) * bn;
       sh[2] = c;
       sh[3] = rb.offsets[lane];
     }
@@ -147,7 +155,7 @@ __device__ bool find_tile(const RouteBufs& rb, int E, int tile, TileInfo& ti, in
   ti.m0 = sh[1];
   ti.g = sh[2];
   ti.base = sh[3];
-  ti.cnt = min(BN, ti.g - ti.m0);
+  ti.cnt = min(bn, ti.g - ti.m0);
   return true;
 }
 
@@ -155,13 +163,12 @@ __device__ bool find_tile(const RouteBufs& rb, int E, int tile, TileInfo& ti, in
 // output row (group position for gate/up, entry for down). Padding members repeat the last
 // real one so every load stays inside the inputs; their outputs are not stored.
 template <int KIND>
-__device__ void member_rows(const RouteBufs& rb, const TileInfo& ti, int K, int32_t* rowidx, int32_t* outrow) {
-  const int tid = threadIdx.x;
-  if (tid < BN) {
-    const int pos = ti.base + ti.m0 + min(tid, ti.cnt - 1);
+__device__ void member_rows(const RouteBufs& rb, const TileInfo& ti, int K, int bn, int32_t* rowidx, int32_t* outrow) {
+  for (int n = threadIdx.x; n < bn; n += blockDim.x) {
+    const int pos = ti.base + ti.m0 + min(n, ti.cnt - 1);
     const int ent = rb.perm[pos];
-    rowidx[tid] = KIND == GEMM_GATEUP ? ent / K : pos;
-    outrow[tid] = KIND == GEMM_GATEUP ? pos : ent;
+    rowidx[n] = KIND == GEMM_GATEUP ? ent / K : pos;
+    outrow[n] = KIND == GEMM_GATEUP ? pos : ent;
   }
 }
 
@@ -176,433 +183,307 @@ __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
   return (long)(((unsigned long)hi << 32) | lo);
 }
 
-// ---- Q4_K grouped GEMM -----------------------------------------------------------------------------
-// Block (member tile of 64, row tile = two 64-row packed tiles), 4 waves. Each wave owns two
-// 16-row weight tiles of one packed tile: for gate/up the gate rows and the up rows of the
-// same 16 outputs (so the SwiGLU pairs meet in one lane), for down two consecutive 16-row
-// tiles. MFMA v_mfma_i32_16x16x32_i8 per 32-element sub-block: A = 16 members x 32
-// activations (lane: member l%16, elements 8(l/16)..+7), B = 32 weights x 16 rows (lane: row
-// l%16, same elements), D lane l = members 4(l/16)..+3 of row l%16.
+// ---- grouped GEMM ------------------------------------------------------------------------------
+// Block (member tile of 16*MT members, row tile = two 64-row packed tiles), 8 waves; wave w owns
+// the 16-row tile (w&3) of packed tile (w>>2) against all members of the tile. For gate/up,
+// 16-row tiles 0-1 of a packed tile are gate rows and 2-3 the up rows of the same 32 outputs;
+// the up waves hand their values to the gate waves through LDS at the end (SwiGLU).
 //
-// Block b's operands are copied from HBM straight into LDS (global_load_lds_dwordx4: lane l's
-// 16 bytes land at base + 16l), double-buffered, so block b+1 streams in while block b is
+// MFMA v_mfma_i32_16x16x64_i8 with the activations as A (16 members x 64 elements; lane l:
+// member l%16) and the weights as B (64 elements x 16 rows; lane l: row l%16); lane group
+// g = l/16 supplies elements 16g..16g+15 of each 64-element step for both, so a lane's weights
+// lie in one sub-block (Q4_K: 32 elements, Q6_K: 16) and its activations are one 16-byte chunk
+// of the member's row. D lane l = members 4(l/16)..+3 of row l%16.
+//
+// Super-block b's operands are copied from HBM straight into LDS (global_load_lds_dwordx4: lane
+// l's 16 bytes land at base + 16l), double-buffered, so block b+1 streams in while block b is
 // computed and no registers hold data in flight:
-//   weights      the two packed tile-blocks verbatim (2 x 9216 B)
+//   weights      the two packed tile-blocks verbatim
 //   activations  member m's 256 quants as 16-byte chunks, chunk c at position c ^ (m%16) of
-//                the member's 256-byte row (conflict-free 8-byte reads of a sub-block piece)
-//   scales       sx of the 64 members
-constexpr int Q4_WBUF = 2 * (int)TB4;
-constexpr int XBUF = BN * QK;
-
-template <int KIND>
-struct Q4Gemm {
-  const uint8_t* w0;  // tile-block 0 of the block's first packed tile
-  size_t tile_bytes;  // bytes of one packed tile (all super-blocks)
-  GemmX x;
-  int n_in;
-  const int32_t* rowidx;
-
-  // Issue the copies of super-block b into one buffer set (every wave issues its share).
-  __device__ __forceinline__ void issue(int b, uint8_t* wb, uint8_t* xb, float* sb) const {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nb = n_in / QK;
-    // weights: 1152 16-byte units, 18 per lane-instruction group
-    for (int i = w; i < Q4_WBUF / 1024; i += 4) {
-      const int u = i * 64 + lane;
-      const int k = u / (int)(TB4 / 16), o = u % (int)(TB4 / 16);
-      const uint8_t* src = w0 + (size_t)k * tile_bytes + (size_t)b * TB4 + 16 * o;
-      __builtin_amdgcn_global_load_lds(src, wb + i * 1024, 16, 0, 0);
-    }
-    // activations: 1024 units
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int i = w + 4 * s;
-      const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
-      const int8_t* src = x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c;
-      __builtin_amdgcn_global_load_lds(src, xb + i * 1024, 16, 0, 0);
-    }
-    if (w == 0) __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[lane] * nb + b, sb, 4, 0, 0);
-  }
+//                the member's 256-byte row (conflict-free 16-byte reads)
+//   scales       sx of the members
+template <int DT>
+struct GemmTraits;
+template <>
+struct GemmTraits<DT_Q4_K> {
+  static constexpr int TB = (int)TB4;
+};
+template <>
+struct GemmTraits<DT_Q6_K> {
+  static constexpr int TB = (int)TB6;
 };
 
-__device__ __forceinline__ long q4_read_x(const uint8_t* xb, int j, int g, int m) {
-  const int c = 2 * j + (g >> 1);
-  return *reinterpret_cast<const long*>(xb + m * QK + 16 * (c ^ (m & 15)) + 8 * (g & 1));
-}
-
-// One super-block of the wave's 2 x 16 rows against the 64 members, added to acc.
-__device__ __forceinline__ void q4_block(const uint8_t* wb, const uint8_t* xb, const float* sb, int t16a, int t16b,
-                                         float (&acc)[2][4][4]) {
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  uint2 qs[2][4];
-  uint4 hd[2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    const int row = 16 * (a ? t16b : t16a) + r;
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      qs[a][c] = *reinterpret_cast<const uint2*>(wb + 1024 * (1 + 2 * c + (g >> 1)) + 16 * row + 8 * (g & 1));
-    hd[a] = *reinterpret_cast<const uint4*>(wb + 16 * row);
-  }
-  // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time
-  uint32_t scw[2][2], mw[2][2];
-  float dd[2], dm[2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    dd[a] = f16_bits_to_f32(hd[a].x & 0xffff);
-    dm[a] = f16_bits_to_f32(hd[a].x >> 16);
-    const uint32_t s0 = hd[a].y, s1 = hd[a].z, s2 = hd[a].w;
-    scw[a][0] = s0 & 0x3F3F3F3Fu;
-    scw[a][1] = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    mw[a][0] = s1 & 0x3F3F3F3Fu;
-    mw[a][1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-  }
-  // sd = 8*Dh + Dl: the high-scale pass accumulates first, is multiplied by 8 in place, and
-  // the low-scale pass continues into the same accumulator
-  v4i Dsd[2][4], Dm[2][4];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) Dsd[a][mt] = Dm[a][mt] = v4i{0, 0, 0, 0};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    long Bh[2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const uint2 qq = qs[a][j >> 1];
-      const uint32_t q0 = (j & 1) ? (qq.x >> 4) & 0x0F0F0F0Fu : qq.x & 0x0F0F0F0Fu;
-      const uint32_t q1 = (j & 1) ? (qq.y >> 4) & 0x0F0F0F0Fu : qq.y & 0x0F0F0F0Fu;
-      const uint32_t hs = (scw[a][j >> 2] >> (8 * (j & 3) + 3)) & 7u;
-      Bh[a] = as_long(mul_bytes(q0, hs), mul_bytes(q1, hs));
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const long ax = q4_read_x(xb, j, g, mt * 16 + r);
-#pragma unroll
-      for (int a = 0; a < 2; ++a) Dsd[a][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, Bh[a], Dsd[a][mt], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep each sub-block's operands short-lived
-  }
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) Dsd[a][mt] = Dsd[a][mt] << 3;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    long Bl[2], Bm[2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const uint2 qq = qs[a][j >> 1];
-      const uint32_t q0 = (j & 1) ? (qq.x >> 4) & 0x0F0F0F0Fu : qq.x & 0x0F0F0F0Fu;
-      const uint32_t q1 = (j & 1) ? (qq.y >> 4) & 0x0F0F0F0Fu : qq.y & 0x0F0F0F0Fu;
-      const uint32_t ls = (scw[a][j >> 2] >> (8 * (j & 3))) & 7u;
-      Bl[a] = as_long(mul_bytes(q0, ls), mul_bytes(q1, ls));
-      const uint32_t ms = ((mw[a][j >> 2] >> (8 * (j & 3))) & 0xffu) * 0x01010101u;
-      Bm[a] = as_long(ms, ms);
-    }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const long ax = q4_read_x(xb, j, g, mt * 16 + r);
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        Dsd[a][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, Bl[a], Dsd[a][mt], 0, 0, 0);
-        Dm[a][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, Bm[a], Dm[a][mt], 0, 0, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // matmul.rs:242 epilogue, in the reference's order of f32 operations
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
-    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = sxv[i] * ((dd[a] * (float)Dsd[a][mt][i]) - (dm[a] * (float)Dm[a][mt][i]));
-        acc[a][mt][i] += v;
-      }
-  }
-}
-
-template <int KIND>
-__global__ void __launch_bounds__(256, 2) k_gemm_q4(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in,
-                                                    int n_t64, int K, int n_out, int E, RouteBufs rb, GemmX x,
-                                                    float* __restrict__ out) {
-  __shared__ __align__(16) uint8_t wb0[Q4_WBUF], wb1[Q4_WBUF];
-  __shared__ __align__(16) uint8_t xb0[XBUF], xb1[XBUF];
-  __shared__ __align__(16) float sb0[BN], sb1[BN];
-  __shared__ int32_t rowidx[BN], outrow[BN];
-  __shared__ int32_t sh[8];
-  TileInfo ti;
-  if (!find_tile(rb, E, blockIdx.x, ti, sh)) return;
-  member_rows<KIND>(rb, ti, K, rowidx, outrow);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
-  const int nb = n_in / QK;
-  const int t64 = 2 * blockIdx.y + (w >> 1);  // n_t64 is even: both packed tiles exist
-  const int t16a = KIND == GEMM_GATEUP ? (w & 1) : 2 * (w & 1);
-  const int t16b = KIND == GEMM_GATEUP ? (w & 1) + 2 : 2 * (w & 1) + 1;
-  const size_t tile_bytes = (size_t)nb * TB4;
-  Q4Gemm<KIND> G{wpk + (size_t)ti.e * stride_e + (size_t)(2 * blockIdx.y) * tile_bytes, tile_bytes, x, n_in, rowidx};
-  const float start = ti.g > 1 ? 0.0f : -0.0f;
-  float acc[2][4][4];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[a][mt][i] = start;
-  __syncthreads();  // rowidx
-  G.issue(0, wb0, xb0, sb0);
-  const int wo = (w >> 1) * (int)TB4;  // this wave's packed tile inside a weight buffer
-  for (int b = 0; b < nb; b += 2) {
-    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
-    __syncthreads();
-    if (b + 1 < nb) G.issue(b + 1, wb1, xb1, sb1);
-    q4_block(wb0 + wo, xb0, sb0, t16a, t16b, acc);
-    if (b + 1 >= nb) break;
-    __builtin_amdgcn_s_waitcnt(0x3f70);
-    __syncthreads();
-    if (b + 2 < nb) G.issue(b + 2, wb0, xb0, sb0);
-    q4_block(wb1 + wo, xb1, sb1, t16a, t16b, acc);
-  }
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = mt * 16 + 4 * g + i;
-      if (n >= ti.cnt) continue;
-      if constexpr (KIND == GEMM_GATEUP) {
-        const int o = 32 * t64 + 16 * (w & 1) + r;
-        out[(size_t)outrow[n] * n_out + o] = silu(acc[0][mt][i]) * acc[1][mt][i];
-      } else {
-        out[(size_t)outrow[n] * n_out + 64 * t64 + 16 * t16a + r] = acc[0][mt][i];
-        out[(size_t)outrow[n] * n_out + 64 * t64 + 16 * t16b + r] = acc[1][mt][i];
-      }
-    }
-  (void)n_t64;
-}
-
-// ---- Q6_K grouped GEMM -----------------------------------------------------------------------------
-// Block (member tile of 64, row tile = two 64-row packed tiles), 4 waves; operands copied
-// into LDS as for Q4_K (weights verbatim, 2 x 13440 B). v_mfma_i32_32x32x16_i8 per 16-element
-// sub-block: A = 32 members x 16 activations (lane: member l%32, elements 8(l/32)..+7),
-// B = 16 weights x 32 rows (lane: row l%32), D lane l = members 8(i/4) + 4(l/32) + i%4
-// (i = 0..15) of row l%32, so the row's i8 scale multiplies all 16 values in the lane.
-//   down:    wave w owns the 32-row half (w&1) of packed tile (w>>1), all 64 members
-//   gate/up: wave w owns packed tile (w>>1) — its gate half and its up half, the 32 outputs'
-//            SwiGLU pairs — for the 32 members of half (w&1)
-constexpr int Q6_WBUF = 2 * (int)TB6;
-
-__device__ __forceinline__ void q6_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
-                                         const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
+template <int DT, int MT>
+__device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
+                                           const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
+  constexpr int TB = GemmTraits<DT>::TB;
+  constexpr int W_UNITS = 2 * TB / 16, X_UNITS = 16 * MT * 16;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nb = n_in / QK;
-  constexpr int units = Q6_WBUF / 16, per_tile = (int)(TB6 / 16);
-  for (int i = w; i < (units + 63) / 64; i += 4) {
+  for (int i = w; i < (W_UNITS + 63) / 64; i += 8) {
     const int u = i * 64 + lane;
-    if (u < units) {
-      const int k = u / per_tile, o = u % per_tile;
-      __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB6 + 16 * o, wb + i * 1024, 16, 0, 0);
+    if (u < W_UNITS) {
+      const int k = u / (TB / 16), o = u % (TB / 16);
+      __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB + 16 * o, wb + i * 1024, 16, 0, 0);
     }
   }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int i = w + 4 * s;
+  for (int s = 0; s < X_UNITS / 512; ++s) {
+    const int i = w + 8 * s;
     const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
     __builtin_amdgcn_global_load_lds(x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c, xb + i * 1024, 16, 0, 0);
   }
-  if (w == 0) __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[lane] * nb + b, sb, 4, 0, 0);
+  if (w < (16 * MT) / 64)
+    __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[w * 64 + lane] * nb + b, sb + w * 64, 4, 0, 0);
 }
 
-// One super-block: NT 32-row weight tiles (rows 32*half[a] + l%32 of packed tile wt) against
-// MT groups of 32 members starting at member m0.
-template <int NT, int MT>
-__device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, const float* sb, const int (&half)[NT],
-                                         int m0, float (&acc)[NT][MT][16]) {
-  const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
-  uint2 ql[NT][8], qh[NT][4];
-  uint4 sc[NT];
-  float dd[NT];
+__device__ __forceinline__ v4i read_x16(const uint8_t* xb, int m, int chunk) {
+  return *reinterpret_cast<const v4i*>(xb + m * QK + 16 * (chunk ^ (m & 15)));
+}
+
+__device__ __forceinline__ uint32_t splat_byte(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0u); }
+
+// Q4_K: sd = Σ_j sc_j·Σ q·x with sc = 8·(sc>>3) + (sc&7): both weight products stay <= 105, so
+// the high- and low-scale passes give sd = 8·Dh + Dl; a third pass with weight m_j for every
+// element of sub-block j gives sm = Σ_j m_j·S_j. Epilogue matmul.rs:242 in the reference's order.
+template <int MT>
+__device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
+                                         float (&acc)[MT][4]) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint4 hd = *reinterpret_cast<const uint4*>(wt + 16 * row);
+  const float dd = f16_bits_to_f32(hd.x & 0xffff);
+  const float dm = f16_bits_to_f32(hd.x >> 16);
+  // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time
+  const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
+  const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
+  const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+  v4i Dh[MT], Dl[MT], Dm[MT];
 #pragma unroll
-  for (int a = 0; a < NT; ++a) {
-    const int row = 32 * half[a] + r;
+  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = Dm[mt] = v4i{0, 0, 0, 0};
+  const int hi = g >> 1;  // high nibbles: sub-block 2c+1
+  const uint32_t nsh = 4 * hi;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) ql[a][k] = *reinterpret_cast<const uint2*>(wt + 1024 * k + 16 * row + 8 * h);
+  for (int c = 0; c < 4; ++c) {
+    const int sh = 8 * (2 * (c & 1) + hi);  // byte of sub-block 2c+hi in the scale dwords
+    const uint4 qv = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * c + (g & 1)) + 16 * row);
+    const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
+                           (qv.w >> nsh) & 0x0F0F0F0Fu};
+    const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
+    const uint32_t hs = scv >> 3, ls = scv & 7u;
+    const int ms = (int)splat_byte(mw[c >> 1] >> sh);
+    v4i Bh, Bl, Bm;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) qh[a][k] = *reinterpret_cast<const uint2*>(wt + 1024 * (8 + k) + 16 * row + 8 * h);
-    sc[a] = *reinterpret_cast<const uint4*>(wt + 1024 * 12 + 16 * row);
-    dd[a] = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(wt + 1024 * 13 + 2 * row));
-  }
-  int S[NT][MT][16];
-#pragma unroll
-  for (int a = 0; a < NT; ++a)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) S[a][mt][i] = 0;
-  // sub-block j = elements 16j..16j+15 = 128n + 32gq + 16m + (0..15), n = j/8, gq = (j/2)%4,
-  // m = j%2: low nibbles of ql[64n + 32(gq&1) + 16m + ..] (high nibbles for gq >= 2) and bits
-  // 2gq of qh[32n + 16m + ..] (dequant.rs:122-138); the weight is q − 32 (per byte, no borrows)
-  auto weights = [&](int j, int a) -> long {
-    const int n = j >> 3, gq = (j >> 1) & 3, m = j & 1;
-    const uint2 l4 = ql[a][4 * n + 2 * (gq & 1) + m];
-    const uint2 h2 = qh[a][2 * n + m];
-    const uint32_t lo0 = (gq >> 1) ? (l4.x >> 4) & 0x0F0F0F0Fu : l4.x & 0x0F0F0F0Fu;
-    const uint32_t lo1 = (gq >> 1) ? (l4.y >> 4) & 0x0F0F0F0Fu : l4.y & 0x0F0F0F0Fu;
-    const uint32_t q0 = lo0 | (((h2.x >> (2 * gq)) & 0x03030303u) << 4);
-    const uint32_t q1 = lo1 | (((h2.y >> (2 * gq)) & 0x03030303u) << 4);
-    return as_long(((q0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u, ((q1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
-  };
-  auto scale = [&](int j, int a) -> int {
-    const uint32_t scd = j < 4 ? sc[a].x : j < 8 ? sc[a].y : j < 12 ? sc[a].z : sc[a].w;
-    return (int)(int8_t)((scd >> (8 * (j & 3))) & 0xffu);
-  };
-  auto mfmas = [&](int j, v16i (&D)[NT][MT]) {
-    long cw[NT];
-#pragma unroll
-    for (int a = 0; a < NT; ++a) cw[a] = weights(j, a);
+    for (int k = 0; k < 4; ++k) {
+      Bh[k] = (int)mul_bytes(q[k], hs);
+      Bl[k] = (int)mul_bytes(q[k], ls);
+      Bm[k] = ms;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int mm = m0 + mt * 32 + r;
-      const long ax = *reinterpret_cast<const long*>(xb + mm * QK + 16 * (j ^ (mm & 15)) + 8 * h);
-#pragma unroll
-      for (int a = 0; a < NT; ++a) {
-        const v16i z = {};
-        D[a][mt] = __builtin_amdgcn_mfma_i32_32x32x16_i8(ax, cw[a], z, 0, 0, 0);
-      }
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
+      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
+      Dm[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm[mt], 0, 0, 0);
     }
-  };
-  // two result sets: the MFMAs of sub-block j+1 run while the VALU scales sub-block j
-  v16i D0[NT][MT], D1[NT][MT];
-  mfmas(0, D0);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    v16i(&Dc)[NT][MT] = (j & 1) ? D1 : D0;
-    v16i(&Dn)[NT][MT] = (j & 1) ? D0 : D1;
-    if (j + 1 < 16) mfmas(j + 1, Dn);
-#pragma unroll
-    for (int a = 0; a < NT; ++a) {
-      const int sj = scale(j, a);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S[a][mt][i] += __mul24(sj, Dc[a][mt][i]);  // |D| < 2^17: exact in 24 bits
-    }
-    // one multiply-add per value and sub-block, in order: keep the sums from being regrouped
-#pragma unroll
-    for (int a = 0; a < NT; ++a)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(S[a][mt][i]));
-    __builtin_amdgcn_sched_barrier(0);
   }
-  // matmul.rs:641 epilogue: sx·(d·(float)s)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
+    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sd = 8 * Dh[mt][i] + Dl[mt][i];
+      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[mt][i]));
+      acc[mt][i] += v;
+    }
+  }
+}
+
+// (hi, lo) int8 parts of sc*(q - 32) for four quant bytes q (<= 63): the products are formed
+// in 16-bit lanes (even and odd bytes) and the bytes put back in order.
+__device__ __forceinline__ void q6_split(uint32_t q, uint32_t scp, uint32_t bias, uint32_t& h, uint32_t& l) {
+  typedef short v2i16 __attribute__((ext_vector_type(2)));
+  const v2i16 ev = __builtin_bit_cast(v2i16, q & 0x00FF00FFu);
+  const v2i16 od = __builtin_bit_cast(v2i16, (q >> 8) & 0x00FF00FFu);
+  const v2i16 sc2 = __builtin_bit_cast(v2i16, scp), b2 = __builtin_bit_cast(v2i16, bias);
+  const v2i16 ae = ev * sc2 + b2, ao = od * sc2 + b2;  // sc*q - 32*sc, exact in 16 bits
+  const uint32_t ue = __builtin_bit_cast(uint32_t, ae), uo = __builtin_bit_cast(uint32_t, ao);
+  const uint32_t he = __builtin_bit_cast(uint32_t, ae >> (v2i16){6, 6});
+  const uint32_t ho = __builtin_bit_cast(uint32_t, ao >> (v2i16){6, 6});
+  // bytes {e0, o0, e1, o1} from the low bytes of the 16-bit lanes (v_perm: bytes 0-3 of the
+  // second operand, 4-7 of the first)
+  l = __builtin_amdgcn_perm(uo & 0x003F003Fu, ue & 0x003F003Fu, 0x06020400u);
+  h = __builtin_amdgcn_perm(ho, he, 0x06020400u);
+}
+
+// Q6_K: s = Σ_j sc_j·Σ (q − 32)·x. With a = sc_j·(q − 32) (|a| <= 4096) split as a = 64·h + l,
+// h in [−64, 64] and l in [0, 63] both fit int8: two passes give s = 64·Dh + Dl. Epilogue
+// matmul.rs:641: sx·(d·(float)s).
+template <int MT>
+__device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
+                                         float (&acc)[MT][4]) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint4 sc = *reinterpret_cast<const uint4*>(wt + 1024 * 12 + 16 * row);
+  const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(wt + 1024 * 13 + 2 * row));
+  v4i Dh[MT], Dl[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    // elements 64c + 16g + t = 128n + 32gq + 16(g&1) + t with n = c/2, gq = 2(c&1) + g/2
+    // (dequant.rs:122-138): ql[64n + 32(g/2) + 16(g&1) + t] (high nibble when c is odd) and
+    // bits 2gq of qh[32n + 16(g&1) + t]; sub-block j = 4c + g
+    const int n2 = c >> 1, gq = 2 * (c & 1) + (g >> 1);
+    const uint4 qlv = *reinterpret_cast<const uint4*>(wt + 1024 * (4 * n2 + 2 * (g >> 1) + (g & 1)) + 16 * row);
+    const uint4 qhv = *reinterpret_cast<const uint4*>(wt + 1024 * (8 + 2 * n2 + (g & 1)) + 16 * row);
+    const uint32_t lsh = 4 * (c & 1), hsh = 2 * gq;
+    const uint32_t scd = c == 0 ? sc.x : c == 1 ? sc.y : c == 2 ? sc.z : sc.w;
+    const int scj = (int)(int8_t)((scd >> (8 * g)) & 0xffu);
+    const uint32_t scp = ((uint32_t)scj & 0xffffu) * 0x00010001u;
+    const uint32_t bias = ((uint32_t)(-32 * scj) & 0xffffu) * 0x00010001u;
+    const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+    v4i Bh, Bl;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t q = ((qlw[k] >> lsh) & 0x0F0F0F0Fu) | (((qhw[k] >> hsh) & 0x03030303u) << 4);
+      uint32_t hh, ll;
+      q6_split(q, scp, bias, hh, ll);
+      Bh[k] = (int)hh;
+      Bl[k] = (int)ll;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
+      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
+    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sv = 64 * Dh[mt][i] + Dl[mt][i];
+      const float v = sxv[i] * (d * (float)sv);
+      acc[mt][i] += v;
+    }
+  }
+}
+
+template <int DT, int KIND, int MT>
+__global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
+                                              int n_out, int E, RouteBufs rb, GemmX x, float* __restrict__ out) {
+  constexpr int TB = GemmTraits<DT>::TB;
+  constexpr int NBM = 16 * MT;  // members per tile
+  __shared__ __align__(16) uint8_t wb0[2 * TB], wb1[2 * TB];
+  __shared__ __align__(16) uint8_t xb0[NBM * QK], xb1[NBM * QK];
+  __shared__ __align__(16) float sb0[NBM], sb1[NBM];
+  __shared__ int32_t rowidx[NBM], outrow[NBM];
+  __shared__ int32_t sh[8];
+  // Workgroups are handed to the 8 XCDs round-robin by id. XCD k takes member tiles k, k+8, ...
+  // and sweeps all row tiles of one member tile before the next, so the member tile's
+  // activations are fetched once into that XCD's L2; the sweep direction alternates so the
+  // weights used last are used first again.
+  const int n_rt = gridDim.y, n_mt = gridDim.x;  // n_mt: an upper bound, a multiple of 8
+  const int lin = blockIdx.y * n_mt + blockIdx.x;
+  const int xcd = lin & 7, slot = lin >> 3;
+  const int mt_local = slot / n_rt, rt_step = slot % n_rt;
+  const int mtile = mt_local * 8 + xcd;
+  const int rtile = (mt_local & 1) ? n_rt - 1 - rt_step : rt_step;
+  TileInfo ti;
+  if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
+  member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int nb = n_in / QK;
+  const int k64 = w >> 2, t16 = w & 3, row = 16 * t16 + r;
+  const int t64 = 2 * rtile + k64;
+  const size_t tile_bytes = (size_t)nb * TB;
+  const uint8_t* w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+  const int wo = k64 * TB;
+  const float start = ti.g > 1 ? 0.0f : -0.0f;
+  float acc[MT][4];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const float4 sx4 = *reinterpret_cast<const float4*>(sb + m0 + mt * 32 + 8 * q4 + 4 * h);
-      const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-#pragma unroll
-      for (int a = 0; a < NT; ++a)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float v = sxv[k] * (dd[a] * (float)S[a][mt][4 * q4 + k]);
-          acc[a][mt][4 * q4 + k] += v;
-        }
-    }
-}
-
-template <int KIND>
-__global__ void __launch_bounds__(256, 2) k_gemm_q6(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in,
-                                                 int n_t64, int K, int n_out, int E, RouteBufs rb, GemmX x,
-                                                 float* __restrict__ out) {
-  constexpr int NT = KIND == GEMM_GATEUP ? 2 : 1;
-  constexpr int MT = KIND == GEMM_GATEUP ? 1 : 2;
-  __shared__ __align__(16) uint8_t wb0[Q6_WBUF], wb1[Q6_WBUF];
-  __shared__ __align__(16) uint8_t xb0[XBUF], xb1[XBUF];
-  __shared__ __align__(16) float sb0[BN], sb1[BN];
-  __shared__ int32_t rowidx[BN], outrow[BN];
-  __shared__ int32_t sh[8];
-  TileInfo ti;
-  if (!find_tile(rb, E, blockIdx.x, ti, sh)) return;
-  member_rows<KIND>(rb, ti, K, rowidx, outrow);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 31, h = lane >> 5;
-  const int nb = n_in / QK;
-  const int t64 = 2 * blockIdx.y + (w >> 1);
-  int half[NT];
-  if constexpr (KIND == GEMM_GATEUP) {
-    half[0] = 0;
-    half[NT - 1] = 1;
-  } else {
-    half[0] = w & 1;
-  }
-  const int m0 = KIND == GEMM_GATEUP ? 32 * (w & 1) : 0;
-  const size_t tile_bytes = (size_t)nb * TB6;
-  const uint8_t* w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * blockIdx.y) * tile_bytes;
-  const int wo = (w >> 1) * (int)TB6;
-  const float start = ti.g > 1 ? 0.0f : -0.0f;
-  float acc[NT][MT][16];
-#pragma unroll
-  for (int a = 0; a < NT; ++a)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][mt][i] = start;
+    for (int i = 0; i < 4; ++i) acc[mt][i] = start;
+  auto block = [&](const uint8_t* wb, const uint8_t* xb, const float* sb) {
+    if constexpr (DT == DT_Q4_K) q4_block<MT>(wb + wo, xb, sb, row, acc);
+    else q6_block<MT>(wb + wo, xb, sb, row, acc);
+  };
   __syncthreads();  // rowidx
-  q6_issue(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+  gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     __syncthreads();
-    if (b + 1 < nb) q6_issue(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
-    q6_block<NT, MT>(wb0 + wo, xb0, sb0, half, m0, acc);
+    if (b + 1 < nb) gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+    block(wb0, xb0, sb0);
     if (b + 1 >= nb) break;
     __builtin_amdgcn_s_waitcnt(0x3f70);
     __syncthreads();
-    if (b + 2 < nb) q6_issue(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
-    q6_block<NT, MT>(wb1 + wo, xb1, sb1, half, m0, acc);
+    if (b + 2 < nb) gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+    block(wb1, xb1, sb1);
   }
+  if constexpr (KIND == GEMM_GATEUP) {
+    // the up waves hand their values to the gate waves of the same outputs
+    __syncthreads();
+    float* upv = reinterpret_cast<float*>(xb0);  // 4 up waves x MT*4 values x 64 lanes = sizeof xb0
+    if (t16 >= 2) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int n = m0 + mt * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-      if (n >= ti.cnt) continue;
-      if constexpr (KIND == GEMM_GATEUP) {
-        out[(size_t)outrow[n] * n_out + 32 * t64 + r] = silu(acc[0][mt][i]) * acc[NT - 1][mt][i];
-      } else {
-        out[(size_t)outrow[n] * n_out + 64 * t64 + 32 * half[0] + r] = acc[0][mt][i];
-      }
+        for (int i = 0; i < 4; ++i) upv[((k64 * 2 + (t16 - 2)) * (4 * MT) + mt * 4 + i) * 64 + lane] = acc[mt][i];
     }
-  (void)n_t64;
+    __syncthreads();
+    if (t16 < 2) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = mt * 16 + 4 * g + i;
+          if (n >= ti.cnt) continue;
+          const float up = upv[((k64 * 2 + t16) * (4 * MT) + mt * 4 + i) * 64 + lane];
+          out[(size_t)outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu(acc[mt][i]) * up;
+        }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = mt * 16 + 4 * g + i;
+        if (n >= ti.cnt) continue;
+        out[(size_t)outrow[n] * n_out + 64 * t64 + 16 * t16 + r] = acc[mt][i];
+      }
+  }
 }
 
-static int max_tiles(int T, int K, int E) { return (T * K + BN - 1) / BN + E; }
+// Member tiles of 128 when the experts' groups are large enough to fill them, else 64.
+template <int DT, int KIND>
+static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
+                              int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
+  const int n_ent = T * K;
+  const bool wide = n_ent >= 64 * E * 2;
+  const int bn = wide ? 128 : 64;
+  const int n_mt = ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;  // enough member tiles, a multiple of 8
+  dim3 grid(n_mt, n_t64 / 2);
+  if (wide)
+    hipLaunchKernelGGL((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+  else
+    hipLaunchKernelGGL((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
                               int E, int K, const RouteBufs& rb, GemmX x, float* act) {
-  const int n_t64 = F / 32;
-  if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_gemm_q4<GEMM_GATEUP>, dim3(max_tiles(T, K, E), n_t64 / 2), dim3(256), 0, s, gu,
-                       stride_gu, H, n_t64, K, F, E, rb, x, act);
-  else
-    hipLaunchKernelGGL(k_gemm_q6<GEMM_GATEUP>, dim3(max_tiles(T, K, E), n_t64 / 2), dim3(256), 0, s, gu,
-                       stride_gu, H, n_t64, K, F, E, rb, x, act);
-  return hipGetLastError();
+  if (dtype == DT_Q4_K) return launch_gemm<DT_Q4_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act);
+  return launch_gemm<DT_Q6_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act);
 }
 
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
                             int K, const RouteBufs& rb, GemmX x, float* slots) {
-  const int n_t64 = H / 64;
-  dim3 grid(max_tiles(T, K, E), n_t64 / 2);
-  if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_gemm_q4<GEMM_DOWN>, grid, dim3(256), 0, s, dn, stride_dn, F, n_t64, K, H, E, rb, x, slots);
-  else
-    hipLaunchKernelGGL(k_gemm_q6<GEMM_DOWN>, grid, dim3(256), 0, s, dn, stride_dn, F, n_t64, K, H, E, rb, x, slots);
-  return hipGetLastError();
+  if (dtype == DT_Q4_K) return launch_gemm<DT_Q4_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots);
+  return launch_gemm<DT_Q6_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots);
 }
 
 // ---- Q8 rows ---------------------------------------------------------------------------------------
