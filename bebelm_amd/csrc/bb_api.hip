@@ -157,10 +157,15 @@ void launch(bb_ctx* c, int id, F&& f) {
     check_hip(f(), bb::kernel_name(id));
     return;
   }
+  // both events are recorded first (valid even if the launcher has nothing to launch); the
+  // kernel's dispatch then re-stamps them with its exact start and end
   hipEvent_t a = take_event(c), b = take_event(c);
   check_hip(hipEventRecord(a, c->stream), "hipEventRecord");
-  check_hip(f(), bb::kernel_name(id));
   check_hip(hipEventRecord(b, c->stream), "hipEventRecord");
+  bb::launch_events() = {a, b};
+  const hipError_t rc = f();
+  bb::launch_events() = {};
+  check_hip(rc, bb::kernel_name(id));
   c->pending.push_back({id, a, b});
 }
 

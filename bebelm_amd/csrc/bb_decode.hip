@@ -148,14 +148,14 @@ __global__ void k_router_chain_major(const float* __restrict__ W, int H, int E, 
 }
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc) {
-  hipLaunchKernelGGL(k_router_chain_major, dim3((unsigned)(((size_t)E * H + 255) / 256)), dim3(256), 0, s, W, H, E, Wc);
+  BB_LAUNCH(k_router_chain_major, dim3((unsigned)(((size_t)E * H + 255) / 256)), dim3(256), 0, s, W, H, E, Wc);
   return hipGetLastError();
 }
 
 hipError_t launch_route(hipStream_t s, const float* router, const float* bias, const float* x, int T, int H, int E,
                         int K, int tpb, XQBufs xq, RouteBufs rb) {
   tpb = max(1, min(tpb, ROUTE_TPB_MAX));
-  hipLaunchKernelGGL(k_route, dim3((T + tpb - 1) / tpb), dim3(1024), 0, s, router, bias, x, T, H, E, K, tpb, xq, rb);
+  BB_LAUNCH(k_route, dim3((T + tpb - 1) / tpb), dim3(1024), 0, s, router, bias, x, T, H, E, K, tpb, xq, rb);
   return hipGetLastError();
 }
 
@@ -402,10 +402,10 @@ static hipError_t launch_experts(hipStream_t s, int dtype, const uint8_t* wpk, s
   const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
   const int grid = min(GEMV_BLOCKS, max_hit * tiles);
   if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL((k_experts<DT_Q4_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+    BB_LAUNCH((k_experts<DT_Q4_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
                        publish, E, rb, xq, act_in, out);
   else
-    hipLaunchKernelGGL((k_experts<DT_Q6_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+    BB_LAUNCH((k_experts<DT_Q6_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
                        publish, E, rb, xq, act_in, out);
   return hipGetLastError();
 }
@@ -468,7 +468,7 @@ hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const ui
   const int n_tiles = rows_a / (b ? 32 : 64);
   const size_t total = (size_t)n_exp * n_tiles * nb * (pack_chunks(dtype) + 1) * 64;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_pack_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, dtype, a, b, stride_a,
+  BB_LAUNCH(k_pack_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, dtype, a, b, stride_a,
                      stride_b, rows_a, nb, n_exp, dst);
   return hipGetLastError();
 }
@@ -486,7 +486,7 @@ __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ slots
 }
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out) {
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, slots, wts, T, H, K,
+  BB_LAUNCH(k_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, slots, wts, T, H, K,
                      out);
   return hipGetLastError();
 }

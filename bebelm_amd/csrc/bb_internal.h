@@ -1,11 +1,28 @@
 // bb_internal.h — launcher declarations shared by the kernels TU and the C-ABI TU.
 #ifndef BB_INTERNAL_H
 #define BB_INTERNAL_H
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace bb {
+
+// Profiling: when set, kernels are launched with hipExtLaunchKernelGGL, which has the kernel's
+// own dispatch stamp the two events (exact start and end, no queue gaps in between).
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents& launch_events();  // per host thread
+
+#define BB_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                  \
+  do {                                                                                                     \
+    const ::bb::LaunchEvents& bb_ev_ = ::bb::launch_events();                                              \
+    if (bb_ev_.start)                                                                                      \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, bb_ev_.start, bb_ev_.stop, 0, __VA_ARGS__); \
+    else                                                                                                   \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                                 \
+  } while (0)
 
 // Device-side routing state for one forward call. All arrays live in the context workspace.
 struct RouteBufs {

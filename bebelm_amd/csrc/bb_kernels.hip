@@ -12,6 +12,11 @@
 
 namespace bb {
 
+LaunchEvents& launch_events() {
+  static thread_local LaunchEvents ev;
+  return ev;
+}
+
 const char* kernel_name(int id) {
   static const char* names[K_COUNT] = {"route_gating",  "gateup_swiglu", "down_combine", "quantize_q8",
                                        "rows_q8",      "rows_f32",      "elementwise",  "rmsnorm",
@@ -63,7 +68,7 @@ __global__ void __launch_bounds__(256) k_quantize(const float* __restrict__ x, s
 hipError_t launch_quantize(hipStream_t s, const float* x, size_t n_vec, size_t n, Q8Bufs q) {
   const size_t waves = n_vec * (n / QK);
   if (waves == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quantize, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_vec, n, q);
+  BB_LAUNCH(k_quantize, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_vec, n, q);
   return hipGetLastError();
 }
 
@@ -91,10 +96,10 @@ hipError_t launch_rows_q8(hipStream_t s, int dtype, const uint8_t* w, size_t row
   if (n_rows == 0) return hipSuccess;
   dim3 grid((unsigned)((n_rows + 31) / 32));
   if (dtype == DT_Q4_K)
-    hipLaunchKernelGGL(k_rows_q8<DT_Q4_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
+    BB_LAUNCH(k_rows_q8<DT_Q4_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
                        y_tok_stride, neg_zero_start);
   else
-    hipLaunchKernelGGL(k_rows_q8<DT_Q6_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
+    BB_LAUNCH(k_rows_q8<DT_Q6_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
                        y_tok_stride, neg_zero_start);
   return hipGetLastError();
 }
@@ -122,9 +127,9 @@ hipError_t launch_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t n_
   if (items == 0) return hipSuccess;
   dim3 grid((unsigned)((items + 7) / 8));
   if (dtype == DT_F32)
-    hipLaunchKernelGGL(k_rows_f32<DT_F32>, grid, dim3(256), 0, s, w, n_in, n_rows, x, n_tok, y);
+    BB_LAUNCH(k_rows_f32<DT_F32>, grid, dim3(256), 0, s, w, n_in, n_rows, x, n_tok, y);
   else
-    hipLaunchKernelGGL(k_rows_f32<DT_F16>, grid, dim3(256), 0, s, w, n_in, n_rows, x, n_tok, y);
+    BB_LAUNCH(k_rows_f32<DT_F16>, grid, dim3(256), 0, s, w, n_in, n_rows, x, n_tok, y);
   return hipGetLastError();
 }
 
@@ -144,7 +149,7 @@ __global__ void __launch_bounds__(256) k_elementwise(int op, float* __restrict__
 hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a, const float* b, float scalar,
                               size_t n) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_elementwise, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, op, out, a, b, scalar, n);
+  BB_LAUNCH(k_elementwise, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, op, out, a, b, scalar, n);
   return hipGetLastError();
 }
 
@@ -179,7 +184,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
                           float* out) {
   if (n_vec == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)n_vec), dim3(256), 0, s, x, gain, eps, n, out);
+  BB_LAUNCH(k_rmsnorm, dim3((unsigned)n_vec), dim3(256), 0, s, x, gain, eps, n, out);
   return hipGetLastError();
 }
 

@@ -119,7 +119,7 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ s
 }
 
 hipError_t launch_dispatch(hipStream_t s, int n_ent, int E, const RouteBufs& rb) {
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, rb.sel, n_ent, E, rb);
+  BB_LAUNCH(k_dispatch, dim3(1), dim3(1024), 0, s, rb.sel, n_ent, E, rb);
   return hipGetLastError();
 }
 
@@ -468,9 +468,9 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   const int n_mt = ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;  // enough member tiles, a multiple of 8
   dim3 grid(n_mt, n_t64 / 2);
   if (wide)
-    hipLaunchKernelGGL((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+    BB_LAUNCH((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
   else
-    hipLaunchKernelGGL((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+    BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
   return hipGetLastError();
 }
 
@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) k_quant_rows(const float* __restrict__ x,
 hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx) {
   const size_t waves = n_rows * (size_t)(n / QK);
   if (waves == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_quant_rows, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_rows, n, q, sx);
+  BB_LAUNCH(k_quant_rows, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_rows, n, q, sx);
   return hipGetLastError();
 }
 

@@ -1,0 +1,138 @@
+"""Profiling driver and counter post-processing for the MoE kernels (not part of the product path).
+
+Two subcommands:
+
+  python3 -m bebelm_amd.perf drive --config 2 [--steps 50] [--layers 12]
+      Runs the config's MoE layer `steps` times on cuda:0 (rotating `layers` weight sets, as
+      bench.py does), then a device-to-device copy of CAL_BYTES with a known byte count. Meant
+      to run under `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`; the copy is
+      the calibration reference for those counters.
+
+  python3 -m bebelm_amd.perf traffic --fetch F.csv --write W.csv --kernel SUBSTR --config 2
+      Reads the two counter-collection CSVs, calibrates FETCH_SIZE and WRITE_SIZE against the
+      copy kernel (read = written = CAL_BYTES), and writes
+      profiles/traffic_<name>_<workload>.json with the HBM bytes per launch of the kernels whose
+      name contains SUBSTR.
+"""
+import argparse
+import collections
+import csv
+import json
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CAL_BYTES = 512 << 20
+COPY_KERNEL = "copyBuffer"
+
+
+def drive(args):
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from bebelm_amd import synth
+    from bebelm_amd.model import Context, MoeLayer
+
+    cfg = synth.CONFIGS[args.config]
+    T = cfg.tokens
+    ctx = Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    layers = [MoeLayer(ctx, synth.config_layer(args.config, seed=0, layer=l)) for l in range(args.layers)]
+    x = torch.from_numpy(synth.hidden_states(0, T)).cuda()
+    out = torch.empty_like(x)
+    for i in range(args.steps):
+        layers[i % len(layers)].forward(x, T, out)
+    torch.cuda.synchronize()
+    src = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for l in layers:
+        l.close()
+    ctx.close()
+    print("perf drive done", flush=True)
+
+
+def _per_kernel(path, counter):
+    vals = collections.defaultdict(list)
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            vals[row["Kernel_Name"]].append(float(row["Counter_Value"]))
+    return vals
+
+
+def traffic(args):
+    sys.path.insert(0, ROOT)
+    from bebelm_amd import synth
+
+    cfg = synth.CONFIGS[args.config]
+    fetch = _per_kernel(args.fetch, "FETCH_SIZE")
+    write = _per_kernel(args.write, "WRITE_SIZE")
+
+    def mean_of(d, sub):
+        xs = [v for k, vs in d.items() if sub in k for v in vs]
+        if not xs:
+            raise SystemExit(f"no dispatches of a kernel containing {sub!r}")
+        return sum(xs) / len(xs), len(xs)
+
+    # counters are in KiB per dispatch; the calibration copies are the large copy dispatches
+    # (smaller ones are the uploads of weights and constants)
+    def cal_of(d):
+        xs = [v for k, vs in d.items() if COPY_KERNEL in k for v in vs if v * 1024.0 > CAL_BYTES / 8]
+        if not xs:
+            raise SystemExit("no calibration copy found")
+        return sum(xs) / len(xs)
+
+    cal_f, cal_w = cal_of(fetch), cal_of(write)
+    f_factor = CAL_BYTES / (cal_f * 1024.0)
+    w_factor = CAL_BYTES / (cal_w * 1024.0)
+    kf, n = mean_of(fetch, args.kernel)
+    kw, _ = mean_of(write, args.kernel)
+    res = {
+        "kernel": args.kernel,
+        "workload": cfg.name,
+        "dispatches": n,
+        "fetch_kib_per_launch": kf,
+        "write_kib_per_launch": kw,
+        "copy_calibration": {"bytes_read": CAL_BYTES, "bytes_written": CAL_BYTES, "fetch_kib": cal_f,
+                             "write_kib": cal_w, "fetch_factor": f_factor, "write_factor": w_factor},
+        "hbm_read_bytes_per_launch": kf * 1024.0 * f_factor,
+        "hbm_write_bytes_per_launch": kw * 1024.0 * w_factor,
+    }
+    res["hbm_bytes_per_launch"] = res["hbm_read_bytes_per_launch"] + res["hbm_write_bytes_per_launch"]
+    if args.command_fetch:
+        res["command_fetch"] = args.command_fetch
+    if args.command_write:
+        res["command_write"] = args.command_write
+    name = args.name or args.kernel
+    out = os.path.join(ROOT, "profiles", f"traffic_{name}_{cfg.name}.json")
+    with open(out, "w") as f:
+        json.dump(res, f, indent=1)
+    print(json.dumps(res, indent=1))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    d = sub.add_parser("drive")
+    d.add_argument("--config", type=int, default=2)
+    d.add_argument("--steps", type=int, default=48)
+    d.add_argument("--layers", type=int, default=12)
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--kernel", required=True, help="substring of the kernel name")
+    t.add_argument("--name", default=None, help="name used in the output file (default: --kernel)")
+    t.add_argument("--config", type=int, default=2)
+    t.add_argument("--command-fetch", default=None)
+    t.add_argument("--command-write", default=None)
+    args = ap.parse_args()
+    drive(args) if args.cmd == "drive" else traffic(args)
+
+
+if __name__ == "__main__":
+    main()
