@@ -96,7 +96,7 @@ def cpu_baseline(run_one, T, seconds, what):
         run_one(calls)
         calls += 1
         el = time.perf_counter() - t0
-        if el >= seconds or calls >= 1000:
+        if el >= seconds or calls >= 1_000_000:
             break
     return {"value": calls * T / el, "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"{calls} calls of the C++ restatement of {what} in {el:.1f} s, OpenMP over output rows"}
