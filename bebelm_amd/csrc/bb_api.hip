@@ -94,7 +94,7 @@ struct bb_ctx {
   std::vector<hipEvent_t> event_pool;
   double kernel_ms[bb::K_COUNT] = {};
   int64_t launches[bb::K_COUNT] = {};
-  size_t batched_min_entries = 129;  // T*k from which MoE calls take the grouped-GEMM path
+  size_t batched_min_entries = 64;  // T*k from which MoE calls take the grouped-GEMM path
 };
 
 struct bb_tensor {
@@ -290,9 +290,15 @@ void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out,
   if (batched) {
     // model.rs:286-371: route all tokens, group entries by expert, grouped GEMMs, combine
     launch(c, bb::K_ROUTE_LARGE, [&] {
-      return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 16, w.xq, w.rb);
+      // tokens per routing block: the router is read once per block, but there must be
+      // enough blocks to fill the GPU
+      const int tpb = (int)std::max<size_t>(1, std::min<size_t>(16, T / 256));
+      return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, tpb, w.xq, w.rb);
     });
-    launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
+    // small batches: the GEMMs group the entries themselves; the dispatch kernel then only
+    // fills the trace's counts, offsets and permutation
+    if (bb::gemm_member_tiles((int)n_ent, m->E) > 1 || tr)
+      launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
     launch(c, bb::K_GEMM_GATEUP, [&] {
       return bb::launch_gemm_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
                                     w.rb, bb::GemmX{w.xq.q, w.xq.sx}, w.act);

@@ -15,6 +15,7 @@
 // (expert, tile) units with the next unit's weights in flight, so HBM streams while the SIMDs
 // compute.
 #include "bb_internal.h"
+#include "bb_members.h"
 #include "bb_rowlane.h"
 
 namespace bb {
@@ -159,81 +160,6 @@ hipError_t launch_route(hipStream_t s, const float* router, const float* bias, c
   return hipGetLastError();
 }
 
-// ---- dispatch: hit experts and their members ---------------------------------------------------
-// Each block reads the T*K selections once into registers (entry i = token*K + slot lives on
-// lane i%64 of wave (i/64)%8, slot k = i/512), forms the mask of selected experts, and builds
-// member lists on demand: the entries with sel == e in ascending order, the order
-// model.rs:316-322 groups them in (one ballot per 64 entries and a prefix over chunk counts).
-constexpr int SEL_REGS = MAX_ENTRIES / 512;
-
-struct SelRegs {
-  int32_t v[SEL_REGS];
-};
-
-struct SmemMembers {
-  int32_t list[MAX_ENTRIES];
-  int32_t chunk[MAX_ENTRIES / 64 + 1];
-  uint32_t mask;
-};
-
-// Uniform across the block; needs blockDim.x == 512.
-__device__ uint32_t read_selection(const int32_t* __restrict__ sel, int n_ent, SelRegs& sr, SmemMembers& sm) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  uint32_t present = 0;
-#pragma unroll
-  for (int k = 0; k < SEL_REGS; ++k) {
-    const int i = k * 512 + tid;
-    sr.v[k] = i < n_ent ? sel[i] : -1;
-    if (sr.v[k] >= 0) present |= 1u << sr.v[k];
-  }
-  if (tid == 0) sm.mask = 0;
-  __syncthreads();
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) present |= (uint32_t)__shfl_xor((int)present, o);
-  if (lane == 0) atomicOr(&sm.mask, present);
-  __syncthreads();
-  return sm.mask;
-}
-
-// Fills sm.list with the members of expert e; returns their count (uniform).
-__device__ int member_list(const SelRegs& sr, int n_ent, int e, SmemMembers& sm) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n_chunks = (n_ent + 63) >> 6;
-  unsigned long long masks[SEL_REGS];
-#pragma unroll
-  for (int k = 0; k < SEL_REGS; ++k) {
-    const int ch = k * 8 + wave;
-    masks[k] = __ballot(sr.v[k] == e);
-    if (ch < n_chunks && lane == 0) sm.chunk[ch] = __popcll(masks[k]);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      const int v = sm.chunk[ch];
-      sm.chunk[ch] = acc;
-      acc += v;
-    }
-    sm.chunk[n_chunks] = acc;
-  }
-  __syncthreads();
-  const unsigned long long lt = (1ull << lane) - 1ull;
-#pragma unroll
-  for (int k = 0; k < SEL_REGS; ++k) {
-    const int ch = k * 8 + wave;
-    if (ch < n_chunks && ((masks[k] >> lane) & 1ull)) sm.list[sm.chunk[ch] + __popcll(masks[k] & lt)] = ch * 64 + lane;
-  }
-  const int cnt = sm.chunk[n_chunks];
-  __syncthreads();
-  return cnt;
-}
-
-// Id of the u-th set bit of mask (ascending).
-__device__ __forceinline__ int nth_expert(uint32_t mask, int u) {
-  for (int k = 0; k < u; ++k) mask &= mask - 1;
-  return __builtin_ctz(mask);
-}
-
 // The dispatch of model.rs:316-322 for the route trace (counts, offsets, grouped entries).
 __device__ void publish_dispatch(const int32_t* __restrict__ sel, int n_ent, int E, RouteBufs rb) {
   __shared__ int32_t cnt[32];
@@ -292,11 +218,12 @@ enum : int { GEMV_GATEUP = 0, GEMV_DOWN = 1 };
 template <int DT, int KIND>
 __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk, size_t stride_e, int T, int H,
                                                  int F, int K, int batch_mode, int publish, int E, RouteBufs rb,
-                                                 XQBufs xq, const float* __restrict__ act_in,
-                                                 float* __restrict__ out) {
+                                                 const int8_t* __restrict__ xq_q, const float* __restrict__ xq_sx,
+                                                 const uint32_t* __restrict__ xq_pairs,
+                                                 const float* __restrict__ act_in, float* __restrict__ out) {
   using R = LaneRow<DT>;
   __shared__ SmemMembers mem;
-  __shared__ __align__(16) SmemXQ xs;
+  __shared__ __align__(16) SmemXQ xs;  // down: the members' Q8 of act
   __shared__ SmemT tv;
   const int n_ent = T * K;
   const int n_in = KIND == GEMV_GATEUP ? H : F;  // row length
@@ -310,30 +237,18 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   const int lo = (int)((long long)blockIdx.x * n_units / gridDim.x);
   const int hi = (int)((long long)(blockIdx.x + 1) * n_units / gridDim.x);
   if (lo >= hi) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool has_blk = w < nb;
   const size_t tile_bytes = (size_t)nb * R::TB_BYTES;
   auto tile_addr = [&](int e, int tile) {
     return wpk + (size_t)e * stride_e + (size_t)tile * tile_bytes + (size_t)w * R::TB_BYTES;
   };
-  // stage the XQ records of members [c0, c0 + cnt) of the current list
+  // down: stage the Q8 of the act rows of members [c0, c0 + cnt) of the current list in LDS.
+  // gate/up reads the route kernel's XQ records straight from memory with uniform (scalar)
+  // loads: every lane of a wave needs the same activations, and scalar operands of v_dot4 cost
+  // no LDS bandwidth.
   auto stage = [&](int c0, int cnt) {
-    if constexpr (KIND == GEMV_GATEUP) {
-      const int nq16 = H / 16;
-      for (int idx = tid; idx < cnt * nq16; idx += 512) {
-        const int m = idx / nq16, k = idx % nq16;
-        const size_t row = mem.list[c0 + m] / K;
-        reinterpret_cast<uint4*>(xs.q[m])[k] = reinterpret_cast<const uint4*>(xq.q + row * H)[k];
-      }
-      for (int idx = tid; idx < cnt * nb * 12; idx += 512) {
-        const int m = idx / (nb * 12), k = idx % (nb * 12);
-        xs.pairs[m][k / 12][k % 12] = xq.pairs[(size_t)(mem.list[c0 + m] / K) * nb * 12 + k];
-      }
-      for (int idx = tid; idx < cnt * nb; idx += 512) {
-        const int m = idx / nb, k = idx % nb;
-        xs.sx[m][k] = xq.sx[(size_t)(mem.list[c0 + m] / K) * nb + k];
-      }
-    } else {
+    if constexpr (KIND == GEMV_DOWN) {
       for (int task = w; task < cnt * nb; task += 8) {
         const int m = task / nb, b = task % nb;
         const float4 v = *reinterpret_cast<const float4*>(act_in + (size_t)mem.list[c0 + m] * F + b * QK + 4 * lane);
@@ -362,14 +277,23 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
     for (int c0 = 0; c0 < n_mem; c0 += MCH) {
       const int cnt = min(n_mem - c0, MCH);
       int sb = c0;  // index of member c0 in xs
-      if (n_mem > MST) {
+      if (KIND == GEMV_DOWN && n_mem > MST) {
         stage(c0, cnt);
         __syncthreads();
         sb = 0;
       }
-      if (has_blk)
-        for (int m = 0; m < cnt; ++m)
-          tv.v[m][w][lane] = R::value(B, xs.q[sb + m] + w * QK, xs.pairs[sb + m][w], xs.sx[sb + m][w]);
+      if (has_blk) {
+        if constexpr (KIND == GEMV_GATEUP) {
+          for (int m = 0; m < cnt; ++m) {
+            const int tok = __builtin_amdgcn_readfirstlane(mem.list[c0 + m] / K);
+            const size_t xb = (size_t)tok * nb + w;
+            tv.v[m][w][lane] = R::value(B, xq_q + xb * QK, xq_pairs + xb * 12, xq_sx[xb]);
+          }
+        } else {
+          for (int m = 0; m < cnt; ++m)
+            tv.v[m][w][lane] = R::value(B, xs.q[sb + m] + w * QK, xs.pairs[sb + m][w], xs.sx[sb + m][w]);
+        }
+      }
       __syncthreads();
       for (int m = w; m < cnt; m += 8) {
         float acc = start;
@@ -403,10 +327,10 @@ static hipError_t launch_experts(hipStream_t s, int dtype, const uint8_t* wpk, s
   const int grid = min(GEMV_BLOCKS, max_hit * tiles);
   if (dtype == DT_Q4_K)
     BB_LAUNCH((k_experts<DT_Q4_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
-                       publish, E, rb, xq, act_in, out);
+              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out);
   else
     BB_LAUNCH((k_experts<DT_Q6_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
-                       publish, E, rb, xq, act_in, out);
+              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out);
   return hipGetLastError();
 }
 

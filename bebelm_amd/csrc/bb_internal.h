@@ -118,6 +118,9 @@ constexpr int PF_MAX_ENTRIES = 32768;
 
 // counts/offsets/perm/hit of rb from sel (stable grouping, model.rs:316-322).
 hipError_t launch_dispatch(hipStream_t s, int n_ent, int E, const RouteBufs& rb);
+// Member tile of the grouped GEMMs in units of 16 members; 1 means the GEMMs derive the
+// grouping from rb.sel themselves and need no dispatch kernel before them.
+int gemm_member_tiles(int n_ent, int E);
 
 // Grouped expert GEMM over the members of each expert (int8 MFMA with exact integer
 // sub-dots and the reference's f32 per-block epilogue).

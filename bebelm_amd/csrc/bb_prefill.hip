@@ -21,6 +21,7 @@
 // every output a lane holds belongs to one weight row and the row's scales stay in the lane.
 #include "bb_device.h"
 #include "bb_internal.h"
+#include "bb_members.h"
 
 namespace bb {
 
@@ -172,6 +173,68 @@ __device__ void member_rows(const RouteBufs& rb, const TileInfo& ti, int K, int 
   }
 }
 
+// Small batches (member tiles of 16, at most MAX_ENTRIES entries): the block derives its tile
+// from the selections instead of a dispatch kernel's output. Counts by LDS atomics, the same
+// expert-by-expert tile enumeration as find_tile, base = the expert's first group position.
+// Needs blockDim.x == 512.
+__device__ bool small_tile(const int32_t* __restrict__ sel, int n_ent, int E, int bn, int tile, TileInfo& ti,
+                           SelRegs& sr, int32_t* cnt, int32_t* sh) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < SEL_REGS; ++k) {
+    const int i = k * 512 + tid;
+    sr.v[k] = i < n_ent ? sel[i] : -1;
+  }
+  if (tid < 32) cnt[tid] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < SEL_REGS; ++k)
+    if (sr.v[k] >= 0) atomicAdd(&cnt[sr.v[k]], 1);
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid;
+    const int c = lane < E ? cnt[lane] : 0;
+    const int nt = (c + bn - 1) / bn;
+    int incl = nt, inclc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o), vc = __shfl_up(inclc, o);
+      if (lane >= o) {
+        incl += v;
+        inclc += vc;
+      }
+    }
+    const int excl = incl - nt;
+    if (lane < E && tile >= excl && tile < incl) {
+      sh[0] = lane;
+      sh[1] = (tile - excl) * bn;
+      sh[2] = c;
+      sh[3] = inclc - c;
+    }
+    if (lane == 63) sh[4] = incl;
+  }
+  __syncthreads();
+  if (tile >= sh[4]) return false;
+  ti.e = sh[0];
+  ti.m0 = sh[1];
+  ti.g = sh[2];
+  ti.base = sh[3];
+  ti.cnt = min(bn, ti.g - ti.m0);
+  return true;
+}
+
+// member_rows from the expert's member list (entries in ascending order).
+template <int KIND>
+__device__ void member_rows_list(const int32_t* list, const TileInfo& ti, int K, int bn, int32_t* rowidx,
+                                 int32_t* outrow) {
+  for (int n = threadIdx.x; n < bn; n += blockDim.x) {
+    const int j = ti.m0 + min(n, ti.cnt - 1);
+    const int ent = list[j];
+    rowidx[n] = KIND == GEMM_GATEUP ? ent / K : ti.base + j;
+    outrow[n] = KIND == GEMM_GATEUP ? ti.base + j : ent;
+  }
+}
+
 // Bytes of q (each <= 15) times s (<= 7), per byte; the products stay below 256.
 __device__ __forceinline__ uint32_t mul_bytes(uint32_t q, uint32_t s) {
   const v2u16 a = __builtin_bit_cast(v2u16, q);
@@ -213,13 +276,11 @@ struct GemmTraits<DT_Q6_K> {
   static constexpr int TB = (int)TB6;
 };
 
-template <int DT, int MT>
-__device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
-                                           const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
+template <int DT>
+__device__ __forceinline__ void gemm_issue_w(const uint8_t* w0, size_t tile_bytes, int b, uint8_t* wb) {
   constexpr int TB = GemmTraits<DT>::TB;
-  constexpr int W_UNITS = 2 * TB / 16, X_UNITS = 16 * MT * 16;
+  constexpr int W_UNITS = 2 * TB / 16;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int nb = n_in / QK;
   for (int i = w; i < (W_UNITS + 63) / 64; i += 8) {
     const int u = i * 64 + lane;
     if (u < W_UNITS) {
@@ -227,14 +288,27 @@ __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes,
       __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB + 16 * o, wb + i * 1024, 16, 0, 0);
     }
   }
-#pragma unroll
-  for (int s = 0; s < X_UNITS / 512; ++s) {
-    const int i = w + 8 * s;
+}
+
+template <int MT>
+__device__ __forceinline__ void gemm_issue_x(GemmX x, int n_in, int b, const int32_t* rowidx, uint8_t* xb, float* sb) {
+  constexpr int X_UNITS = 16 * MT * 16;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nb = n_in / QK;
+  for (int i = w; i < X_UNITS / 64; i += 8) {
     const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
     __builtin_amdgcn_global_load_lds(x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c, xb + i * 1024, 16, 0, 0);
   }
-  if (w < (16 * MT) / 64)
+  constexpr int NBM = 16 * MT;
+  if (w < (NBM + 63) / 64 && w * 64 + lane < NBM)
     __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[w * 64 + lane] * nb + b, sb + w * 64, 4, 0, 0);
+}
+
+template <int DT, int MT>
+__device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
+                                           const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
+  gemm_issue_w<DT>(w0, tile_bytes, b, wb);
+  gemm_issue_x<MT>(x, n_in, b, rowidx, xb, sb);
 }
 
 __device__ __forceinline__ v4i read_x16(const uint8_t* xb, int m, int chunk) {
@@ -373,7 +447,8 @@ __device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, c
 
 template <int DT, int KIND, int MT>
 __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
-                                              int n_out, int E, RouteBufs rb, GemmX x, float* __restrict__ out) {
+                                              int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
+                                              float* __restrict__ out) {
   constexpr int TB = GemmTraits<DT>::TB;
   constexpr int NBM = 16 * MT;  // members per tile
   __shared__ __align__(16) uint8_t wb0[2 * TB], wb1[2 * TB];
@@ -381,26 +456,49 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   __shared__ __align__(16) float sb0[NBM], sb1[NBM];
   __shared__ int32_t rowidx[NBM], outrow[NBM];
   __shared__ int32_t sh[8];
-  // Workgroups are handed to the 8 XCDs round-robin by id. XCD k takes member tiles k, k+8, ...
-  // and sweeps all row tiles of one member tile before the next, so the member tile's
-  // activations are fetched once into that XCD's L2; the sweep direction alternates so the
-  // weights used last are used first again.
-  const int n_rt = gridDim.y, n_mt = gridDim.x;  // n_mt: an upper bound, a multiple of 8
+  // Workgroups are handed to the 8 XCDs round-robin by id. With member tiles of 16 (small
+  // batches: the weights dominate and each expert has about one member tile) consecutive ids
+  // take consecutive row tiles of one member tile, so every XCD streams an equal share of the
+  // weights. With larger member tiles XCD k takes member tiles k, k+8, ... and sweeps all row
+  // tiles of one member tile before the next, so the member tile's activations are fetched
+  // once into that XCD's L2; the sweep direction alternates so the weights used last are used
+  // first again.
+  const int n_rt = gridDim.y, n_mt = gridDim.x;  // n_mt: an upper bound (a multiple of 8 when MT > 1)
   const int lin = blockIdx.y * n_mt + blockIdx.x;
-  const int xcd = lin & 7, slot = lin >> 3;
-  const int mt_local = slot / n_rt, rt_step = slot % n_rt;
-  const int mtile = mt_local * 8 + xcd;
-  const int rtile = (mt_local & 1) ? n_rt - 1 - rt_step : rt_step;
-  TileInfo ti;
-  if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
-  member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
+  int mtile, rtile;
+  if constexpr (MT == 1) {
+    mtile = lin / n_rt;
+    rtile = lin % n_rt;
+  } else {
+    const int xcd = lin & 7, slot = lin >> 3;
+    const int mt_local = slot / n_rt, rt_step = slot % n_rt;
+    mtile = mt_local * 8 + xcd;
+    rtile = (mt_local & 1) ? n_rt - 1 - rt_step : rt_step;
+  }
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
   const int nb = n_in / QK;
   const int k64 = w >> 2, t16 = w & 3, row = 16 * t16 + r;
   const int t64 = 2 * rtile + k64;
   const size_t tile_bytes = (size_t)nb * TB;
-  const uint8_t* w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
   const int wo = k64 * TB;
+  TileInfo ti;
+  const uint8_t* w0;
+  // the first block's weights are requested as soon as the expert is known
+  if constexpr (MT == 1) {
+    __shared__ SmemMembers mem;
+    __shared__ int32_t cnt[32];
+    SelRegs sr;
+    if (!small_tile(rb.sel, n_ent, E, NBM, mtile, ti, sr, cnt, sh)) return;
+    w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+    gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    member_list(sr, n_ent, ti.e, mem);
+    member_rows_list<KIND>(mem.list, ti, K, NBM, rowidx, outrow);
+  } else {
+    if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
+    w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+    gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
+  }
   const float start = ti.g > 1 ? 0.0f : -0.0f;
   float acc[MT][4];
 #pragma unroll
@@ -412,7 +510,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     else q6_block<MT>(wb + wo, xb, sb, row, acc);
   };
   __syncthreads();  // rowidx
-  gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+  gemm_issue_x<MT>(x, n_in, 0, rowidx, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     __syncthreads();
@@ -458,19 +556,25 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   }
 }
 
-// Member tiles of 128 when the experts' groups are large enough to fill them, else 64.
+// Member tile (in units of 16 members): 128 when the groups fill it on average, 16 for
+// decode-sized batches, else 64. Tiles of 16 take their grouping from the selections.
+int gemm_member_tiles(int n_ent, int E) { return n_ent >= 128 * E ? 8 : n_ent >= 16 * E ? 4 : 1; }
+
 template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
                               int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
   const int n_ent = T * K;
-  const bool wide = n_ent >= 64 * E * 2;
-  const int bn = wide ? 128 : 64;
-  const int n_mt = ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;  // enough member tiles, a multiple of 8
+  const int mt = gemm_member_tiles(n_ent, E);
+  const int bn = 16 * mt;
+  // enough member tiles: every hit expert adds at most one partial tile
+  const int n_mt = mt == 1 ? (n_ent + bn - 1) / bn + std::min(E, n_ent) : ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;
   dim3 grid(n_mt, n_t64 / 2);
-  if (wide)
-    BB_LAUNCH((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+  if (mt == 8)
+    BB_LAUNCH((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
+  else if (mt == 4)
+    BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else
-    BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, rb, x, out);
+    BB_LAUNCH((k_gemm<DT, KIND, 1>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   return hipGetLastError();
 }
 

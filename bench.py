@@ -36,6 +36,7 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (the north-star prefill targ
 
 DECODE_KERNELS = ("gateup_swiglu", "down_combine")
 GEMM_KERNELS = ("gemm_gateup", "gemm_down")
+BATCHED_MIN_ENTRIES = 64  # the library's default T*k from which the grouped-GEMM path runs
 
 
 def parse():
@@ -121,7 +122,7 @@ def main():
     torch.cuda.set_device(dev)
     ctx = Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    batched = T * 4 >= 129
+    batched = T * 4 >= BATCHED_MIN_ENTRIES
 
     t_gen = time.perf_counter()
     x_host = synth.hidden_states(args.seed, T)
@@ -146,18 +147,21 @@ def main():
     # data-dependent hit counts (for the algorithmic byte counts)
     if args.config == 5:
         per_layer = [None]
-        xs = x_host.reshape(-1).copy()
-        from oracle import bbo
-        # routing of every MoE layer of the stack for this token, from the CPU restatement's trace
+        from bebelm_amd import kernels as kops
+        # routing of every MoE layer of the stack for this token, from the library's own route
+        # trace, layer by layer on the host-side residual stream (run_layers, model.rs:105-130)
         layers_work = []
-        h = xs.copy()
-        for g, w in spec:
-            normed = bbo.rmsnorm(h, g, 1e-5)
+        h = x_host.reshape(-1).copy()
+        for (g, w), (_, layer) in zip(spec, built):
+            normed = np.empty_like(h)
+            kops.rmsnorm(ctx, h, g, 1e-5, normed)
+            y = np.empty_like(h)
             if isinstance(w, synth.MoeWeights):
-                y, tr = bbo.moe_ffn(w, normed, trace=True)
+                tr = RouteTrace(1, w.n_experts, w.n_used)
+                layer.forward(normed, 1, y, tr)
                 layers_work.append(layer_work(w, tr.counts, 1, False))
             else:
-                y = bbo.dense_ffn(w, normed, 1)
+                layer.forward(normed, 1, y)
             h = (h + y).astype(np.float32)
         dense_bytes = sum(synth.byte_size(w.gate_dtype, w.hidden * w.ff) * 3 for w in dense_w)
         step_bytes = sum(l["step_bytes"] for l in layers_work) + dense_bytes

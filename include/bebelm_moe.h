@@ -74,7 +74,7 @@ int bb_ctx_kernel_stats(bb_ctx* ctx, int idx, const char** name, double* total_m
 int bb_ctx_reset_stats(bb_ctx* ctx);
 /* New (no counterpart in the reference, which has one CPU path): MoE calls with T*k >=
  * min_entries route all tokens, group the entries by expert and run the grouped-GEMM kernels;
- * smaller calls take the per-expert GEMV kernels. Both give the reference's bits. Default 129. */
+ * smaller calls take the per-expert GEMV kernels. Both give the reference's bits. Default 64. */
 int bb_ctx_set_batched_min_entries(bb_ctx* ctx, size_t min_entries);
 
 /* ---- weights ------------------------------------------------------------------------------ */

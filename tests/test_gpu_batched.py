@@ -17,7 +17,7 @@ from test_gpu_parity import Q4_K, Q6_K, assert_bits, check_moe, log
 
 pytestmark = pytest.mark.gpu
 
-DEFAULT_MIN_ENTRIES = 129
+DEFAULT_MIN_ENTRIES = 64
 
 
 @pytest.fixture
