@@ -209,7 +209,8 @@ struct SmemT {
 // lanes 32-63 the up rows of 32 outputs (model.rs:504-524); for down, 64 outputs of the down
 // rows (model.rs:529-548). Wave w owns super-block w of the tile. A tile's weights are
 // unpacked into registers, the next unit's loads are issued, and only then are the current
-// tile's values computed, so one tile per block is always in flight.
+// tile's values computed, so one tile per block is always in flight (the barriers below order
+// LDS only and do not wait for it).
 //
 // Members' activations: for gate/up the route kernel's XQ record of the member's token; for
 // down the member's act row, quantised here (quantize_q8 per member, model.rs:530-534).
@@ -263,7 +264,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   typename R::Loaded L;
   if (has_blk) R::load(L, tile_addr(e, tile));
   if (n_mem <= MST) stage(0, n_mem);
-  __syncthreads();
+  lds_barrier();
   for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
     if (has_blk) R::prep(B, L);
@@ -279,7 +280,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
       int sb = c0;  // index of member c0 in xs
       if (KIND == GEMV_DOWN && n_mem > MST) {
         stage(c0, cnt);
-        __syncthreads();
+        lds_barrier();
         sb = 0;
       }
       if (has_blk) {
@@ -294,7 +295,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
             tv.v[m][w][lane] = R::value(B, xs.q[sb + m] + w * QK, xs.pairs[sb + m][w], xs.sx[sb + m][w]);
         }
       }
-      __syncthreads();
+      lds_barrier();
       for (int m = w; m < cnt; m += 8) {
         float acc = start;
         for (int b = 0; b < nb; ++b) acc += tv.v[m][b][lane];
@@ -306,13 +307,13 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
           out[(size_t)ent * out_w + tile * 64 + lane] = acc;
         }
       }
-      __syncthreads();
+      lds_barrier();
     }
     if (more && u_n != u) {
       e = e_n;
       n_mem = member_list(sr, n_ent, e, mem);
       if (n_mem <= MST) stage(0, n_mem);
-      __syncthreads();
+      lds_barrier();
     }
     u = u_n;
     tile = tile_n;

@@ -44,6 +44,18 @@ __device__ __forceinline__ int q8_round(float y) {
   return (int)r;
 }
 
+// ---- block barrier for LDS traffic only ----------------------------------------------------
+// __syncthreads() also waits for every global load the wave has in flight (its release fence
+// waits on vmcnt, which counts loads and LDS-DMA copies alike). Where a barrier only orders LDS
+// accesses, this one waits for the wave's LDS operations alone, so prefetches stay in flight
+// across it. The empty asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ---- cross-lane reductions -----------------------------------------------------------------
 
 // Sum over each aligned group of 8 lanes, result in all 8 lanes (DPP: half-row mirror, then

@@ -5,6 +5,7 @@
 // selections are few (at most MAX_ENTRIES) and one block sorts them out in a few LDS passes.
 #ifndef BB_MEMBERS_H
 #define BB_MEMBERS_H
+#include "bb_device.h"
 #include "bb_internal.h"
 
 namespace bb {
@@ -44,7 +45,8 @@ __device__ inline uint32_t read_selection(const int32_t* __restrict__ sel, int n
   return sm.mask;
 }
 
-// Fills sm.list with the members of expert e; returns their count (uniform).
+// Fills sm.list with the members of expert e; returns their count (uniform). Its barriers order
+// LDS only, so loads in flight stay in flight.
 __device__ inline int member_list(const SelRegs& sr, int n_ent, int e, SmemMembers& sm) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_chunks = (n_ent + 63) >> 6;
@@ -55,7 +57,7 @@ __device__ inline int member_list(const SelRegs& sr, int n_ent, int e, SmemMembe
     masks[k] = __ballot(sr.v[k] == e);
     if (ch < n_chunks && lane == 0) sm.chunk[ch] = __popcll(masks[k]);
   }
-  __syncthreads();
+  lds_barrier();
   if (tid == 0) {
     int acc = 0;
     for (int ch = 0; ch < n_chunks; ++ch) {
@@ -65,7 +67,7 @@ __device__ inline int member_list(const SelRegs& sr, int n_ent, int e, SmemMembe
     }
     sm.chunk[n_chunks] = acc;
   }
-  __syncthreads();
+  lds_barrier();
   const unsigned long long lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int k = 0; k < SEL_REGS; ++k) {
@@ -73,7 +75,7 @@ __device__ inline int member_list(const SelRegs& sr, int n_ent, int e, SmemMembe
     if (ch < n_chunks && ((masks[k] >> lane) & 1ull)) sm.list[sm.chunk[ch] + __popcll(masks[k] & lt)] = ch * 64 + lane;
   }
   const int cnt = sm.chunk[n_chunks];
-  __syncthreads();
+  lds_barrier();
   return cnt;
 }
 

@@ -173,53 +173,28 @@ __device__ void member_rows(const RouteBufs& rb, const TileInfo& ti, int K, int 
   }
 }
 
-// Small batches (member tiles of 16, at most MAX_ENTRIES entries): the block derives its tile
-// from the selections instead of a dispatch kernel's output. Counts by LDS atomics, the same
-// expert-by-expert tile enumeration as find_tile, base = the expert's first group position.
-// Needs blockDim.x == 512.
-__device__ bool small_tile(const int32_t* __restrict__ sel, int n_ent, int E, int bn, int tile, TileInfo& ti,
-                           SelRegs& sr, int32_t* cnt, int32_t* sh) {
+// Small batches (member tiles of 16, at most MAX_ENTRIES entries): the block's unit is member
+// tile mt_e of expert e, and the block derives the tile from the selections instead of a
+// dispatch kernel's output (the grouping k_dispatch would publish): counts by LDS atomics,
+// base = the expert's first group position. The selections must have been loaded into sr.
+// Its barriers order LDS only. Needs blockDim.x == 512.
+__device__ bool expert_tile(int E, int bn, int e, int mt_e, TileInfo& ti, const SelRegs& sr, int32_t* cnt) {
   const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < SEL_REGS; ++k) {
-    const int i = k * 512 + tid;
-    sr.v[k] = i < n_ent ? sel[i] : -1;
-  }
   if (tid < 32) cnt[tid] = 0;
-  __syncthreads();
+  lds_barrier();
 #pragma unroll
   for (int k = 0; k < SEL_REGS; ++k)
     if (sr.v[k] >= 0) atomicAdd(&cnt[sr.v[k]], 1);
-  __syncthreads();
-  if (tid < 64) {
-    const int lane = tid;
-    const int c = lane < E ? cnt[lane] : 0;
-    const int nt = (c + bn - 1) / bn;
-    int incl = nt, inclc = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o), vc = __shfl_up(inclc, o);
-      if (lane >= o) {
-        incl += v;
-        inclc += vc;
-      }
-    }
-    const int excl = incl - nt;
-    if (lane < E && tile >= excl && tile < incl) {
-      sh[0] = lane;
-      sh[1] = (tile - excl) * bn;
-      sh[2] = c;
-      sh[3] = inclc - c;
-    }
-    if (lane == 63) sh[4] = incl;
-  }
-  __syncthreads();
-  if (tile >= sh[4]) return false;
-  ti.e = sh[0];
-  ti.m0 = sh[1];
-  ti.g = sh[2];
-  ti.base = sh[3];
-  ti.cnt = min(bn, ti.g - ti.m0);
+  lds_barrier();
+  const int c = cnt[e];
+  if (mt_e * bn >= c) return false;
+  int base = 0;
+  for (int x = 0; x < e; ++x) base += cnt[x];
+  ti.e = e;
+  ti.m0 = mt_e * bn;
+  ti.g = c;
+  ti.base = base;
+  ti.cnt = min(bn, c - ti.m0);
   return true;
 }
 
@@ -459,7 +434,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   // Workgroups are handed to the 8 XCDs round-robin by id. With member tiles of 16 (small
   // batches: the weights dominate and each expert has about one member tile) consecutive ids
   // take consecutive row tiles of one member tile, so every XCD streams an equal share of the
-  // weights. With larger member tiles XCD k takes member tiles k, k+8, ... and sweeps all row
+  // weights; member tile m is tile m / E of expert m % E. With larger member tiles XCD k takes member tiles k, k+8, ... and sweeps all row
   // tiles of one member tile before the next, so the member tile's activations are fetched
   // once into that XCD's L2; the sweep direction alternates so the weights used last are used
   // first again.
@@ -485,12 +460,25 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   const uint8_t* w0;
   // the first block's weights are requested as soon as the expert is known
   if constexpr (MT == 1) {
+    // unit = (expert e, its member tile mt_e, row tile): the expert is known from the block id,
+    // so the first block's weights of an expert's first member tile are requested before the
+    // selections are even read (wasted only when the expert has no member)
     __shared__ SmemMembers mem;
     __shared__ int32_t cnt[32];
+    const int e = mtile % E, mt_e = mtile / E;
+    w0 = wpk + (size_t)e * stride_e + (size_t)(2 * rtile) * tile_bytes;
     SelRegs sr;
-    if (!small_tile(rb.sel, n_ent, E, NBM, mtile, ti, sr, cnt, sh)) return;
-    w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
-    gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+#pragma unroll
+    for (int k = 0; k < SEL_REGS; ++k) {
+      const int i = k * 512 + tid;
+      sr.v[k] = i < n_ent ? rb.sel[i] : -1;
+    }
+    if (mt_e == 0) gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    if (!expert_tile(E, NBM, e, mt_e, ti, sr, cnt)) {
+      __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): no copy may land after the block's LDS is released
+      return;
+    }
+    if (mt_e > 0) gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
     member_list(sr, n_ent, ti.e, mem);
     member_rows_list<KIND>(mem.list, ti, K, NBM, rowidx, outrow);
   } else {
@@ -509,7 +497,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     if constexpr (DT == DT_Q4_K) q4_block<MT>(wb + wo, xb, sb, row, acc);
     else q6_block<MT>(wb + wo, xb, sb, row, acc);
   };
-  __syncthreads();  // rowidx
+  lds_barrier();  // rowidx; the first block's weights stay in flight
   gemm_issue_x<MT>(x, n_in, 0, rowidx, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
@@ -566,8 +554,9 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   const int n_ent = T * K;
   const int mt = gemm_member_tiles(n_ent, E);
   const int bn = 16 * mt;
-  // enough member tiles: every hit expert adds at most one partial tile
-  const int n_mt = mt == 1 ? (n_ent + bn - 1) / bn + std::min(E, n_ent) : ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;
+  // enough member tiles: with tiles of 16, ceil(T/16) per expert (an expert has at most T
+  // members); else every hit expert adds at most one partial tile
+  const int n_mt = mt == 1 ? E * ((T + bn - 1) / bn) : ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;
   dim3 grid(n_mt, n_t64 / 2);
   if (mt == 8)
     BB_LAUNCH((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
