@@ -1,0 +1,189 @@
+// bb_mfma.h — int8 MFMA building blocks of the grouped expert GEMMs (Q4_K / Q6_K rows against
+// Q8 activation rows).
+//
+// MFMA v_mfma_i32_16x16x64_i8 with the activations as A (16 members x 64 elements; lane l:
+// member l%16) and the weights as B (64 elements x 16 rows; lane l: row l%16); lane group
+// g = l/16 supplies elements 16g..16g+15 of each 64-element step for both, so a lane's weights
+// lie in one sub-block (Q4_K: 32 elements, Q6_K: 16) and its activations are one 16-byte chunk
+// of the member's row. D lane l = members 4(l/16)..+3 of row l%16.
+//
+// Operands in LDS, per 256-element super-block b:
+//   weights      the packed tile-block of the 64-row tile verbatim (chunk k of lane/row j at
+//                1024k + 16j, Q6_K's d values after the 13 chunks)
+//   activations  member m's 256 quants as 16-byte chunks, chunk c at position c ^ (m%16) of
+//                the member's 256-byte row (conflict-free 16-byte reads)
+//   scales       sx of the members
+#ifndef BB_MFMA_H
+#define BB_MFMA_H
+#include "bb_device.h"
+#include "bb_internal.h"
+
+namespace bb {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+
+enum : int { GEMM_GATEUP = 0, GEMM_DOWN = 1 };
+
+constexpr size_t TB4 = pack_tile_block_bytes(DT_Q4_K);
+constexpr size_t TB6 = pack_tile_block_bytes(DT_Q6_K);
+
+// Bytes of q (each <= 15) times s (<= 7), per byte; the products stay below 256.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t q, uint32_t s) {
+  const v2u16 a = __builtin_bit_cast(v2u16, q);
+  const v2u16 m = {(unsigned short)s, (unsigned short)s};
+  return __builtin_bit_cast(uint32_t, a * m);
+}
+
+__device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
+  return (long)(((unsigned long)hi << 32) | lo);
+}
+
+template <int DT>
+struct GemmTraits;
+template <>
+struct GemmTraits<DT_Q4_K> {
+  static constexpr int TB = (int)TB4;
+};
+template <>
+struct GemmTraits<DT_Q6_K> {
+  static constexpr int TB = (int)TB6;
+};
+
+__device__ __forceinline__ v4i read_x16(const uint8_t* xb, int m, int chunk) {
+  return *reinterpret_cast<const v4i*>(xb + m * QK + 16 * (chunk ^ (m & 15)));
+}
+
+__device__ __forceinline__ uint32_t splat_byte(uint32_t v) { return __builtin_amdgcn_perm(0u, v, 0u); }
+
+// Q4_K: sd = Σ_j sc_j·Σ q·x with sc = 8·(sc>>3) + (sc&7): both weight products stay <= 105, so
+// the high- and low-scale passes give sd = 8·Dh + Dl; a third pass with weight m_j for every
+// element of sub-block j gives sm = Σ_j m_j·S_j. Epilogue matmul.rs:242 in the reference's order.
+template <int MT>
+__device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
+                                         float (&acc)[MT][4]) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint4 hd = *reinterpret_cast<const uint4*>(wt + 16 * row);
+  const float dd = f16_bits_to_f32(hd.x & 0xffff);
+  const float dm = f16_bits_to_f32(hd.x >> 16);
+  // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time
+  const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
+  const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
+  const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+  v4i Dh[MT], Dl[MT], Dm[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = Dm[mt] = v4i{0, 0, 0, 0};
+  const int hi = g >> 1;  // high nibbles: sub-block 2c+1
+  const uint32_t nsh = 4 * hi;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int sh = 8 * (2 * (c & 1) + hi);  // byte of sub-block 2c+hi in the scale dwords
+    const uint4 qv = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * c + (g & 1)) + 16 * row);
+    const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
+                           (qv.w >> nsh) & 0x0F0F0F0Fu};
+    const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
+    const uint32_t hs = scv >> 3, ls = scv & 7u;
+    const int ms = (int)splat_byte(mw[c >> 1] >> sh);
+    v4i Bh, Bl, Bm;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      Bh[k] = (int)mul_bytes(q[k], hs);
+      Bl[k] = (int)mul_bytes(q[k], ls);
+      Bm[k] = ms;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
+      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
+      Dm[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm[mt], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
+    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sd = 8 * Dh[mt][i] + Dl[mt][i];
+      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[mt][i]));
+      acc[mt][i] += v;
+    }
+  }
+}
+
+// (hi, lo) int8 parts of sc*(q - 32) for four quant bytes q (<= 63): the products are formed
+// in 16-bit lanes (even and odd bytes) and the bytes put back in order.
+__device__ __forceinline__ void q6_split(uint32_t q, uint32_t scp, uint32_t bias, uint32_t& h, uint32_t& l) {
+  typedef short v2i16 __attribute__((ext_vector_type(2)));
+  const v2i16 ev = __builtin_bit_cast(v2i16, q & 0x00FF00FFu);
+  const v2i16 od = __builtin_bit_cast(v2i16, (q >> 8) & 0x00FF00FFu);
+  const v2i16 sc2 = __builtin_bit_cast(v2i16, scp), b2 = __builtin_bit_cast(v2i16, bias);
+  const v2i16 ae = ev * sc2 + b2, ao = od * sc2 + b2;  // sc*q - 32*sc, exact in 16 bits
+  const uint32_t ue = __builtin_bit_cast(uint32_t, ae), uo = __builtin_bit_cast(uint32_t, ao);
+  const uint32_t he = __builtin_bit_cast(uint32_t, ae >> (v2i16){6, 6});
+  const uint32_t ho = __builtin_bit_cast(uint32_t, ao >> (v2i16){6, 6});
+  // bytes {e0, o0, e1, o1} from the low bytes of the 16-bit lanes (v_perm: bytes 0-3 of the
+  // second operand, 4-7 of the first)
+  l = __builtin_amdgcn_perm(uo & 0x003F003Fu, ue & 0x003F003Fu, 0x06020400u);
+  h = __builtin_amdgcn_perm(ho, he, 0x06020400u);
+}
+
+// Q6_K: s = Σ_j sc_j·Σ (q − 32)·x. With a = sc_j·(q − 32) (|a| <= 4096) split as a = 64·h + l,
+// h in [−64, 64] and l in [0, 63] both fit int8: two passes give s = 64·Dh + Dl. Epilogue
+// matmul.rs:641: sx·(d·(float)s).
+template <int MT>
+__device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
+                                         float (&acc)[MT][4]) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint4 sc = *reinterpret_cast<const uint4*>(wt + 1024 * 12 + 16 * row);
+  const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(wt + 1024 * 13 + 2 * row));
+  v4i Dh[MT], Dl[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    // elements 64c + 16g + t = 128n + 32gq + 16(g&1) + t with n = c/2, gq = 2(c&1) + g/2
+    // (dequant.rs:122-138): ql[64n + 32(g/2) + 16(g&1) + t] (high nibble when c is odd) and
+    // bits 2gq of qh[32n + 16(g&1) + t]; sub-block j = 4c + g
+    const int n2 = c >> 1, gq = 2 * (c & 1) + (g >> 1);
+    const uint4 qlv = *reinterpret_cast<const uint4*>(wt + 1024 * (4 * n2 + 2 * (g >> 1) + (g & 1)) + 16 * row);
+    const uint4 qhv = *reinterpret_cast<const uint4*>(wt + 1024 * (8 + 2 * n2 + (g & 1)) + 16 * row);
+    const uint32_t lsh = 4 * (c & 1), hsh = 2 * gq;
+    const uint32_t scd = c == 0 ? sc.x : c == 1 ? sc.y : c == 2 ? sc.z : sc.w;
+    const int scj = (int)(int8_t)((scd >> (8 * g)) & 0xffu);
+    const uint32_t scp = ((uint32_t)scj & 0xffffu) * 0x00010001u;
+    const uint32_t bias = ((uint32_t)(-32 * scj) & 0xffffu) * 0x00010001u;
+    const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+    v4i Bh, Bl;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t q = ((qlw[k] >> lsh) & 0x0F0F0F0Fu) | (((qhw[k] >> hsh) & 0x03030303u) << 4);
+      uint32_t hh, ll;
+      q6_split(q, scp, bias, hh, ll);
+      Bh[k] = (int)hh;
+      Bl[k] = (int)ll;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
+      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
+    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sv = 64 * Dh[mt][i] + Dl[mt][i];
+      const float v = sxv[i] * (d * (float)sv);
+      acc[mt][i] += v;
+    }
+  }
+}
+
+}  // namespace bb
+#endif

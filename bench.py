@@ -36,7 +36,7 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (the north-star prefill targ
 
 DECODE_KERNELS = ("gateup_swiglu", "down_combine")
 GEMM_KERNELS = ("gemm_gateup", "gemm_down")
-BATCHED_MIN_ENTRIES = 64  # the library's default T*k from which the grouped-GEMM path runs
+BATCHED_MIN_ENTRIES = 64  # the library's default T*k from which the grouped int8-MFMA path runs
 
 
 def parse():
@@ -56,6 +56,12 @@ def q8_bytes(n):
     return n + n // 256 * 4
 
 
+def kernel_names(T, K, E, batched):
+    """The two expert kernels a call runs: per-expert GEMVs below BATCHED_MIN_ENTRIES entries,
+    grouped int8-MFMA GEMMs from there."""
+    return GEMM_KERNELS if batched else DECODE_KERNELS
+
+
 def layer_work(w, counts, T, batched):
     """Algorithmic bytes and int8 operations per kernel launch of one MoE layer.
 
@@ -72,7 +78,7 @@ def layer_work(w, counts, T, batched):
     down_b = u_hit * dn + n_ent * (F * 4 if not batched else q8_bytes(F)) + n_ent * H * 4
     gate_ops = 2.0 * n_ent * 2 * F * H
     down_ops = 2.0 * n_ent * F * H
-    names = GEMM_KERNELS if batched else DECODE_KERNELS
+    names = kernel_names(T, K, w.n_experts, batched)
     return {
         names[0]: (gate_b, gate_ops),
         names[1]: (down_b, down_ops),
@@ -200,7 +206,7 @@ def main():
         avg_ops = {n: float(np.mean([lw[n][1] for lw in layers_work])) for n in names}
         u_hit = float(np.mean([lw["u_hit"] for lw in layers_work]))
     else:
-        names = GEMM_KERNELS if batched else DECODE_KERNELS
+        names = kernel_names(T, 4, 32, batched)
         used = [per_layer[i % L] for i in range(steps)]
         avg = {n: float(np.mean([u[n][0] for u in used])) for n in names}
         avg_ops = {n: float(np.mean([u[n][1] for u in used])) for n in names}
@@ -243,7 +249,7 @@ def main():
                    "moe_ff": 1792, "experts": 32, "top_k": 4,
                    "down": "Q4_K/Q6_K alternating" if args.config == 5 else
                            ("Q6_K" if cfg.down_dtype == 14 else "Q4_K"),
-                   "path": "batched (grouped int8-MFMA GEMM)" if batched else "per-expert GEMV",
+                   "path": "grouped int8-MFMA GEMMs" if batched else "per-expert GEMV",
                    "weight_sets_rotated": L, "weight_bytes_resident": weight_bytes},
         "block_hbm_gbps": step_bytes / (ms * 1e-3) / 1e9,
         "block_frac_of_8tbs": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
