@@ -28,7 +28,10 @@ namespace bb {
 // token's x is staged in LDS (the next one prefetched) and quantised into its XQ record
 // (model.rs:501; the pair dwords only when xq.pairs is set). Then half-wave i gates token i
 // (model.rs:485-495): sigmoid, rank of score+bias by total_cmp with the lower index first on
-// exact ties, renormalisation.
+// exact ties, renormalisation. The ranks compare every lane's key with all 32 keys of its
+// half-wave read from registers; the denominator adds the selected scores in rank order. When
+// the block's tokens fit one stage, the XQ records are written by waves 8-15 while the gating
+// runs.
 constexpr int ROUTE_TPB_MAX = 16;
 constexpr int ROUTE_G = 2;  // tokens staged in LDS together (one float4 per thread)
 
@@ -37,11 +40,10 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
                                                 XQBufs xq, RouteBufs rb) {
   __shared__ __align__(16) float xs[ROUTE_G][GU_H_MAX];
   __shared__ float lg[ROUTE_TPB_MAX][32];
-  __shared__ int32_t s_key[ROUTE_TPB_MAX][32];
-  __shared__ float s_rank_s[ROUTE_TPB_MAX][8];
-  __shared__ int32_t s_rank_e[ROUTE_TPB_MAX][8];
-  __shared__ float s_rank_key[ROUTE_TPB_MAX][9];
+  __shared__ uint64_t exptab[32];
+  const uint64_t exp_e = exp_table_entry();
   const int t0 = blockIdx.x * tpb, nt = min(tpb, T - t0);
+  const bool single = nt <= ROUTE_G;  // one stage: XQ records after the logits
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int e = tid >> 5, c = tid & 31;
   const int nm = H / 32;
@@ -64,14 +66,17 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
   for (int i0 = 0; i0 < nt; i0 += ROUTE_G) {
     const int g = min(ROUTE_G, nt - i0);
     if (my_tk < ROUTE_G) reinterpret_cast<float4*>(xs[my_tk])[my_q] = xr;
+    if (i0 == 0 && tid < 32) exptab[tid] = exp_e;  // loaded before x
     __syncthreads();
     if (i0 + ROUTE_G < nt) xr = fetch(i0 + ROUTE_G);
     // XQ records of the staged tokens: one wave per 256-block
-    for (int task = wave; task < g * nbx; task += 16) {
-      const int tk = task / nbx, bk = task % nbx, t = t0 + i0 + tk;
-      const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
-      wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
-                       xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+    if (!single) {
+      for (int task = wave; task < g * nbx; task += 16) {
+        const int tk = task / nbx, bk = task % nbx, t = t0 + i0 + tk;
+        const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
+        wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                         xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+      }
     }
     for (int tk = 0; tk < g; ++tk) {
       const float* xt = xs[tk];
@@ -97,42 +102,52 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, co
     }
     __syncthreads();
   }
+  if (single && wave >= 8) {
+    // the staged tokens are still in xs: their XQ records, while waves 0-7 gate
+    for (int task = wave - 8; task < nt * nbx; task += 8) {
+      const int tk = task / nbx, bk = task % nbx, t = t0 + tk;
+      const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
+      wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                       xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+    }
+    return;
+  }
   const int i = tid >> 5;  // half-wave i gates token t0 + i
   if (i < nt) {
-    const int t = t0 + i;
+    const int t = t0 + i, half = lane >> 5;
     const bool live = c < E;
-    const float s = live ? sigmoid(lg[i][c]) : 0.0f;
+    const float s = live ? sigmoid_tab(lg[i][c], exptab) : 0.0f;
     const float key = live ? s + bias[c] : 0.0f;
     const int32_t kk = total_key(key);
-    if (live) s_key[i][c] = kk;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
     int rank = 0, eq_after = 0;
-    if (live) {
-      for (int j = 0; j < E; ++j) {
-        const int32_t kj = s_key[i][j];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int32_t k0 = __builtin_amdgcn_readlane(kk, j), k1 = __builtin_amdgcn_readlane(kk, 32 + j);
+      const int32_t kj = half ? k1 : k0;
+      if (j < E) {
         rank += (kj > kk) || (kj == kk && j < c);
         eq_after += (kj == kk && j > c);
       }
     }
-    if (live && rank < K) {
-      s_rank_s[i][rank] = s;
-      s_rank_e[i][rank] = c;
+    if (!live) rank = 64;
+    // the selected scores in rank order (the lane of rank k is unique in its half-wave)
+    auto lane_of_rank = [&](int k) {
+      const uint32_t m = (uint32_t)(__ballot(rank == k) >> (32 * half));
+      return 32 * half + (m ? __builtin_ctz(m) : 0);
+    };
+    float denom = -0.0f;
+    for (int k = 0; k < K; ++k) denom += __shfl(s, lane_of_rank(k));
+    denom = denom + 1e-6f;
+    if (rank < K) {
+      rb.sel[(size_t)t * K + rank] = c;
+      rb.wts[(size_t)t * K + rank] = s / denom;
     }
-    if (live && rank <= K) s_rank_key[i][rank] = key;
-    const int tie = (live && rank < K && eq_after > 0) ? 1 : 0;
-    const uint32_t tm = (uint32_t)(__ballot(tie) >> (lane & 32));
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+    const float key_last = __shfl(key, lane_of_rank(K - 1));
+    const float key_next = K < E ? __shfl(key, lane_of_rank(K)) : 0.0f;
+    const int tie = (rank < K && eq_after > 0) ? 1 : 0;
+    const uint32_t tm = (uint32_t)(__ballot(tie) >> (32 * half));
     if (c == 0) {
-      float denom = -0.0f;
-      for (int k = 0; k < K; ++k) denom += s_rank_s[i][k];
-      denom = denom + 1e-6f;
-      for (int k = 0; k < K; ++k) {
-        rb.sel[(size_t)t * K + k] = s_rank_e[i][k];
-        rb.wts[(size_t)t * K + k] = s_rank_s[i][k] / denom;
-      }
-      rb.margin[t] = K < E ? s_rank_key[i][K - 1] - s_rank_key[i][K] : __builtin_inff();
+      rb.margin[t] = K < E ? key_last - key_next : __builtin_inff();
       rb.ties[t] = __popc(tm);
     }
   }
@@ -226,6 +241,8 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   __shared__ SmemMembers mem;
   __shared__ __align__(16) SmemXQ xs;  // down: the members' Q8 of act
   __shared__ SmemT tv;
+  __shared__ uint64_t exptab[32];
+  const uint64_t exp_e = KIND == GEMV_GATEUP ? exp_table_entry() : 0;
   const int n_ent = T * K;
   const int n_in = KIND == GEMV_GATEUP ? H : F;  // row length
   const int nb = n_in / QK;
@@ -268,6 +285,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
     if (has_blk) R::prep(B, L);
+    if (KIND == GEMV_GATEUP && unit == lo && tid < 32) exptab[tid] = exp_e;  // loaded before the weights
     // the next unit's weights go in flight before this tile is computed
     const bool more = unit + 1 < hi;
     const int tile_n = tile + 1 == tiles ? 0 : tile + 1;
@@ -302,7 +320,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
         const int ent = mem.list[c0 + m];
         if constexpr (KIND == GEMV_GATEUP) {
           const float upv = __shfl(acc, (lane + 32) & 63);
-          if (lane < 32) out[(size_t)ent * out_w + tile * 32 + lane] = silu(acc) * upv;
+          if (lane < 32) out[(size_t)ent * out_w + tile * 32 + lane] = silu_tab(acc, exptab) * upv;
         } else {
           out[(size_t)ent * out_w + tile * 64 + lane] = acc;
         }

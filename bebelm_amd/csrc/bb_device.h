@@ -29,6 +29,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + bb_expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + bb_expf(-x)); }
 
+// The same with the exp table in LDS: kernels whose epilogue would otherwise wait for the
+// table's first read from memory load it at their start (exp_table_entry, threads 0-31) and
+// store it where they wait for their first loads anyway; a barrier then publishes it.
+__device__ __forceinline__ float sigmoid_tab(float x, const uint64_t* tab) { return 1.0f / (1.0f + bb_expf_tab(-x, tab)); }
+__device__ __forceinline__ float silu_tab(float x, const uint64_t* tab) { return x / (1.0f + bb_expf_tab(-x, tab)); }
+__device__ __forceinline__ uint64_t exp_table_entry() {
+  return threadIdx.x < 32 ? bb_exp2f_tab_dev[threadIdx.x] : 0;
+}
+
 // Rust f32::total_cmp key: signed compare of the sign-magnitude-flipped bits (-0 < +0).
 __device__ __forceinline__ int32_t total_key(float f) {
   int32_t b = (int32_t)bb_f32_bits(f);

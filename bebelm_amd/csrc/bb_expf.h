@@ -55,7 +55,8 @@ BB_HD uint64_t bb_f64_bits(double d) {
   return v.u;
 }
 
-BB_HD float bb_expf(float x) {
+// tab: the 32 table entries (kernels may pass a copy of them in LDS).
+BB_HD float bb_expf_tab(float x, const uint64_t* tab) {
   const double N = 32.0;
   const double InvLn2N = 0x1.71547652b82fep+0 * N;
   const double SHIFT = 0x1.8p+52;
@@ -75,11 +76,7 @@ BB_HD float bb_expf(float x) {
   const uint64_t ki = bb_f64_bits(kd);
   kd -= SHIFT;
   const double r = fma(InvLn2N, xd, -kd);
-#if defined(__HIPCC__)
-  uint64_t t = bb_exp2f_tab_dev[ki % 32];
-#else
-  uint64_t t = bb_exp2f_tab_host[ki % 32];
-#endif
+  uint64_t t = tab[ki % 32];
   t += ki << (52 - 5);
   const double s = bb_f64_from_bits(t);
   const double z = fma(C0, r, C1);
@@ -88,6 +85,14 @@ BB_HD float bb_expf(float x) {
   y = fma(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+BB_HD float bb_expf(float x) {
+#if defined(__HIPCC__)
+  return bb_expf_tab(x, bb_exp2f_tab_dev);
+#else
+  return bb_expf_tab(x, bb_exp2f_tab_host);
+#endif
 }
 
 #endif

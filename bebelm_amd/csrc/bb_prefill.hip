@@ -267,6 +267,8 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   __shared__ __align__(16) float sb0[NBM], sb1[NBM];
   __shared__ int32_t rowidx[NBM], outrow[NBM];
   __shared__ int32_t sh[8];
+  __shared__ uint64_t exptab[32];
+  const uint64_t exp_e = KIND == GEMM_GATEUP ? exp_table_entry() : 0;
   // Workgroups are handed to the 8 XCDs round-robin by id. With member tiles of 16 (small
   // batches: the weights dominate and each expert has about one member tile) consecutive ids
   // take consecutive row tiles of one member tile, so every XCD streams an equal share of the
@@ -337,6 +339,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   gemm_issue_x<MT>(x, n_in, 0, rowidx, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
+    if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
     __syncthreads();
     if (b + 1 < nb) gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
     block(wb0, xb0, sb0);
@@ -365,7 +368,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
           const int n = mt * 16 + 4 * g + i;
           if (n >= ti.cnt) continue;
           const float up = upv[((k64 * 2 + t16) * (4 * MT) + mt * 4 + i) * 64 + lane];
-          out[(size_t)outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu(acc[mt][i]) * up;
+          out[(size_t)outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[mt][i], exptab) * up;
         }
     }
   } else {

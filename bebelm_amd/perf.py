@@ -1,6 +1,6 @@
 """Profiling driver and counter post-processing for the MoE kernels (not part of the product path).
 
-Two subcommands:
+Three subcommands:
 
   python3 -m bebelm_amd.perf drive --config 2 [--steps 50] [--layers 12]
       Runs the config's MoE layer `steps` times on cuda:0 (rotating `layers` weight sets, as
@@ -13,6 +13,11 @@ Two subcommands:
       copy kernel (read = written = CAL_BYTES), and writes
       profiles/traffic_<name>_<workload>.json with the HBM bytes per launch of the kernels whose
       name contains SUBSTR.
+
+  python3 -m bebelm_amd.perf stats --csv S.csv --bench B.json --config 2 --command CMD
+      Writes profiles/kernel_stats_<workload>.md from a `rocprofv3 --kernel-trace --stats` run
+      of bench.py: the per-kernel table of S (the run's *_kernel_stats.csv) and the bench line
+      B that the same run printed.
 """
 import argparse
 import collections
@@ -115,6 +120,40 @@ def traffic(args):
     print(json.dumps(res, indent=1))
 
 
+def stats(args):
+    sys.path.insert(0, ROOT)
+    from bebelm_amd import synth
+
+    cfg = synth.CONFIGS[args.config]
+    rows = []
+    with open(args.csv) as f:
+        for row in csv.DictReader(f):
+            name = row["Name"].split("(")[0]
+            rows.append((name, int(row["Calls"]), float(row["AverageNs"]) / 1e3, float(row["MinNs"]) / 1e3,
+                         float(row["MaxNs"]) / 1e3, float(row["Percentage"])))
+    bench = None
+    with open(args.bench) as f:
+        for line in f:
+            line = line.strip()
+            if line.startswith("{"):
+                bench = json.loads(line)
+    keep = ("value", "unit", "ms_per_step", "kernel_us", "roofline")
+    out = [f"# Kernel statistics — config {args.config} ({cfg.name}): {cfg.description}", "",
+           "Command (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` first for "
+           "rocprofv3's scratch files):", "", "```", args.command, "```", "",
+           "Per-kernel durations over every launch of that run (the timed pass and the event-timed pass):", "",
+           "| kernel | calls | mean µs | min µs | max µs | share |", "|---|---|---|---|---|---|"]
+    for name, calls, avg, mn, mx, pct in rows:
+        out.append(f"| `{name}` | {calls} | {avg:.2f} | {mn:.2f} | {mx:.2f} | {pct:.1f}% |")
+    if bench is not None:
+        out += ["", "The bench line of the same run (HIP events stamped by each kernel's dispatch, mean µs "
+                "per launch):", "", "```", json.dumps({k: bench[k] for k in keep if k in bench}), "```"]
+    path = os.path.join(ROOT, "profiles", f"kernel_stats_{cfg.name}.md")
+    with open(path, "w") as f:
+        f.write("\n".join(out) + "\n")
+    print(path)
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -130,8 +169,13 @@ def main():
     t.add_argument("--config", type=int, default=2)
     t.add_argument("--command-fetch", default=None)
     t.add_argument("--command-write", default=None)
+    st = sub.add_parser("stats")
+    st.add_argument("--csv", required=True)
+    st.add_argument("--bench", required=True)
+    st.add_argument("--config", type=int, default=2)
+    st.add_argument("--command", required=True)
     args = ap.parse_args()
-    drive(args) if args.cmd == "drive" else traffic(args)
+    {"drive": drive, "traffic": traffic, "stats": stats}[args.cmd](args)
 
 
 if __name__ == "__main__":
