@@ -14,10 +14,11 @@ Three subcommands:
       profiles/traffic_<name>_<workload>.json with the HBM bytes per launch of the kernels whose
       name contains SUBSTR.
 
-  python3 -m bebelm_amd.perf stats --csv S.csv --bench B.json --config 2 --command CMD
-      Writes profiles/kernel_stats_<workload>.md from a `rocprofv3 --kernel-trace --stats` run
-      of bench.py: the per-kernel table of S (the run's *_kernel_stats.csv) and the bench line
-      B that the same run printed.
+  python3 -m bebelm_amd.perf stats --csv S.csv --command CMD --bench B.json --bench-command BCMD
+      Writes profiles/kernel_stats_<workload>.md: the per-kernel table of S, the
+      *_kernel_stats.csv of the `rocprofv3 --kernel-trace --stats` run CMD of bench.py, and the
+      bench line B of the unprofiled run BCMD (the profiler's own completion signals slow the
+      bench's event-timed pass, so its line comes from a run without it).
 """
 import argparse
 import collections
@@ -141,13 +142,15 @@ def stats(args):
     out = [f"# Kernel statistics — config {args.config} ({cfg.name}): {cfg.description}", "",
            "Command (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` first for "
            "rocprofv3's scratch files):", "", "```", args.command, "```", "",
-           "Per-kernel durations over every launch of that run (the timed pass and the event-timed pass):", "",
+           "Per-kernel durations over every launch of that run (bench.py's timed pass and its event-timed "
+           "pass):", "",
            "| kernel | calls | mean µs | min µs | max µs | share |", "|---|---|---|---|---|---|"]
     for name, calls, avg, mn, mx, pct in rows:
         out.append(f"| `{name}` | {calls} | {avg:.2f} | {mn:.2f} | {mx:.2f} | {pct:.1f}% |")
     if bench is not None:
-        out += ["", "The bench line of the same run (HIP events stamped by each kernel's dispatch, mean µs "
-                "per launch):", "", "```", json.dumps({k: bench[k] for k in keep if k in bench}), "```"]
+        out += ["", "The bench line (HIP events stamped by each kernel's dispatch, mean µs per launch) of the "
+                "same workload without the profiler:", "", "```", args.bench_command, "```", "", "```",
+                json.dumps({k: bench[k] for k in keep if k in bench}), "```"]
     path = os.path.join(ROOT, "profiles", f"kernel_stats_{cfg.name}.md")
     with open(path, "w") as f:
         f.write("\n".join(out) + "\n")
@@ -174,6 +177,7 @@ def main():
     st.add_argument("--bench", required=True)
     st.add_argument("--config", type=int, default=2)
     st.add_argument("--command", required=True)
+    st.add_argument("--bench-command", required=True)
     args = ap.parse_args()
     {"drive": drive, "traffic": traffic, "stats": stats}[args.cmd](args)
 
