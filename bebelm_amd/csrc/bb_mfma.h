@@ -71,9 +71,10 @@ __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, c
   const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
   const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
   const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
-  v4i Dh[MT], Dl[MT], Dm[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = Dm[mt] = v4i{0, 0, 0, 0};
+  // the lane's weight operands for the whole block first, then member tile by member tile:
+  // twelve MFMAs and the tile's f32 epilogue, which is independent of the next tile's MFMAs
+  // and can issue while they run
+  v4i Bh[4], Bl[4], Bm[4];
   const int hi = g >> 1;  // high nibbles: sub-block 2c+1
   const uint32_t nsh = 4 * hi;
 #pragma unroll
@@ -85,29 +86,29 @@ __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, c
     const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
     const uint32_t hs = scv >> 3, ls = scv & 7u;
     const int ms = (int)splat_byte(mw[c >> 1] >> sh);
-    v4i Bh, Bl, Bm;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      Bh[k] = (int)mul_bytes(q[k], hs);
-      Bl[k] = (int)mul_bytes(q[k], ls);
-      Bm[k] = ms;
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
-      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
-      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
-      Dm[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm[mt], 0, 0, 0);
+      Bh[c][k] = (int)mul_bytes(q[k], hs);
+      Bl[c][k] = (int)mul_bytes(q[k], ls);
+      Bm[c][k] = ms;
     }
   }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0}, Dm = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh[c], Dh, 0, 0, 0);
+      Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl[c], Dl, 0, 0, 0);
+      Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm[c], Dm, 0, 0, 0);
+    }
     const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
     const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int sd = 8 * Dh[mt][i] + Dl[mt][i];
-      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[mt][i]));
+      const int sd = 8 * Dh[i] + Dl[i];
+      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[i]));
       acc[mt][i] += v;
     }
   }
@@ -139,9 +140,7 @@ __device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, c
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const uint4 sc = *reinterpret_cast<const uint4*>(wt + 1024 * 12 + 16 * row);
   const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(wt + 1024 * 13 + 2 * row));
-  v4i Dh[MT], Dl[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) Dh[mt] = Dl[mt] = v4i{0, 0, 0, 0};
+  v4i Bh[4], Bl[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     // elements 64c + 16g + t = 128n + 32gq + 16(g&1) + t with n = c/2, gq = 2(c&1) + g/2
@@ -156,29 +155,29 @@ __device__ __forceinline__ void q6_block(const uint8_t* wt, const uint8_t* xb, c
     const uint32_t scp = ((uint32_t)scj & 0xffffu) * 0x00010001u;
     const uint32_t bias = ((uint32_t)(-32 * scj) & 0xffffu) * 0x00010001u;
     const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-    v4i Bh, Bl;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t q = ((qlw[k] >> lsh) & 0x0F0F0F0Fu) | (((qhw[k] >> hsh) & 0x03030303u) << 4);
       uint32_t hh, ll;
       q6_split(q, scp, bias, hh, ll);
-      Bh[k] = (int)hh;
-      Bl[k] = (int)ll;
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
-      Dh[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh[mt], 0, 0, 0);
-      Dl[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl[mt], 0, 0, 0);
+      Bh[c][k] = (int)hh;
+      Bl[c][k] = (int)ll;
     }
   }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
+      Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh[c], Dh, 0, 0, 0);
+      Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl[c], Dl, 0, 0, 0);
+    }
     const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
     const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int sv = 64 * Dh[mt][i] + Dl[mt][i];
+      const int sv = 64 * Dh[i] + Dl[i];
       const float v = sxv[i] * (d * (float)sv);
       acc[mt][i] += v;
     }

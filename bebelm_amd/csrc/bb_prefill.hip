@@ -221,50 +221,72 @@ __device__ void member_rows_list(const int32_t* list, const TileInfo& ti, int K,
 //   activations  member m's 256 quants as 16-byte chunks, chunk c at position c ^ (m%16) of
 //                the member's 256-byte row (conflict-free 16-byte reads)
 //   scales       sx of the members
-template <int DT>
-__device__ __forceinline__ void gemm_issue_w(const uint8_t* w0, size_t tile_bytes, int b, uint8_t* wb) {
-  constexpr int TB = GemmTraits<DT>::TB;
-  constexpr int W_UNITS = 2 * TB / 16;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int i = w; i < (W_UNITS + 63) / 64; i += 8) {
-    const int u = i * 64 + lane;
-    if (u < W_UNITS) {
-      const int k = u / (TB / 16), o = u % (TB / 16);
-      __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB + 16 * o, wb + i * 1024, 16, 0, 0);
-    }
-  }
-}
-
-template <int MT>
-__device__ __forceinline__ void gemm_issue_x(GemmX x, int n_in, int b, const int32_t* rowidx, uint8_t* xb, float* sb) {
-  constexpr int X_UNITS = 16 * MT * 16;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int nb = n_in / QK;
-  for (int i = w; i < X_UNITS / 64; i += 8) {
-    const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
-    __builtin_amdgcn_global_load_lds(x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c, xb + i * 1024, 16, 0, 0);
-  }
-  constexpr int NBM = 16 * MT;
-  if (w < (NBM + 63) / 64 && w * 64 + lane < NBM)
-    __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[w * 64 + lane] * nb + b, sb + w * 64, 4, 0, 0);
-}
-
+// Copies of super-block b: the two packed tile-blocks' weights, the members' activation chunks
+// and their scales, as a list of 64-lane copies. Wave w issues copies w, w+8, ... of the list,
+// OPS of them per super-block (the list is padded with repeats of the first scale copy into
+// spare bytes), so the copies a wave has in flight after a super-block are a known count.
+// PARTS selects the weight copies, the activation copies or both (the weights of the first
+// super-block are requested before the member rows are known).
 template <int DT, int MT>
+struct GemmCfg {
+  static constexpr int TB = GemmTraits<DT>::TB;
+  static constexpr int NBM = 16 * MT;
+  static constexpr int W_UNITS = 2 * TB / 16;
+  static constexpr int WCH = (W_UNITS + 63) / 64;
+  static constexpr int XCH = NBM * QK / 1024;
+  static constexpr int SCH = (NBM + 63) / 64;
+  static constexpr int OPS = (WCH + XCH + SCH + 7) / 8;
+  static constexpr int SB_FLOATS = (SCH + 1) * 64;  // scales, then the spare copies' bytes
+};
+
+enum : int { ISSUE_W = 1, ISSUE_X = 2, ISSUE_ALL = 3 };
+
+template <int DT, int MT, int PARTS>
 __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
                                            const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
-  gemm_issue_w<DT>(w0, tile_bytes, b, wb);
-  gemm_issue_x<MT>(x, n_in, b, rowidx, xb, sb);
+  using C = GemmCfg<DT, MT>;
+  constexpr int TB = C::TB;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = n_in / QK;
+#pragma unroll
+  for (int t = 0; t < C::OPS; ++t) {
+    const int j = w + 8 * t;
+    if (j < C::WCH) {
+      if (PARTS & ISSUE_W) {
+        const int u = j * 64 + lane;
+        if (u < C::W_UNITS) {
+          const int k = u / (TB / 16), o = u % (TB / 16);
+          __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB + 16 * o, wb + j * 1024, 16,
+                                           0, 0);
+        }
+      }
+    } else if (PARTS & ISSUE_X) {
+      if (j < C::WCH + C::XCH) {
+        const int i = j - C::WCH;
+        const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
+        __builtin_amdgcn_global_load_lds(x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c, xb + i * 1024, 16, 0, 0);
+      } else {
+        const int i = min(j - C::WCH - C::XCH, C::SCH);  // SCH: the spare bytes
+        const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
+        __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[m] * nb + b, sb + i * 64, 4, 0, 0);
+      }
+    }
+  }
 }
 
 template <int DT, int KIND, int MT>
 __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
                                               int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
                                               float* __restrict__ out) {
-  constexpr int TB = GemmTraits<DT>::TB;
-  constexpr int NBM = 16 * MT;  // members per tile
+  using C = GemmCfg<DT, MT>;
+  constexpr int TB = C::TB;
+  constexpr int NBM = C::NBM;  // members per tile
+  // double-buffered stages: the weights, then the activations followed by their scales
+  constexpr int XS = NBM * QK + 4 * C::SB_FLOATS;
   __shared__ __align__(16) uint8_t wb0[2 * TB], wb1[2 * TB];
-  __shared__ __align__(16) uint8_t xb0[NBM * QK], xb1[NBM * QK];
-  __shared__ __align__(16) float sb0[NBM], sb1[NBM];
+  __shared__ __align__(16) uint8_t xb0[XS], xb1[XS];
+  float* const sb0 = reinterpret_cast<float*>(xb0 + NBM * QK);
+  float* const sb1 = reinterpret_cast<float*>(xb1 + NBM * QK);
   __shared__ int32_t rowidx[NBM], outrow[NBM];
   __shared__ int32_t sh[8];
   __shared__ uint64_t exptab[32];
@@ -272,10 +294,10 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   // Workgroups are handed to the 8 XCDs round-robin by id. With member tiles of 16 (small
   // batches: the weights dominate and each expert has about one member tile) consecutive ids
   // take consecutive row tiles of one member tile, so every XCD streams an equal share of the
-  // weights; member tile m is tile m / E of expert m % E. With larger member tiles XCD k takes member tiles k, k+8, ... and sweeps all row
-  // tiles of one member tile before the next, so the member tile's activations are fetched
-  // once into that XCD's L2; the sweep direction alternates so the weights used last are used
-  // first again.
+  // weights; member tile m is tile m / E of expert m % E. With larger member tiles XCD k takes
+  // member tiles k, k+8, ... and sweeps all row tiles of one member tile before the next, so
+  // the member tile's activations are fetched once into that XCD's L2; the sweep direction
+  // alternates so the weights used last are used first again.
   const int n_rt = gridDim.y, n_mt = gridDim.x;  // n_mt: an upper bound (a multiple of 8 when MT > 1)
   const int lin = blockIdx.y * n_mt + blockIdx.x;
   int mtile, rtile;
@@ -311,18 +333,18 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
       const int i = k * 512 + tid;
       sr.v[k] = i < n_ent ? rb.sel[i] : -1;
     }
-    if (mt_e == 0) gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    if (mt_e == 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     if (!expert_tile(E, NBM, e, mt_e, ti, sr, cnt)) {
       __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): no copy may land after the block's LDS is released
       return;
     }
-    if (mt_e > 0) gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    if (mt_e > 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_list(sr, n_ent, ti.e, mem);
     member_rows_list<KIND>(mem.list, ti, K, NBM, rowidx, outrow);
   } else {
     if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
     w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
-    gemm_issue_w<DT>(w0, tile_bytes, 0, wb0);
+    gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
   }
   const float start = ti.g > 1 ? 0.0f : -0.0f;
@@ -336,17 +358,17 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     else q6_block<MT>(wb + wo, xb, sb, row, acc);
   };
   lds_barrier();  // rowidx; the first block's weights stay in flight
-  gemm_issue_x<MT>(x, n_in, 0, rowidx, xb0, sb0);
+  gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
     __syncthreads();
-    if (b + 1 < nb) gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+    if (b + 1 < nb) gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
     block(wb0, xb0, sb0);
     if (b + 1 >= nb) break;
     __builtin_amdgcn_s_waitcnt(0x3f70);
     __syncthreads();
-    if (b + 2 < nb) gemm_issue<DT, MT>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+    if (b + 2 < nb) gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
     block(wb1, xb1, sb1);
   }
   if constexpr (KIND == GEMM_GATEUP) {
@@ -383,22 +405,25 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   }
 }
 
-// Member tile (in units of 16 members): 128 when the groups fill it on average, 16 for
-// decode-sized batches, else 64. Tiles of 16 take their grouping from the selections.
-int gemm_member_tiles(int n_ent, int E) { return n_ent >= 128 * E ? 8 : n_ent >= 16 * E ? 4 : 1; }
+// Member tile (in units of 16 members): 16 for decode-sized batches (these tiles take their
+// grouping from the selections), else 64; Q6_K rows take 128 when the groups fill such tiles
+// on average. (A Q4_K block of 64 members leaves room for two blocks per CU, which beat one
+// block of 128 members: 483 vs 554 µs for config 4's gate/up. A Q6_K block of 64 members
+// still fills a CU's LDS alone.)
+int gemm_member_tiles(int n_ent, int E) { return n_ent >= 16 * E ? 4 : 1; }
 
 template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
                               int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
   const int n_ent = T * K;
-  const int mt = gemm_member_tiles(n_ent, E);
+  const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
   const int bn = 16 * mt;
   // enough member tiles: with tiles of 16, ceil(T/16) per expert (an expert has at most T
   // members); else every hit expert adds at most one partial tile
   const int n_mt = mt == 1 ? E * ((T + bn - 1) / bn) : ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;
   dim3 grid(n_mt, n_t64 / 2);
-  if (mt == 8)
-    BB_LAUNCH((k_gemm<DT, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
+  if (DT == DT_Q6_K && mt == 8)
+    BB_LAUNCH((k_gemm<DT_Q6_K, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4)
     BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else
