@@ -27,65 +27,84 @@
 namespace bb {
 
 // ---- dispatch ------------------------------------------------------------------------------------
-// One block of 1024 threads (16 waves). Per 64-entry chunk and expert a ballot count; an
-// exclusive scan over chunks per expert gives each chunk's first group position; an entry's
-// position is that plus its rank among the chunk's entries of the same expert.
+// One block of 1024 threads (16 waves); wave w takes the 64-entry chunks w, w+16, ... An entry's
+// rank among the chunk's entries of its expert comes from five ballots (one per bit of the
+// expert id, E <= 32): the lanes whose ids agree in every bit. The first entry of each expert
+// in a chunk records the chunk's count; an exclusive scan over chunks per expert (shuffles in
+// half-waves) and over experts gives each chunk's first group position, and an entry's position
+// is that plus its rank: the stable grouping of model.rs:316-322.
 __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ sel, int n_ent, int E, RouteBufs rb) {
-  constexpr int CPW = PF_MAX_ENTRIES / 64 / 16;  // chunks per wave
-  __shared__ int32_t cc[PF_MAX_ENTRIES / 64][32];
+  constexpr int NCH = PF_MAX_ENTRIES / 64;
+  constexpr int CPW = NCH / 16;  // chunks per wave
+  __shared__ int32_t cc[NCH][32];
   __shared__ int32_t part[32][33];
   __shared__ int32_t off[33];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_chunks = (n_ent + 63) >> 6;
-  // every selection this lane needs, loaded once up front (chunk wave + 16k, entry lane)
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int i = tid; i < n_chunks * 32; i += 1024) cc[i >> 5][i & 31] = 0;
   int v[CPW];
 #pragma unroll
   for (int k = 0; k < CPW; ++k) {
     const int i = (wave + 16 * k) * 64 + lane;
     v[k] = i < n_ent ? sel[i] : -1;
   }
+  __syncthreads();
+  int rank[CPW];
 #pragma unroll
   for (int k = 0; k < CPW; ++k) {
     const int ch = wave + 16 * k;
-    if (ch >= n_chunks) break;
-    int mine = 0;
-    for (int x = 0; x < E; ++x) {
-      const int c = __popcll(__ballot(v[k] == x));
-      if (lane == x) mine = c;
+    rank[k] = 0;
+    if (ch >= n_chunks) continue;
+    unsigned long long same = __ballot(v[k] >= 0);
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit) {
+      const unsigned long long b = __ballot((v[k] >> bit) & 1);
+      same &= ((v[k] >> bit) & 1) ? b : ~b;
     }
-    if (lane < 32) cc[ch][lane] = mine;
+    rank[k] = __popcll(same & lt);
+    if (v[k] >= 0 && rank[k] == 0) cc[ch][v[k]] = __popcll(same);
   }
-  if (tid < 33) off[tid] = 0;
   __syncthreads();
-  const int e = tid & 31, p = tid >> 5;  // 32 parts of the chunk range per expert
+  // thread (e = tid % 32, p = tid / 32) sums chunks [p*cpp, (p+1)*cpp) of expert e
+  const int e = tid & 31, p = tid >> 5;
   const int cpp = (n_chunks + 31) >> 5;
   const int c0 = min(p * cpp, n_chunks), c1 = min(c0 + cpp, n_chunks);
   int s = 0;
   for (int ch = c0; ch < c1; ++ch) s += cc[ch][e];
   part[e][p] = s;
   __syncthreads();
-  if (tid < 32) {
-    int acc = 0;
-    for (int q = 0; q < 32; ++q) {
-      const int x = part[tid][q];
-      part[tid][q] = acc;
-      acc += x;
+  if (wave < 16) {
+    // half-wave h of wave w scans the 32 parts of expert 2w + h
+    const int ex = 2 * wave + (lane >> 5), q = lane & 31;
+    const int val = part[ex][q];
+    int incl = val;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      const int y = __shfl_up(incl, o, 32);
+      if (q >= o) incl += y;
     }
-    part[tid][32] = acc;
+    part[ex][q] = incl - val;
+    if (q == 31) part[ex][32] = incl;
   }
   __syncthreads();
-  if (tid == 0) {
-    int acc = 0, nh = 0;
-    for (int x = 0; x < E; ++x) {
-      const int c = part[x][32];
-      rb.counts[x] = c;
-      rb.offsets[x] = acc;
-      off[x] = acc;
-      if (c) rb.hit[1 + nh++] = x;
-      acc += c;
+  if (tid < 64) {
+    const int c = tid < E ? part[tid & 31][32] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o);
+      if (tid >= o) incl += y;
     }
-    rb.offsets[E] = acc;
-    rb.hit[0] = nh;
+    const unsigned long long hitm = __ballot(c > 0);
+    if (tid < E) {
+      off[tid] = incl - c;
+      rb.counts[tid] = c;
+      rb.offsets[tid] = incl - c;
+      if (c > 0) rb.hit[1 + __popcll(hitm & ((1ull << tid) - 1ull))] = tid;
+    }
+    if (tid == E - 1) rb.offsets[E] = incl;
+    if (tid == 0) rb.hit[0] = __popcll(hitm);
   }
   __syncthreads();
   {
@@ -97,17 +116,11 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ s
     }
   }
   __syncthreads();
-  const unsigned long long lt = (1ull << lane) - 1ull;
 #pragma unroll
   for (int k = 0; k < CPW; ++k) {
     const int ch = wave + 16 * k;
     if (ch >= n_chunks) break;
-    unsigned long long mb = 0;
-    for (int x = 0; x < E; ++x) {
-      const unsigned long long b = __ballot(v[k] == x);
-      if (v[k] == x) mb = b;
-    }
-    if (v[k] >= 0) rb.perm[cc[ch][v[k]] + __popcll(mb & lt)] = ch * 64 + lane;
+    if (v[k] >= 0) rb.perm[cc[ch][v[k]] + rank[k]] = ch * 64 + lane;
   }
 }
 
