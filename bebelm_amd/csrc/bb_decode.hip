@@ -21,146 +21,157 @@
 namespace bb {
 
 // ---- router + gating + XQ of x ------------------------------------------------------------------
-// Block of 1024 threads for tpb consecutive tokens: lane (e = tid/32, c = tid%32) runs fmaf
-// chain c of router row e (matmul.rs:36-66: chains i = c mod 32, lane combine
-// (acc0+acc1)+(acc2+acc3), reduce_add ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7))). The router is held
-// regrouped by chain (built once per layer) and read once per block into registers; each
-// token's x is staged in LDS (the next one prefetched) and quantised into its XQ record
-// (model.rs:501; the pair dwords only when xq.pairs is set). Then half-wave i gates token i
-// (model.rs:485-495): sigmoid, rank of score+bias by total_cmp with the lower index first on
-// exact ties, renormalisation. The ranks compare every lane's key with all 32 keys of its
-// half-wave read from registers; the denominator adds the selected scores in rank order. When
-// the block's tokens fit one stage, the XQ records are written by waves 8-15 while the gating
-// runs.
+// Block of 1024 threads for tpb consecutive tokens. The router dot (matmul.rs:36-66) runs as 32
+// fmaf chains per (token, expert), chain c over the elements i = c mod 32, then the lane combine
+// (acc0+acc1)+(acc2+acc3) and reduce_add ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7)). Lane (e, h) of
+// wave w runs chain c = 2w + h of expert e for every token, its 64 router values in registers
+// (the router is held regrouped so these loads are contiguous per chain); the token's x is
+// staged in LDS transposed, chain-major, so the 32 lanes of a half-wave read the same 16 bytes
+// (a broadcast) for four steps of their chains. Each token's 32 x 32 chain values meet in LDS and
+// one lane per expert adds them in the reference's tree order.
+//
+// Then half-wave i gates token i (model.rs:485-495): sigmoid, rank of score+bias by total_cmp
+// with the lower index first on exact ties, renormalisation. Every lane compares its key with
+// all 32 keys of its token (LDS, broadcast reads); the denominator adds the selected scores in
+// rank order. The XQ records (model.rs:501; the pair dwords only when xq.pairs is set)
+// are written from the staged rows while the gating runs.
 constexpr int ROUTE_TPB_MAX = 16;
-constexpr int ROUTE_G = 2;  // tokens staged in LDS together (one float4 per thread)
+constexpr int XT_STRIDE = GU_H_MAX / 32 + 4;  // a chain's row in LDS, padded: chains c, c+1 on other banks
 
-__global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wc, const float* __restrict__ bias,
+__global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, const float* __restrict__ bias,
                                                 const float* __restrict__ x, int T, int H, int E, int K, int tpb,
                                                 XQBufs xq, RouteBufs rb) {
-  __shared__ __align__(16) float xs[ROUTE_G][GU_H_MAX];
+  __shared__ __align__(16) float xT[ROUTE_TPB_MAX][32][XT_STRIDE];
+  __shared__ float part[2][32][33];  // a token's chain values [expert][chain], two tokens in turn
   __shared__ float lg[ROUTE_TPB_MAX][32];
+  __shared__ __align__(16) int32_t s_key[ROUTE_TPB_MAX][32];
+  __shared__ float s_rank_s[ROUTE_TPB_MAX][8];
+  __shared__ float s_rank_key[ROUTE_TPB_MAX][9];
   __shared__ uint64_t exptab[32];
   const uint64_t exp_e = exp_table_entry();
   const int t0 = blockIdx.x * tpb, nt = min(tpb, T - t0);
-  const bool single = nt <= ROUTE_G;  // one stage: XQ records after the logits
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int e = tid >> 5, c = tid & 31;
-  const int nm = H / 32;
-  // this lane's chain operands, independent of everything below
-  float4 wv[GU_H_MAX / 32 / 4];
-  const float4* wr = reinterpret_cast<const float4*>(Wc) + (size_t)(e < E ? e : 0) * nm / 4 * 32 + c;
-#pragma unroll
-  for (int k = 0; k < GU_H_MAX / 32 / 4; ++k)
-    if (k < nm / 4) wv[k] = wr[32 * k];
-  const int nq = H / 4;  // float4 per token (<= 512)
-  const float4* x4 = reinterpret_cast<const float4*>(x);
+  const int e = lane & 31, c = 2 * wave + (lane >> 5);  // this lane's expert and chain
+  const int nm4 = H / 128;                             // float4 steps of a chain
   const int nbx = H / QK;
-  // stage s covers tokens t0 + ROUTE_G*s .. ; each thread carries one float4 of the next stage
-  const int my_tk = tid / nq, my_q = tid % nq;
-  auto fetch = [&](int i0) {
-    return (my_tk < ROUTE_G && i0 + my_tk < nt) ? x4[(size_t)(t0 + i0 + my_tk) * nq + my_q]
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
-  };
-  float4 xr = fetch(0);
-  for (int i0 = 0; i0 < nt; i0 += ROUTE_G) {
-    const int g = min(ROUTE_G, nt - i0);
-    if (my_tk < ROUTE_G) reinterpret_cast<float4*>(xs[my_tk])[my_q] = xr;
-    if (i0 == 0 && tid < 32) exptab[tid] = exp_e;  // loaded before x
-    __syncthreads();
-    if (i0 + ROUTE_G < nt) xr = fetch(i0 + ROUTE_G);
-    // XQ records of the staged tokens: one wave per 256-block
-    if (!single) {
-      for (int task = wave; task < g * nbx; task += 16) {
-        const int tk = task / nbx, bk = task % nbx, t = t0 + i0 + tk;
-        const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
-        wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
-                         xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
-      }
-    }
-    for (int tk = 0; tk < g; ++tk) {
-      const float* xt = xs[tk];
-      float acc = 0.0f;
+  const float bias_c = e < E ? bias[e] : 0.0f;
+  // the block's x rows, 4 elements per thread and step, written transposed: xT[tk][i % 32][i / 32]
+  constexpr int XSTEPS = ROUTE_TPB_MAX * GU_H_MAX / 4 / 1024;
+  float4 xr[XSTEPS];
+  const int nq = H / 4, n_x = nt * nq;
 #pragma unroll
-      for (int k = 0; k < GU_H_MAX / 32 / 4; ++k) {
-        if (k < nm / 4) {
-          acc = fmaf(wv[k].x, xt[32 * (4 * k + 0) + c], acc);
-          acc = fmaf(wv[k].y, xt[32 * (4 * k + 1) + c], acc);
-          acc = fmaf(wv[k].z, xt[32 * (4 * k + 2) + c], acc);
-          acc = fmaf(wv[k].w, xt[32 * (4 * k + 3) + c], acc);
-        }
-      }
-      const float A = acc + __shfl_down(acc, 8, 32);
-      const float v = A + __shfl_down(A, 16, 32);
-      const float u = v + __shfl_down(v, 4, 32);
-      const float y = u + __shfl_down(u, 2, 32);
-      const float r = y + __shfl_down(y, 1, 32);
-      if (c == 0 && e < E) {
-        lg[i0 + tk][e] = r;
-        rb.logits[(size_t)(t0 + i0 + tk) * E + e] = r;
+  for (int k = 0; k < XSTEPS; ++k) {
+    const int idx = k * 1024 + tid;
+    if (idx < n_x) xr[k] = reinterpret_cast<const float4*>(x)[(size_t)t0 * nq + idx];
+  }
+  float4 wv[GU_H_MAX / 128];
+  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + e;
+#pragma unroll
+  for (int k = 0; k < GU_H_MAX / 128; ++k)
+    wv[k] = (k < nm4 && e < E) ? wr[(size_t)k * E] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < XSTEPS; ++k) {
+    const int idx = k * 1024 + tid;
+    if (idx < n_x) {
+      const int tk = idx / nq, i = 4 * (idx % nq), cc = i & 31, m = i >> 5;
+      xT[tk][cc][m] = xr[k].x;
+      xT[tk][cc + 1][m] = xr[k].y;
+      xT[tk][cc + 2][m] = xr[k].z;
+      xT[tk][cc + 3][m] = xr[k].w;
+    }
+  }
+  if (tid < 32) exptab[tid] = exp_e;
+  __syncthreads();
+  for (int tk = 0; tk < nt; ++tk) {
+    const float* xc = xT[tk][c];
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < GU_H_MAX / 128; ++k) {
+      if (k < nm4) {
+        const float4 xv = *reinterpret_cast<const float4*>(xc + 4 * k);
+        acc = fmaf(wv[k].x, xv.x, acc);
+        acc = fmaf(wv[k].y, xv.y, acc);
+        acc = fmaf(wv[k].z, xv.z, acc);
+        acc = fmaf(wv[k].w, xv.w, acc);
       }
     }
-    __syncthreads();
-  }
-  if (single && wave >= 8) {
-    // the staged tokens are still in xs: their XQ records, while waves 0-7 gate
-    for (int task = wave - 8; task < nt * nbx; task += 8) {
-      const int tk = task / nbx, bk = task % nbx, t = t0 + tk;
-      const float4 v = reinterpret_cast<const float4*>(xs[tk] + bk * QK)[lane];
-      wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
-                       xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+    part[tk & 1][e][c] = acc;
+    lds_barrier();  // (not __syncthreads: it would wait for the logits stores in flight)
+    if (wave == (tk & 15) && lane < E) {
+      const float* p = part[tk & 1][lane];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (p[j] + p[j + 8]) + (p[j + 16] + p[j + 24]);
+      const float r = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+      lg[tk][lane] = r;
+      rb.logits[(size_t)(t0 + tk) * E + lane] = r;
     }
-    return;
   }
+  lds_barrier();
   const int i = tid >> 5;  // half-wave i gates token t0 + i
   if (i < nt) {
-    const int t = t0 + i, half = lane >> 5;
-    const bool live = c < E;
-    const float s = live ? sigmoid_tab(lg[i][c], exptab) : 0.0f;
-    const float key = live ? s + bias[c] : 0.0f;
+    const int t = t0 + i, cx = lane & 31;
+    const bool live = cx < E;
+    const float s = live ? sigmoid_tab(lg[i][cx], exptab) : 0.0f;
+    const float key = live ? s + bias_c : 0.0f;
     const int32_t kk = total_key(key);
+    // every lane compares its key with the 32 keys of its token, read from LDS eight at a time
+    // (the 32 lanes of a half-wave read the same words)
+    // (a wave's LDS accesses complete in order: no fence, which would also wait for the
+    // logits stores in flight)
+    s_key[i][cx] = kk;
+    asm volatile("" ::: "memory");
     int rank = 0, eq_after = 0;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const int32_t k0 = __builtin_amdgcn_readlane(kk, j), k1 = __builtin_amdgcn_readlane(kk, 32 + j);
-      const int32_t kj = half ? k1 : k0;
-      if (j < E) {
-        rank += (kj > kk) || (kj == kk && j < c);
-        eq_after += (kj == kk && j > c);
+    for (int q = 0; q < 8; ++q) {
+      const int4 k4 = reinterpret_cast<const int4*>(s_key[i])[q];
+      const int kq[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = 4 * q + u;
+        const bool in = j < E;
+        rank += (in && ((kq[u] > kk) || (kq[u] == kk && j < cx))) ? 1 : 0;
+        eq_after += (in && kq[u] == kk && j > cx) ? 1 : 0;
       }
     }
     if (!live) rank = 64;
-    // the selected scores in rank order (the lane of rank k is unique in its half-wave)
-    auto lane_of_rank = [&](int k) {
-      const uint32_t m = (uint32_t)(__ballot(rank == k) >> (32 * half));
-      return 32 * half + (m ? __builtin_ctz(m) : 0);
-    };
+    // the selected scores and the keys of ranks 0..K by rank
+    if (rank < K) s_rank_s[i][rank] = s;
+    if (rank <= K) s_rank_key[i][rank] = key;
+    asm volatile("" ::: "memory");
     float denom = -0.0f;
-    for (int k = 0; k < K; ++k) denom += __shfl(s, lane_of_rank(k));
+    for (int k = 0; k < K; ++k) denom += s_rank_s[i][k];
     denom = denom + 1e-6f;
     if (rank < K) {
-      rb.sel[(size_t)t * K + rank] = c;
+      rb.sel[(size_t)t * K + rank] = cx;
       rb.wts[(size_t)t * K + rank] = s / denom;
     }
-    const float key_last = __shfl(key, lane_of_rank(K - 1));
-    const float key_next = K < E ? __shfl(key, lane_of_rank(K)) : 0.0f;
     const int tie = (rank < K && eq_after > 0) ? 1 : 0;
-    const uint32_t tm = (uint32_t)(__ballot(tie) >> (32 * half));
-    if (c == 0) {
-      rb.margin[t] = K < E ? key_last - key_next : __builtin_inff();
+    const uint32_t tm = (uint32_t)(__ballot(tie) >> (lane & 32));
+    if (cx == 0) {
+      rb.margin[t] = K < E ? s_rank_key[i][K - 1] - s_rank_key[i][K] : __builtin_inff();
       rb.ties[t] = __popc(tm);
     }
   }
+  // XQ records of the staged rows, one wave per 256-block: the waves that gate nothing first
+  const int first = (nt + 1) / 2;  // waves 0 .. first-1 gate
+  for (int task = (wave + 16 - first) % 16; task < nt * nbx; task += 16) {
+    const int tk = task / nbx, bk = task % nbx, t = t0 + tk;
+    const int i0 = bk * QK + 4 * lane;  // elements i0 .. i0+3: chains (i0 % 32) + j, step i0 / 32
+    const float* col = &xT[tk][i0 & 31][i0 >> 5];
+    const float4 v = make_float4(col[0], col[XT_STRIDE], col[2 * XT_STRIDE], col[3 * XT_STRIDE]);
+    wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                     xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+  }
 }
 
-// Wc[e][k][c][j] = W[e][32(4k + j) + c]: the router rows regrouped so that float4 k of dot chain
-// c (elements 128k + c, +32, +64, +96) sits at float4 index 32k + c of the expert's rows, and
-// the 32 chains of an expert load 512 contiguous bytes per step (layout only).
-__global__ void k_router_chain_major(const float* __restrict__ W, int H, int E, float* __restrict__ Wc) {
+// Wr[c][k][e][j] = W[e][32(4k + j) + c]: float4 k of dot chain c of expert e (elements
+// 128k + c, +32, +64, +96), the 32 experts of a chain step contiguous (layout only).
+__global__ void k_router_chain_major(const float* __restrict__ W, int H, int E, float* __restrict__ Wr) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (size_t)E * H) return;
   const size_t e = i / H, r = i % H, c = r % 32, m = r / 32;
-  Wc[((e * (H / 128) + m / 4) * 32 + c) * 4 + m % 4] = W[i];
+  Wr[((c * (H / 128) + m / 4) * E + e) * 4 + m % 4] = W[i];
 }
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc) {
@@ -420,17 +431,24 @@ hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const ui
 // out[t][o] = Σ_k w[t,k]·slots[t*K+k][o], k ascending from +0.0 (add_scaled, elementwise.rs:12).
 __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ slots, const float* __restrict__ wts, int T,
                                                  int H, int K, float* __restrict__ out) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)T * H) return;
-  const size_t t = i / H, o = i % H;
-  float acc = 0.0f;
-  for (int k = 0; k < K; ++k) acc = acc + wts[t * K + k] * slots[(t * K + k) * H + o];
-  out[i] = acc;
+  // block (x, t): outputs 4·(256x + thread) .. +3 of token t
+  const int t = blockIdx.y, o4 = blockIdx.x * 256 + threadIdx.x;
+  if (o4 * 4 >= H) return;
+  const float4* s4 = reinterpret_cast<const float4*>(slots);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int k = 0; k < K; ++k) {
+    const float wk = wts[(size_t)t * K + k];
+    const float4 v = s4[((size_t)t * K + k) * (H / 4) + o4];
+    acc.x = acc.x + wk * v.x;
+    acc.y = acc.y + wk * v.y;
+    acc.z = acc.z + wk * v.z;
+    acc.w = acc.w + wk * v.w;
+  }
+  reinterpret_cast<float4*>(out)[(size_t)t * (H / 4) + o4] = acc;
 }
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out) {
-  BB_LAUNCH(k_combine, dim3((unsigned)(((size_t)T * H + 255) / 256)), dim3(256), 0, s, slots, wts, T, H, K,
-                     out);
+  BB_LAUNCH(k_combine, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, s, slots, wts, T, H, K, out);
   return hipGetLastError();
 }
 

@@ -43,7 +43,10 @@ __device__ __forceinline__ void wave_quantize_xq(float4 v, int8_t* __restrict__ 
   int s4 = q0 + q1 + q2 + q3;
   int t16 = s4 + __builtin_amdgcn_update_dpp(0, s4, 0xB1, 0xf, 0xf, false);  // quad [1,0,3,2]
   t16 += __builtin_amdgcn_update_dpp(0, t16, 0x4E, 0xf, 0xf, false);         // quad [2,3,0,1]
-  const int s32 = t16 + __shfl_xor(t16, 4);                                  // lanes 8j..8j+7: S_j
+  const int s32 = t16 + __builtin_amdgcn_update_dpp(0, t16, 0x141, 0xf, 0xf, false);  // lanes 8j..8j+7: S_j
+  // (half-row mirror: the other quad of the 8-lane group, whose lanes all hold its sum)
+  if (lane == 0) *sx = amax / 127.0f;
+  if (!pairs) return;
   // pair dword j is built by lane j: sources are lanes holding the two sums
   int srcA, srcB;
   bool wide;
@@ -59,8 +62,7 @@ __device__ __forceinline__ void wave_quantize_xq(float4 v, int8_t* __restrict__ 
   }
   const int a32 = __shfl(s32, srcA), b32 = __shfl(s32, srcB);
   const int a16 = __shfl(t16, srcA), b16 = __shfl(t16, srcB);
-  if (pairs && lane < 12) pairs[lane] = wide ? pack16(a32, b32) : pack16(a16, b16);
-  if (lane == 0) *sx = amax / 127.0f;
+  if (lane < 12) pairs[lane] = wide ? pack16(a32, b32) : pack16(a16, b16);
 }
 
 // ---- Q4_K row block ----------------------------------------------------------------------------
