@@ -71,6 +71,43 @@ __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, c
   const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
   const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
   const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+  if constexpr (MT == 1) {
+    // one member tile: the operands of step c feed its three MFMAs right away (fewer live
+    // registers, so more blocks fit on a CU)
+    v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0}, Dm = {0, 0, 0, 0};
+    const int hi = g >> 1;
+    const uint32_t nsh = 4 * hi;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int sh = 8 * (2 * (c & 1) + hi);
+      const uint4 qv = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * c + (g & 1)) + 16 * row);
+      const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
+                             (qv.w >> nsh) & 0x0F0F0F0Fu};
+      const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
+      const uint32_t hs = scv >> 3, ls = scv & 7u;
+      const int ms = (int)splat_byte(mw[c >> 1] >> sh);
+      v4i Bh, Bl, Bm;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        Bh[k] = (int)mul_bytes(q[k], hs);
+        Bl[k] = (int)mul_bytes(q[k], ls);
+        Bm[k] = ms;
+      }
+      const v4i ax = read_x16(xb, r, 4 * c + g);
+      Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh, 0, 0, 0);
+      Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl, 0, 0, 0);
+      Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm, 0, 0, 0);
+    }
+    const float4 sx4 = *reinterpret_cast<const float4*>(sb + 4 * g);
+    const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sd = 8 * Dh[i] + Dl[i];
+      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[i]));
+      acc[0][i] += v;
+    }
+    return;
+  }
   // the lane's weight operands for the whole block first, then member tile by member tile:
   // twelve MFMAs and the tile's f32 epilogue, which is independent of the next tile's MFMAs
   // and can issue while they run
