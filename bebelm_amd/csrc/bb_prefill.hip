@@ -166,15 +166,15 @@ __device__ bool find_tile(const RouteBufs& rb, int E, int bn, int tile, TileInfo
 }
 
 // Member rows of the tile: x row (the token for gate/up, the group position for down) and
-// output row (group position for gate/up, entry for down). Padding members repeat the last
-// real one so every load stays inside the inputs; their outputs are not stored.
+// output row (group position for gate/up, entry for down; -1: not stored). Padding members
+// repeat the last real one so every load stays inside the inputs.
 template <int KIND>
 __device__ void member_rows(const RouteBufs& rb, const TileInfo& ti, int K, int bn, int32_t* rowidx, int32_t* outrow) {
   for (int n = threadIdx.x; n < bn; n += blockDim.x) {
     const int pos = ti.base + ti.m0 + min(n, ti.cnt - 1);
     const int ent = rb.perm[pos];
     rowidx[n] = KIND == GEMM_GATEUP ? ent / K : pos;
-    outrow[n] = KIND == GEMM_GATEUP ? pos : ent;
+    outrow[n] = n < ti.cnt ? (KIND == GEMM_GATEUP ? pos : ent) : -1;
   }
 }
 
@@ -211,7 +211,7 @@ __device__ void member_rows_list(const int32_t* list, const TileInfo& ti, int K,
     const int j = ti.m0 + min(n, ti.cnt - 1);
     const int ent = list[j];
     rowidx[n] = KIND == GEMM_GATEUP ? ent / K : ti.base + j;
-    outrow[n] = KIND == GEMM_GATEUP ? ti.base + j : ent;
+    outrow[n] = n < ti.cnt ? (KIND == GEMM_GATEUP ? ti.base + j : ent) : -1;
   }
 }
 
@@ -340,6 +340,11 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     __shared__ int32_t cnt[32];
     const int e = mtile % E, mt_e = mtile / E;
     w0 = wpk + (size_t)e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+    // gate/up of at most 16 tokens: the member tile is every token of the batch (outputs of the
+    // tokens that did not choose the expert are computed and dropped), so the activations of
+    // the first block are requested with its weights, before the selections are read
+    const int n_tok = n_ent / K;
+    const bool all_tokens = KIND == GEMM_GATEUP && n_tok <= 16;
     SelRegs sr;
 #pragma unroll
     for (int k = 0; k < SEL_REGS; ++k) {
@@ -347,13 +352,25 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
       sr.v[k] = i < n_ent ? rb.sel[i] : -1;
     }
     if (mt_e == 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    if (all_tokens) {
+      if (tid < NBM) rowidx[tid] = min(tid, n_tok - 1);
+      lds_barrier();
+      gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    }
     if (!expert_tile(E, NBM, e, mt_e, ti, sr, cnt)) {
       __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): no copy may land after the block's LDS is released
       return;
     }
     if (mt_e > 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_list(sr, n_ent, ti.e, mem);
-    member_rows_list<KIND>(mem.list, ti, K, NBM, rowidx, outrow);
+    if (all_tokens) {
+      // output row of token n: its group position, or -1 when it did not choose the expert
+      if (tid < NBM) outrow[tid] = -1;
+      lds_barrier();
+      if (tid < ti.cnt) outrow[mem.list[tid] / K] = ti.base + tid;
+    } else {
+      member_rows_list<KIND>(mem.list, ti, K, NBM, rowidx, outrow);
+    }
   } else {
     if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
     w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
@@ -370,8 +387,9 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     if constexpr (DT == DT_Q4_K) q4_block<MT>(wb + wo, xb, sb, row, acc);
     else q6_block<MT>(wb + wo, xb, sb, row, acc);
   };
-  lds_barrier();  // rowidx; the first block's weights stay in flight
-  gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+  lds_barrier();  // rowidx, outrow; the first block's copies stay in flight
+  if (MT > 1 || !(KIND == GEMM_GATEUP && n_ent / K <= 16))
+    gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
@@ -401,7 +419,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int n = mt * 16 + 4 * g + i;
-          if (n >= ti.cnt) continue;
+          if (outrow[n] < 0) continue;
           const float up = upv[((k64 * 2 + t16) * (4 * MT) + mt * 4 + i) * 64 + lane];
           out[(size_t)outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[mt][i], exptab) * up;
         }
@@ -412,7 +430,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int n = mt * 16 + 4 * g + i;
-        if (n >= ti.cnt) continue;
+        if (outrow[n] < 0) continue;
         out[(size_t)outrow[n] * n_out + 64 * t64 + 16 * t16 + r] = acc[mt][i];
       }
   }
