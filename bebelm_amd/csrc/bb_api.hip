@@ -278,7 +278,9 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched) {
   return {};
 }
 
-void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr) {
+// With combine false the caller combines: the slots and weights stay in the returned workspace.
+MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr,
+                      bool combine = true) {
   need(T >= 1, BB_ERR_ARG, "T must be >= 1");
   const size_t n_ent = T * (size_t)m->K;
   const bool batched = n_ent >= c->batched_min_entries;
@@ -323,7 +325,8 @@ void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out,
                              batch_mode, w.rb, w.act, w.slots);
     });
   }
-  launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
+  if (combine)
+    launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
   if (tr) {
     const size_t E = m->E, K = m->K;
     auto cp = [&](void* dst, const void* src, size_t bytes) {
@@ -345,6 +348,7 @@ void moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out,
       *tr->ties = tot;
     }
   }
+  return w;
 }
 
 // ---- dense FFN on device pointers (model.rs:459-469 / :262-278) --------------------------------
@@ -929,11 +933,27 @@ int bb_stack_forward(bb_ctx* c, bb_stack* s, const float* x, size_t T, float* h_
     }
     with_io(c, loc, {{x, T * H * 4, true, false}, {h_out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
       check_hip(hipMemcpyAsync(s->h, d[0], T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
-      for (const bb_layer_desc& L : s->layers) {
-        launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, s->h, L.ffn_norm, s->eps, H, T, s->normed); });
-        if (L.moe) moe_forward_dev(c, L.moe, s->normed, T, s->ffn, nullptr);
-        else dense_forward_dev(c, L.dense, s->normed, T, s->ffn);
-        launch(c, bb::K_ELEMWISE, [&] { return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, s->h, s->ffn, nullptr, 0.f, T * H); });
+      const size_t nl = s->layers.size();
+      if (nl)
+        launch(c, bb::K_RMSNORM,
+               [&] { return bb::launch_rmsnorm(c->stream, s->h, s->layers[0].ffn_norm, s->eps, H, T, s->normed); });
+      for (size_t l = 0; l < nl; ++l) {
+        const bb_layer_desc& L = s->layers[l];
+        // the layer's FFN on normed, then h += its output and the next layer's rmsnorm, fused
+        const float* next_gain = l + 1 < nl ? s->layers[l + 1].ffn_norm : nullptr;
+        if (L.moe) {
+          MoeWs w = moe_forward_dev(c, L.moe, s->normed, T, nullptr, nullptr, false);
+          launch(c, bb::K_RESIDUAL_NORM, [&] {
+            return bb::launch_residual_norm(c->stream, s->h, w.slots, w.rb.wts, L.moe->K, nullptr, next_gain, s->eps, H,
+                                            T, s->normed);
+          });
+        } else {
+          dense_forward_dev(c, L.dense, s->normed, T, s->ffn);
+          launch(c, bb::K_RESIDUAL_NORM, [&] {
+            return bb::launch_residual_norm(c->stream, s->h, nullptr, nullptr, 0, s->ffn, next_gain, s->eps, H, T,
+                                            s->normed);
+          });
+        }
       }
       check_hip(hipMemcpyAsync(d[1], s->h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
     });

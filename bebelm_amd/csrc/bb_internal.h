@@ -58,6 +58,7 @@ enum KernelId : int {
   K_GEMM_GATEUP,
   K_GEMM_DOWN,
   K_COMBINE,
+  K_RESIDUAL_NORM,
   K_COUNT
 };
 const char* kernel_name(int id);
@@ -154,6 +155,9 @@ hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a,
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
                           float* out);
+// h += (slots, wts, K) combine or ffn row; then normed = rmsnorm(h, gain) unless gain is null.
+hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
+                                const float* gain, float eps, size_t n, size_t n_vec, float* normed);
 
 }  // namespace bb
 #endif

@@ -21,7 +21,7 @@ const char* kernel_name(int id) {
   static const char* names[K_COUNT] = {"route_gating",  "gateup_swiglu", "down_combine", "quantize_q8",
                                        "rows_q8",      "rows_f32",      "elementwise",  "rmsnorm",
                                        "route_large",  "dispatch",      "gemm_gateup",  "gemm_down",
-                                       "combine"};
+                                       "combine",      "residual_norm"};
   return (id >= 0 && id < K_COUNT) ? names[id] : "?";
 }
 
@@ -179,6 +179,86 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
   __syncthreads();
   const float scale = s_scale;
   for (size_t i = threadIdx.x; i < n; i += 256) ov[i] = xv[i] * scale * gain[i];
+}
+
+// The FFN path's layer boundary for one token per block (model.rs:105-130 with the operator
+// sub-layer as identity): h += y, where y is the MoE combine of the token's k slot rows in
+// selection order from +0.0 (model.rs:550-553 / :362-369) or a dense FFN output row; then the
+// next layer's rmsnorm of h (as k_rmsnorm: the same f64 partial sums and tree) unless gain is
+// null. One launch instead of combine, add_assign and rmsnorm.
+__global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, const float* __restrict__ slots,
+                                                       const float* __restrict__ wts, int K,
+                                                       const float* __restrict__ ffn, const float* __restrict__ gain,
+                                                       float eps, size_t n, float* __restrict__ normed) {
+  const size_t t = blockIdx.x;
+  float* hv = h + t * n;
+  // thread j takes elements j, j+256, ... (k_rmsnorm's order); every load is issued before the
+  // first use, so the block waits for memory once
+  constexpr int NI = GU_H_MAX / 256;
+  float hr[NI], yr[NI];
+  float wk[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) wk[k] = (slots && k < K) ? wts[t * K + k] : 0.0f;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const size_t i = threadIdx.x + 256 * it;
+    hr[it] = i < n ? hv[i] : 0.0f;
+    yr[it] = 0.0f;
+    if (!slots && i < n) yr[it] = ffn[t * n + i];
+  }
+  if (slots) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k >= K) break;
+      float sv[NI];
+#pragma unroll
+      for (int it = 0; it < NI; ++it) {
+        const size_t i = threadIdx.x + 256 * it;
+        sv[it] = i < n ? slots[(t * K + k) * n + i] : 0.0f;
+      }
+#pragma unroll
+      for (int it = 0; it < NI; ++it) yr[it] = yr[it] + wk[k] * sv[it];
+    }
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const size_t i = threadIdx.x + 256 * it;
+    if (i >= n) break;
+    const float v = hr[it] + yr[it];
+    hv[i] = v;
+    hr[it] = v;
+    ss += (double)(v * v);
+  }
+  if (!gain) return;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  __shared__ double s_part[4];
+  __shared__ float s_scale;
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float)(tot / (double)n);
+    s_scale = 1.0f / sqrtf(mean + eps);
+  }
+  __syncthreads();
+  const float scale = s_scale;
+  float* ov = normed + t * n;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const size_t i = threadIdx.x + 256 * it;
+    if (i >= n) break;
+    ov[i] = hr[it] * scale * gain[i];
+  }
+}
+
+hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
+                                const float* gain, float eps, size_t n, size_t n_vec, float* normed) {
+  if (n_vec == 0) return hipSuccess;
+  if (n > (size_t)GU_H_MAX || K > 8) return hipErrorInvalidValue;  // the kernel's register tiles
+  BB_LAUNCH(k_residual_norm, dim3((unsigned)n_vec), dim3(256), 0, s, h, slots, wts, K, ffn, gain, eps, n, normed);
+  return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
