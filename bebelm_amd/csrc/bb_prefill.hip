@@ -15,8 +15,9 @@
 //         h_j·q_k and l_j·q_k (≤ 105) fit int8, so two MFMA passes over the whole block give
 //         Dh and Dl with sd = 8·Dh + Dl. The min term sm = Σ_j m_j·S_j is a third pass whose
 //         weight for element k is m_j (the 6-bit min of its sub-block).
-//   Q6_K  s = Σ_j sc_j·Σ_{k∈j} (q_k − 32)·x_k with i8 scales: one MFMA per 16-element
-//         sub-block (q − 32 fits int8) and an exact integer multiply-add by sc_j.
+//   Q6_K  s = Σ_j sc_j·Σ_{k∈j} (q_k − 32)·x_k with i8 scales. The per-element weight
+//         a_k = sc_j·(q_k − 32) (|a_k| <= 4096) is split as a_k = 64·h_k + l_k, h_k in
+//         [−64, 64], l_k in [0, 63], both int8: two MFMA passes give s = 64·Dh + Dl.
 // The MFMA runs with the activations as the A operand and the weight rows as the B operand, so
 // every output a lane holds belongs to one weight row and the row's scales stay in the lane.
 #include "bb_device.h"
