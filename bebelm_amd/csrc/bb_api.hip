@@ -191,6 +191,8 @@ uint8_t* ensure_ws(bb_ctx* c, size_t bytes) {
     c->ws_bytes = 0;
     c->ws = static_cast<uint8_t*>(dev_alloc(bytes));
     c->ws_bytes = bytes;
+    // selections read before any route wrote them must still name experts in range
+    check_hip(hipMemset(c->ws, 0, bytes), "hipMemset");
   }
   return c->ws;
 }

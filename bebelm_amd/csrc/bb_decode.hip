@@ -20,6 +20,72 @@
 
 namespace bb {
 
+// ---- gating ----------------------------------------------------------------------------------------
+// max over each 32-lane half of the wave (all 64 lanes active); lanes < 32 get the low half's
+__device__ __forceinline__ int half_max(int v) {
+  auto dpp = [](int x, auto ctrl) {
+    return __builtin_amdgcn_update_dpp(0, x, decltype(ctrl)::value, 0xf, 0xf, false);
+  };
+  v = max(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad [1,0,3,2]
+  v = max(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad [2,3,0,1]
+  v = max(v, dpp(v, std::integral_constant<int, 0x141>{}));  // half-row mirror
+  v = max(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row mirror
+  const int lo = max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16));
+  const int hi = max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48));
+  return (threadIdx.x & 32) ? hi : lo;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Gating of one token per half-wave (model.rs:485-495): lane e of the half-wave holds expert e's
+// logit. sigmoid, key = score + bias, the top k by total_cmp in k rounds of a half-wave maximum
+// (the lowest expert index first among equal keys), weights = score / (scores summed in rank
+// order from -0.0, + 1e-6). Also the margin between the k-th and (k+1)-th keys and the number
+// of selected experts whose key another expert after them shares. Every lane of the wave
+// calls it; live is false for lanes of absent tokens or experts.
+__device__ __forceinline__ void gate_halfwave(float logit, bool live, bool tok, float bias_e, int t, int E, int K,
+                                              const uint64_t* exptab, RouteBufs rb) {
+  const int lane = threadIdx.x & 63, e = lane & 31;
+  const float s = live ? sigmoid_tab(logit, exptab) : 0.0f;
+  const float key = live ? s + bias_e : 0.0f;
+  const int32_t kk = total_key(key);
+  bool avail = live;
+  int rank = 64, ties = 0;
+  float denom = -0.0f, key_k1 = 0.0f, key_k = 0.0f;
+  const bool hi = (lane & 32) != 0;
+  const int nr = min(K + 1, E);
+  for (int rd = 0; rd < nr; ++rd) {
+    const int m = half_max(avail ? kk : -2147483647 - 1);
+    const uint64_t eq = __ballot(avail && kk == m);
+    const uint32_t e0 = (uint32_t)eq, e1 = (uint32_t)(eq >> 32);
+    const int f0 = e0 ? __builtin_ctz(e0) : 0, f1 = e1 ? __builtin_ctz(e1) : 0;
+    const float s0 = readlane_f(s, f0), s1 = readlane_f(s, 32 + f1);
+    const float k0 = readlane_f(key, f0), k1 = readlane_f(key, 32 + f1);
+    const uint32_t eh = hi ? e1 : e0;
+    if (eh != 0 && e == (hi ? f1 : f0)) {
+      rank = rd;
+      avail = false;
+    }
+    if (rd < K) {
+      if (eh != 0) denom += hi ? s1 : s0;
+      ties += __popc(eh) > 1 ? 1 : 0;
+    }
+    if (rd == K - 1) key_k1 = hi ? k1 : k0;
+    if (rd == K) key_k = hi ? k1 : k0;
+  }
+  denom = denom + 1e-6f;
+  if (live && rank < K) {
+    rb.sel[(size_t)t * K + rank] = e;
+    rb.wts[(size_t)t * K + rank] = s / denom;
+  }
+  if (tok && e == 0) {
+    rb.margin[t] = K < E ? key_k1 - key_k : __builtin_inff();
+    rb.ties[t] = ties;
+  }
+}
+
 // ---- router + gating + XQ of x ------------------------------------------------------------------
 // Block of 1024 threads for tpb consecutive tokens. The router dot (matmul.rs:36-66) runs as 32
 // fmaf chains per (token, expert), chain c over the elements i = c mod 32, then the lane combine
@@ -30,11 +96,8 @@ namespace bb {
 // (a broadcast) for four steps of their chains. Each token's 32 x 32 chain values meet in LDS and
 // one lane per expert adds them in the reference's tree order.
 //
-// Then half-wave i gates token i (model.rs:485-495): sigmoid, rank of score+bias by total_cmp
-// with the lower index first on exact ties, renormalisation. Every lane compares its key with
-// all 32 keys of its token (LDS, broadcast reads); the denominator adds the selected scores in
-// rank order. The XQ records (model.rs:501; the pair dwords only when xq.pairs is set)
-// are written from the staged rows while the gating runs.
+// Then half-wave i gates token i (gate_halfwave). The XQ records (model.rs:501; the pair dwords
+// only when xq.pairs is set) are written from the staged rows while the gating runs.
 constexpr int ROUTE_TPB_MAX = 16;
 constexpr int XT_STRIDE = GU_H_MAX / 32 + 4;  // a chain's row in LDS, padded: chains c, c+1 on other banks
 
@@ -44,9 +107,6 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
   __shared__ __align__(16) float xT[ROUTE_TPB_MAX][32][XT_STRIDE];
   __shared__ float part[2][32][33];  // a token's chain values [expert][chain], two tokens in turn
   __shared__ float lg[ROUTE_TPB_MAX][32];
-  __shared__ __align__(16) int32_t s_key[ROUTE_TPB_MAX][32];
-  __shared__ float s_rank_s[ROUTE_TPB_MAX][8];
-  __shared__ float s_rank_key[ROUTE_TPB_MAX][9];
   __shared__ uint64_t exptab[32];
   const uint64_t exp_e = exp_table_entry();
   const int t0 = blockIdx.x * tpb, nt = min(tpb, T - t0);
@@ -84,15 +144,23 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
   __syncthreads();
   for (int tk = 0; tk < nt; ++tk) {
     const float* xc = xT[tk][c];
+    // the steps' x is read eight float4 at a time, unconditionally (the row is GU_H_MAX long;
+    // steps past H/128 are not used), so the reads are issued together
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < GU_H_MAX / 128; ++k) {
-      if (k < nm4) {
-        const float4 xv = *reinterpret_cast<const float4*>(xc + 4 * k);
-        acc = fmaf(wv[k].x, xv.x, acc);
-        acc = fmaf(wv[k].y, xv.y, acc);
-        acc = fmaf(wv[k].z, xv.z, acc);
-        acc = fmaf(wv[k].w, xv.w, acc);
+    for (int h = 0; h < GU_H_MAX / 1024; ++h) {
+      float4 xv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) xv[k] = *reinterpret_cast<const float4*>(xc + 32 * h + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (8 * h + k < nm4) {
+          const float4 w = wv[8 * h + k];
+          acc = fmaf(w.x, xv[k].x, acc);
+          acc = fmaf(w.y, xv[k].y, acc);
+          acc = fmaf(w.z, xv[k].z, acc);
+          acc = fmaf(w.w, xv[k].w, acc);
+        }
       }
     }
     part[tk & 1][e][c] = acc;
@@ -108,50 +176,11 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
     }
   }
   lds_barrier();
-  const int i = tid >> 5;  // half-wave i gates token t0 + i
-  if (i < nt) {
-    const int t = t0 + i, cx = lane & 31;
-    const bool live = cx < E;
-    const float s = live ? sigmoid_tab(lg[i][cx], exptab) : 0.0f;
-    const float key = live ? s + bias_c : 0.0f;
-    const int32_t kk = total_key(key);
-    // every lane compares its key with the 32 keys of its token, read from LDS eight at a time
-    // (the 32 lanes of a half-wave read the same words)
-    // (a wave's LDS accesses complete in order: no fence, which would also wait for the
-    // logits stores in flight)
-    s_key[i][cx] = kk;
-    asm volatile("" ::: "memory");
-    int rank = 0, eq_after = 0;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int4 k4 = reinterpret_cast<const int4*>(s_key[i])[q];
-      const int kq[4] = {k4.x, k4.y, k4.z, k4.w};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = 4 * q + u;
-        const bool in = j < E;
-        rank += (in && ((kq[u] > kk) || (kq[u] == kk && j < cx))) ? 1 : 0;
-        eq_after += (in && kq[u] == kk && j > cx) ? 1 : 0;
-      }
-    }
-    if (!live) rank = 64;
-    // the selected scores and the keys of ranks 0..K by rank
-    if (rank < K) s_rank_s[i][rank] = s;
-    if (rank <= K) s_rank_key[i][rank] = key;
-    asm volatile("" ::: "memory");
-    float denom = -0.0f;
-    for (int k = 0; k < K; ++k) denom += s_rank_s[i][k];
-    denom = denom + 1e-6f;
-    if (rank < K) {
-      rb.sel[(size_t)t * K + rank] = cx;
-      rb.wts[(size_t)t * K + rank] = s / denom;
-    }
-    const int tie = (rank < K && eq_after > 0) ? 1 : 0;
-    const uint32_t tm = (uint32_t)(__ballot(tie) >> (lane & 32));
-    if (cx == 0) {
-      rb.margin[t] = K < E ? s_rank_key[i][K - 1] - s_rank_key[i][K] : __builtin_inff();
-      rb.ties[t] = __popc(tm);
-    }
+  // half-wave i gates token t0 + i
+  if (2 * wave < nt) {
+    const int i = tid >> 5;
+    const bool tok = i < nt, live = tok && e < E;
+    gate_halfwave(live ? lg[i][e] : 0.0f, live, tok, bias_c, t0 + i, E, K, exptab, rb);
   }
   // XQ records of the staged rows, one wave per 256-block: the waves that gate nothing first
   const int first = (nt + 1) / 2;  // waves 0 .. first-1 gate
