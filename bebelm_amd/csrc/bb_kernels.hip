@@ -160,25 +160,51 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
                                                  float eps, size_t n, float* __restrict__ out) {
   const float* xv = x + (size_t)blockIdx.x * n;
   float* ov = out + (size_t)blockIdx.x * n;
+  constexpr int NI = GU_H_MAX / 256;
+  const bool regs = n <= (size_t)GU_H_MAX;  // rows up to GU_H_MAX stay in registers, read once
+  float xr[NI], gr[NI];
   double ss = 0.0;
-  for (size_t i = threadIdx.x; i < n; i += 256) {
-    const float v = xv[i];
-    ss += (double)(v * v);
+  if (regs) {
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = min((size_t)(threadIdx.x + 256 * it), n - 1);  // in bounds; elements past n unused
+      xr[it] = xv[i];
+      gr[it] = gain[i];
+    }
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      if (threadIdx.x + 256 * it >= n) break;
+      ss += (double)(xr[it] * xr[it]);
+    }
+  } else {
+    for (size_t i = threadIdx.x; i < n; i += 256) {
+      const float v = xv[i];
+      ss += (double)(v * v);
+    }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   __shared__ double s_part[4];
   __shared__ float s_scale;
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) {
     const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
     const float mean = (float)(tot / (double)n);
     s_scale = 1.0f / sqrtf(mean + eps);
   }
-  __syncthreads();
+  lds_barrier();
   const float scale = s_scale;
-  for (size_t i = threadIdx.x; i < n; i += 256) ov[i] = xv[i] * scale * gain[i];
+  if (regs) {
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = threadIdx.x + 256 * it;
+      if (i >= n) break;
+      ov[i] = xr[it] * scale * gr[it];
+    }
+  } else {
+    for (size_t i = threadIdx.x; i < n; i += 256) ov[i] = xv[i] * scale * gain[i];
+  }
 }
 
 // The FFN path's layer boundary for one token per block (model.rs:105-130 with the operator
@@ -195,29 +221,41 @@ __global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, co
   // thread j takes elements j, j+256, ... (k_rmsnorm's order); every load is issued before the
   // first use, so the block waits for memory once
   constexpr int NI = GU_H_MAX / 256;
-  float hr[NI], yr[NI];
-  float wk[8];
+  float hr[NI], yr[NI], gr[NI];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) wk[k] = (slots && k < K) ? wts[t * K + k] : 0.0f;
-#pragma unroll
-  for (int it = 0; it < NI; ++it) {
-    const size_t i = threadIdx.x + 256 * it;
-    hr[it] = i < n ? hv[i] : 0.0f;
-    yr[it] = 0.0f;
-    if (!slots && i < n) yr[it] = ffn[t * n + i];
-  }
+  for (int it = 0; it < NI; ++it) gr[it] = gain ? gain[min((size_t)(threadIdx.x + 256 * it), n - 1)] : 0.0f;
   if (slots) {
+    // the K slot rows (slot indices clamped to K-1, so every load is unconditional and in
+    // bounds; slots past K are not used)
+    float wk[8], sv[8][NI];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      if (k >= K) break;
-      float sv[NI];
+      const size_t row = t * K + min(k, K - 1);
+      wk[k] = wts[row];
 #pragma unroll
       for (int it = 0; it < NI; ++it) {
-        const size_t i = threadIdx.x + 256 * it;
-        sv[it] = i < n ? slots[(t * K + k) * n + i] : 0.0f;
+        const size_t i = min((size_t)(threadIdx.x + 256 * it), n - 1);
+        sv[k][it] = slots[row * n + i];
       }
+    }
 #pragma unroll
-      for (int it = 0; it < NI; ++it) yr[it] = yr[it] + wk[k] * sv[it];
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = min((size_t)(threadIdx.x + 256 * it), n - 1);
+      hr[it] = hv[i];
+      yr[it] = 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < K) {
+#pragma unroll
+        for (int it = 0; it < NI; ++it) yr[it] = yr[it] + wk[k] * sv[k][it];
+      }
+  } else {
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = min((size_t)(threadIdx.x + 256 * it), n - 1);
+      hr[it] = hv[i];
+      yr[it] = ffn[t * n + i];
     }
   }
   double ss = 0.0;
@@ -236,20 +274,20 @@ __global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, co
   __shared__ double s_part[4];
   __shared__ float s_scale;
   if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
-  __syncthreads();
+  lds_barrier();  // (LDS only: the h stores stay in flight)
   if (threadIdx.x == 0) {
     const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
     const float mean = (float)(tot / (double)n);
     s_scale = 1.0f / sqrtf(mean + eps);
   }
-  __syncthreads();
+  lds_barrier();
   const float scale = s_scale;
   float* ov = normed + t * n;
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const size_t i = threadIdx.x + 256 * it;
     if (i >= n) break;
-    ov[i] = hr[it] * scale * gain[i];
+    ov[i] = hr[it] * scale * gr[it];
   }
 }
 
