@@ -315,10 +315,17 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
   } else {
     const int batch_mode = T > 1;
     const int max_hit = (int)std::min<size_t>((size_t)m->E, n_ent);
-    launch(c, bb::K_ROUTE, [&] {
-      return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 1, w.xq, w.rb);
-    });
+    // a few tokens: every gate/up block routes them itself
+    const bool route_in = T <= (size_t)bb::ROUTE_IN_GATEUP_MAX_T;
+    if (!route_in)
+      launch(c, bb::K_ROUTE, [&] {
+        return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 1, w.xq, w.rb);
+      });
     launch(c, bb::K_GATEUP, [&] {
+      if (route_in)
+        return bb::launch_route_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E,
+                                       m->K, max_hit, batch_mode, tr != nullptr, w.rb, m->router_cm, m->bias_dev, x,
+                                       w.act);
       return bb::launch_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
                                max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
     });

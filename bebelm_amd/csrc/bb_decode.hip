@@ -44,9 +44,11 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 // (the lowest expert index first among equal keys), weights = score / (scores summed in rank
 // order from -0.0, + 1e-6). Also the margin between the k-th and (k+1)-th keys and the number
 // of selected experts whose key another expert after them shares. Every lane of the wave
-// calls it; live is false for lanes of absent tokens or experts.
+// calls it; live is false for lanes of absent tokens or experts. The results go to rb when
+// global_out is set, and the selections also to lds_sel[t*K + rank] when it is not null.
 __device__ __forceinline__ void gate_halfwave(float logit, bool live, bool tok, float bias_e, int t, int E, int K,
-                                              const uint64_t* exptab, RouteBufs rb) {
+                                              const uint64_t* exptab, RouteBufs rb, bool global_out = true,
+                                              int32_t* lds_sel = nullptr) {
   const int lane = threadIdx.x & 63, e = lane & 31;
   const float s = live ? sigmoid_tab(logit, exptab) : 0.0f;
   const float key = live ? s + bias_e : 0.0f;
@@ -77,10 +79,13 @@ __device__ __forceinline__ void gate_halfwave(float logit, bool live, bool tok, 
   }
   denom = denom + 1e-6f;
   if (live && rank < K) {
-    rb.sel[(size_t)t * K + rank] = e;
-    rb.wts[(size_t)t * K + rank] = s / denom;
+    if (lds_sel) lds_sel[t * K + rank] = e;
+    if (global_out) {
+      rb.sel[(size_t)t * K + rank] = e;
+      rb.wts[(size_t)t * K + rank] = s / denom;
+    }
   }
-  if (tok && e == 0) {
+  if (global_out && tok && e == 0) {
     rb.margin[t] = K < E ? key_k1 - key_k : __builtin_inff();
     rb.ties[t] = ties;
   }
@@ -114,21 +119,20 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
   const int e = lane & 31, c = 2 * wave + (lane >> 5);  // this lane's expert and chain
   const int nm4 = H / 128;                             // float4 steps of a chain
   const int nbx = H / QK;
-  const float bias_c = e < E ? bias[e] : 0.0f;
+  const float bias_c = bias[min(e, E - 1)];
   // the block's x rows, 4 elements per thread and step, written transposed: xT[tk][i % 32][i / 32]
   constexpr int XSTEPS = ROUTE_TPB_MAX * GU_H_MAX / 4 / 1024;
   float4 xr[XSTEPS];
   const int nq = H / 4, n_x = nt * nq;
+  // every load is unconditional, its index clamped into bounds (values of steps past H/128 and
+  // of experts past E are not used), so the loads go out together
 #pragma unroll
-  for (int k = 0; k < XSTEPS; ++k) {
-    const int idx = k * 1024 + tid;
-    if (idx < n_x) xr[k] = reinterpret_cast<const float4*>(x)[(size_t)t0 * nq + idx];
-  }
+  for (int k = 0; k < XSTEPS; ++k)
+    xr[k] = reinterpret_cast<const float4*>(x)[(size_t)t0 * nq + min(k * 1024 + tid, n_x - 1)];
   float4 wv[GU_H_MAX / 128];
-  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + e;
+  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + min(e, E - 1);
 #pragma unroll
-  for (int k = 0; k < GU_H_MAX / 128; ++k)
-    wv[k] = (k < nm4 && e < E) ? wr[(size_t)k * E] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k = 0; k < GU_H_MAX / 128; ++k) wv[k] = wr[(size_t)min(k, nm4 - 1) * E];
 #pragma unroll
   for (int k = 0; k < XSTEPS; ++k) {
     const int idx = k * 1024 + tid;
@@ -192,6 +196,115 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
     wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
                      xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
   }
+}
+
+// ---- route inside the gate/up GEMV block (a few tokens) ------------------------------------------
+// For a few tokens the route is recomputed by every block of the gate/up GEMV instead of in a
+// kernel of its own: the router (256 KB) is read from L2 once per block, and the blocks learn
+// their experts without a launch and a round trip through memory in between. The arithmetic is
+// k_route's (the same fmaf chains over the same elements, x staged transposed in LDS, one lane
+// per expert adding the 32 chain values in the tree order, gate_halfwave) on 512 threads. The
+// XQ records of the tokens are built in LDS. Block 0 writes the route's
+// outputs (logits, selections, weights, margins, ties) for the kernels after it.
+constexpr int RT_MAX = ROUTE_IN_GATEUP_MAX_T;
+struct SmemRoute {
+  float xT[RT_MAX][32][XT_STRIDE];
+  float xdummy[64 + 3 * XT_STRIDE];  // where lanes past the rows store (keeps the stores unconditional)
+  float part[2][32][33];
+  float lg[RT_MAX][32];
+  int32_t sel[RT_MAX * 8];
+  int8_t q[RT_MAX][GU_H_MAX];
+  uint32_t pairs[RT_MAX][GU_H_MAX / QK][12];
+  float sx[RT_MAX][GU_H_MAX / QK];
+};
+
+__device__ void route_block(const float* __restrict__ Wr, const float* __restrict__ bias, const float* __restrict__ x,
+                            int T, int H, int E, int K, bool global_out, RouteBufs rb, SmemRoute& sm,
+                            uint64_t* exptab, uint64_t exp_e) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // lane group g (16 lanes) of wave w runs chain c = 4w + g of experts e0 = lane % 16 and
+  // e0 + 16: one read of x from LDS serves two experts
+  const int c = 4 * wave + (lane >> 4), e0 = lane & 15, e1 = e0 + 16;
+  const int nm4 = H / 128, nq = H / 4, n_x = T * nq, nbx = H / QK;
+  // every load is unconditional, its index clamped into bounds (values of steps past H/128 and
+  // of experts past E are not used), so the loads go out together, x first
+  const float bias_i = bias[min(tid & 31, E - 1)];
+  constexpr int XSTEPS = RT_MAX * GU_H_MAX / 4 / 512;
+  float4 xr[XSTEPS];
+#pragma unroll
+  for (int k = 0; k < XSTEPS; ++k) xr[k] = reinterpret_cast<const float4*>(x)[min(k * 512 + tid, n_x - 1)];
+  float4 wa[GU_H_MAX / 128], wb[GU_H_MAX / 128];
+  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E;
+  const int ea = min(e0, E - 1), eb = min(e1, E - 1);
+#pragma unroll
+  for (int k = 0; k < GU_H_MAX / 128; ++k) {
+    const int kc = min(k, nm4 - 1);
+    wa[k] = wr[(size_t)kc * E + ea];
+    wb[k] = wr[(size_t)kc * E + eb];
+  }
+#pragma unroll
+  for (int k = 0; k < XSTEPS; ++k) {
+    const int idx = k * 512 + tid;
+    const int tk = idx / nq, i = 4 * (idx % nq), cc = i & 31, m = i >> 5;
+    float* dst = idx < n_x ? &sm.xT[tk][cc][m] : sm.xdummy + lane;
+    dst[0] = xr[k].x;
+    dst[XT_STRIDE] = xr[k].y;
+    dst[2 * XT_STRIDE] = xr[k].z;
+    dst[3 * XT_STRIDE] = xr[k].w;
+  }
+  if (tid < 32) exptab[tid] = exp_e;
+  lds_barrier();  // (LDS only: the router loads stay in flight)
+  // the XQ records of the tokens in LDS, one wave per 256-block, while the router arrives
+  for (int task = wave; task < T * nbx; task += 8) {
+    const int tk = task / nbx, bk = task % nbx;
+    const int i0 = bk * QK + 4 * lane;
+    const float* col = &sm.xT[tk][i0 & 31][i0 >> 5];
+    const float4 v = make_float4(col[0], col[XT_STRIDE], col[2 * XT_STRIDE], col[3 * XT_STRIDE]);
+    wave_quantize_xq(v, sm.q[tk] + bk * QK, &sm.sx[tk][bk], sm.pairs[tk][bk]);
+  }
+  for (int tk = 0; tk < T; ++tk) {
+    const float* xc = sm.xT[tk][c];
+    float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+    for (int h = 0; h < GU_H_MAX / 1024; ++h) {
+      float4 xv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) xv[k] = *reinterpret_cast<const float4*>(xc + 32 * h + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (8 * h + k < nm4) {
+          const float4 wa4 = wa[8 * h + k], wb4 = wb[8 * h + k];
+          acc_a = fmaf(wa4.x, xv[k].x, acc_a);
+          acc_a = fmaf(wa4.y, xv[k].y, acc_a);
+          acc_a = fmaf(wa4.z, xv[k].z, acc_a);
+          acc_a = fmaf(wa4.w, xv[k].w, acc_a);
+          acc_b = fmaf(wb4.x, xv[k].x, acc_b);
+          acc_b = fmaf(wb4.y, xv[k].y, acc_b);
+          acc_b = fmaf(wb4.z, xv[k].z, acc_b);
+          acc_b = fmaf(wb4.w, xv[k].w, acc_b);
+        }
+      }
+    }
+    sm.part[tk & 1][e0][c] = acc_a;
+    sm.part[tk & 1][e1][c] = acc_b;
+    lds_barrier();
+    if (wave == (tk & 7) && lane < E) {
+      const float* p = sm.part[tk & 1][lane];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (p[j] + p[j + 8]) + (p[j + 16] + p[j + 24]);
+      const float r = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+      sm.lg[tk][lane] = r;
+      if (global_out) rb.logits[(size_t)tk * E + lane] = r;
+    }
+  }
+  lds_barrier();
+  if (2 * wave < T) {  // half-wave i gates token i
+    const int i = tid >> 5, e = lane & 31;
+    const bool tok = i < T, live = tok && e < E;
+    gate_halfwave(live ? sm.lg[i][e] : 0.0f, live, tok, bias_i, i, E, K, exptab, rb, global_out, sm.sel);
+  }
+  lds_barrier();
 }
 
 // Wr[c][k][e][j] = W[e][32(4k + j) + c]: float4 k of dot chain c of expert e (elements
@@ -271,12 +384,16 @@ struct SmemT {
 // down the member's act row, quantised here (quantize_q8 per member, model.rs:530-534).
 enum : int { GEMV_GATEUP = 0, GEMV_DOWN = 1 };
 
-template <int DT, int KIND>
+// With ROUTE (gate/up of at most RT_MAX tokens) the block routes the tokens itself
+// (route_block) from the router, bias and f32 rows x_in, and reads the XQ records from LDS.
+template <int DT, int KIND, bool ROUTE>
 __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk, size_t stride_e, int T, int H,
                                                  int F, int K, int batch_mode, int publish, int E, RouteBufs rb,
                                                  const int8_t* __restrict__ xq_q, const float* __restrict__ xq_sx,
                                                  const uint32_t* __restrict__ xq_pairs,
-                                                 const float* __restrict__ act_in, float* __restrict__ out) {
+                                                 const float* __restrict__ act_in, float* __restrict__ out,
+                                                 const float* __restrict__ router, const float* __restrict__ bias,
+                                                 const float* __restrict__ x_in) {
   using R = LaneRow<DT>;
   __shared__ SmemMembers mem;
   __shared__ __align__(16) SmemXQ xs;  // down: the members' Q8 of act
@@ -288,9 +405,15 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   const int nb = n_in / QK;
   const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
   const int out_w = KIND == GEMV_GATEUP ? F : H;  // output row stride
-  if (publish && blockIdx.x == 0) publish_dispatch(rb.sel, n_ent, E, rb);
+  const int32_t* sel = rb.sel;
+  __shared__ __align__(16) typename std::conditional<ROUTE, SmemRoute, char>::type rt;
+  if constexpr (ROUTE) {
+    route_block(router, bias, x_in, T, H, E, K, blockIdx.x == 0, rb, rt, exptab, exp_e);
+    sel = rt.sel;
+  }
+  if (publish && blockIdx.x == 0) publish_dispatch(sel, n_ent, E, rb);
   SelRegs sr;
-  const uint32_t mask = read_selection(rb.sel, n_ent, sr, mem);
+  const uint32_t mask = read_selection(sel, n_ent, sr, mem);
   const int n_units = __popc(mask) * tiles;
   const int lo = (int)((long long)blockIdx.x * n_units / gridDim.x);
   const int hi = (int)((long long)(blockIdx.x + 1) * n_units / gridDim.x);
@@ -325,7 +448,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
     if (has_blk) R::prep(B, L);
-    if (KIND == GEMV_GATEUP && unit == lo && tid < 32) exptab[tid] = exp_e;  // loaded before the weights
+    if (KIND == GEMV_GATEUP && !ROUTE && unit == lo && tid < 32) exptab[tid] = exp_e;  // loaded before the weights
     // the next unit's weights go in flight before this tile is computed
     const bool more = unit + 1 < hi;
     const int tile_n = tile + 1 == tiles ? 0 : tile + 1;
@@ -345,8 +468,12 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
         if constexpr (KIND == GEMV_GATEUP) {
           for (int m = 0; m < cnt; ++m) {
             const int tok = __builtin_amdgcn_readfirstlane(mem.list[c0 + m] / K);
-            const size_t xb = (size_t)tok * nb + w;
-            tv.v[m][w][lane] = R::value(B, xq_q + xb * QK, xq_pairs + xb * 12, xq_sx[xb]);
+            if constexpr (ROUTE) {
+              tv.v[m][w][lane] = R::value(B, rt.q[tok] + w * QK, rt.pairs[tok][w], rt.sx[tok][w]);
+            } else {
+              const size_t xb = (size_t)tok * nb + w;
+              tv.v[m][w][lane] = R::value(B, xq_q + xb * QK, xq_pairs + xb * 12, xq_sx[xb]);
+            }
           }
         } else {
           for (int m = 0; m < cnt; ++m)
@@ -381,15 +508,28 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
 template <int KIND>
 static hipError_t launch_experts(hipStream_t s, int dtype, const uint8_t* wpk, size_t stride_e, int T, int H, int F,
                                  int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
-                                 XQBufs xq, const float* act_in, float* out) {
+                                 XQBufs xq, const float* act_in, float* out, const float* router = nullptr,
+                                 const float* bias = nullptr, const float* x_in = nullptr) {
   const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
   const int grid = min(GEMV_BLOCKS, max_hit * tiles);
+  if constexpr (KIND == GEMV_GATEUP) {
+    if (router) {
+      if (T > RT_MAX || E > 32 || K > 8 || H > GU_H_MAX) return hipErrorInvalidValue;
+      if (dtype == DT_Q4_K)
+        BB_LAUNCH((k_experts<DT_Q4_K, KIND, true>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+                  batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
+      else
+        BB_LAUNCH((k_experts<DT_Q6_K, KIND, true>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+                  batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
+      return hipGetLastError();
+    }
+  }
   if (dtype == DT_Q4_K)
-    BB_LAUNCH((k_experts<DT_Q4_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
-              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out);
+    BB_LAUNCH((k_experts<DT_Q4_K, KIND, false>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, nullptr, nullptr, nullptr);
   else
-    BB_LAUNCH((k_experts<DT_Q6_K, KIND>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
-              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out);
+    BB_LAUNCH((k_experts<DT_Q6_K, KIND, false>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+              publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, nullptr, nullptr, nullptr);
   return hipGetLastError();
 }
 
@@ -397,6 +537,13 @@ hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t str
                          int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb, XQBufs xq, float* act) {
   return launch_experts<GEMV_GATEUP>(s, dtype, gu, stride_gu, T, H, F, E, K, max_hit, batch_mode, publish, rb, xq,
                                      nullptr, act);
+}
+
+hipError_t launch_route_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
+                               int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
+                               const float* router, const float* bias, const float* x, float* act) {
+  return launch_experts<GEMV_GATEUP>(s, dtype, gu, stride_gu, T, H, F, E, K, max_hit, batch_mode, publish, rb,
+                                     XQBufs{}, nullptr, act, router, bias, x);
 }
 
 hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,

@@ -37,7 +37,7 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + bb_expf(-x))
 __device__ __forceinline__ float sigmoid_tab(float x, const uint64_t* tab) { return 1.0f / (1.0f + bb_expf_tab(-x, tab)); }
 __device__ __forceinline__ float silu_tab(float x, const uint64_t* tab) { return x / (1.0f + bb_expf_tab(-x, tab)); }
 __device__ __forceinline__ uint64_t exp_table_entry() {
-  return threadIdx.x < 32 ? bb_exp2f_tab_dev[threadIdx.x] : 0;
+  return bb_exp2f_tab_dev[threadIdx.x & 31];  // unconditional: other loads are not held behind it
 }
 
 // Rust f32::total_cmp key: signed compare of the sign-magnitude-flipped bits (-0 < +0).

@@ -106,6 +106,13 @@ hipError_t launch_route(hipStream_t s, const float* router, const float* bias, c
 
 hipError_t launch_router_chain_major(hipStream_t s, const float* W, int H, int E, float* Wc);
 
+// Gate/up GEMV of at most ROUTE_IN_GATEUP_MAX_T tokens that routes the tokens itself (route
+// of launch_route, rb written by the first block): no launch_route before it.
+constexpr int ROUTE_IN_GATEUP_MAX_T = 4;
+hipError_t launch_route_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
+                               int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
+                               const float* router, const float* bias, const float* x, float* act);
+
 // gu / dn: tile-packed gate+up and down tensors; stride_*: packed bytes per expert.
 hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F, int E,
                          int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb, XQBufs xq, float* act);

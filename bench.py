@@ -37,6 +37,7 @@ BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (the north-star prefill targ
 DECODE_KERNELS = ("gateup_swiglu", "down_combine")
 GEMM_KERNELS = ("gemm_gateup", "gemm_down")
 BATCHED_MIN_ENTRIES = 64  # the library's default T*k from which the grouped int8-MFMA path runs
+ROUTE_IN_GATEUP_MAX_T = 4  # up to this many tokens the gate/up GEMV routes them itself
 
 
 def parse():
@@ -74,7 +75,11 @@ def layer_work(w, counts, T, batched):
     u_hit = int(np.count_nonzero(counts))
     gu = synth.byte_size(w.gate_dtype, H * F) + synth.byte_size(w.up_dtype, H * F)
     dn = synth.byte_size(w.down_dtype, F * H)
-    gate_b = u_hit * gu + T * q8_bytes(H) + n_ent * F * 4
+    if not batched and T <= ROUTE_IN_GATEUP_MAX_T:
+        # the kernel also routes: the router and the f32 rows are its inputs
+        gate_b = u_hit * gu + w.router.nbytes + T * H * 4 + n_ent * F * 4
+    else:
+        gate_b = u_hit * gu + T * q8_bytes(H) + n_ent * F * 4
     down_b = u_hit * dn + n_ent * (F * 4 if not batched else q8_bytes(F)) + n_ent * H * 4
     gate_ops = 2.0 * n_ent * 2 * F * H
     down_ops = 2.0 * n_ent * F * H
