@@ -204,6 +204,31 @@ __device__ bool expert_tile(int E, int bn, int e, int mt_e, TileInfo& ti, const 
   return true;
 }
 
+// As expert_tile for the h-th expert that has members (ascending ids) instead of expert h;
+// false when fewer than h + 1 experts have members.
+__device__ bool hit_expert_tile(int E, int bn, int h, int mt_e, TileInfo& ti, const SelRegs& sr, int32_t* cnt) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 32) cnt[tid] = 0;
+  lds_barrier();
+#pragma unroll
+  for (int k = 0; k < SEL_REGS; ++k)
+    if (sr.v[k] >= 0) atomicAdd(&cnt[sr.v[k]], 1);
+  lds_barrier();
+  const uint32_t mask = (uint32_t)__ballot(lane < E && cnt[lane & 31] > 0);  // the same in every wave
+  if (h >= __popc(mask)) return false;
+  const int e = nth_expert(mask, h);
+  const int c = cnt[e];
+  if (mt_e * bn >= c) return false;
+  int base = 0;
+  for (int x = 0; x < e; ++x) base += cnt[x];
+  ti.e = e;
+  ti.m0 = mt_e * bn;
+  ti.g = c;
+  ti.base = base;
+  ti.cnt = min(bn, c - ti.m0);
+  return true;
+}
+
 // member_rows from the expert's member list (entries in ascending order).
 template <int KIND>
 __device__ void member_rows_list(const int32_t* list, const TileInfo& ti, int K, int bn, int32_t* rowidx,
@@ -334,11 +359,15 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   const uint8_t* w0;
   // the first block's weights are requested as soon as the expert is known
   if constexpr (MT == 1) {
-    // unit = (expert e, its member tile mt_e, row tile): the expert is known from the block id,
-    // so the first block's weights of an expert's first member tile are requested before the
-    // selections are even read (wasted only when the expert has no member)
+    // unit = (expert, its member tile mt_e, row tile). Down: the expert is e = mtile % E, known
+    // from the block id, so the first block's weights of an expert's first member tile are
+    // requested before the selections are even read (wasted only when the expert has no
+    // member). Gate/up: the (mtile % E)-th expert that has members, so the blocks of the experts
+    // nobody chose are the last of the grid and leave at once instead of holding a slot while
+    // their weights arrive (the gate/up grid is larger than the resident blocks).
     __shared__ SmemMembers mem;
     __shared__ int32_t cnt[32];
+    constexpr bool BY_HIT = KIND == GEMM_GATEUP;
     const int e = mtile % E, mt_e = mtile / E;
     w0 = wpk + (size_t)e * stride_e + (size_t)(2 * rtile) * tile_bytes;
     // gate/up of at most 16 tokens: the member tile is every token of the batch (outputs of the
@@ -352,17 +381,19 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
       const int i = k * 512 + tid;
       sr.v[k] = i < n_ent ? rb.sel[i] : -1;
     }
-    if (mt_e == 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    if (!BY_HIT && mt_e == 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     if (all_tokens) {
       if (tid < NBM) rowidx[tid] = min(tid, n_tok - 1);
       lds_barrier();
       gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     }
-    if (!expert_tile(E, NBM, e, mt_e, ti, sr, cnt)) {
+    const bool live = BY_HIT ? hit_expert_tile(E, NBM, e, mt_e, ti, sr, cnt) : expert_tile(E, NBM, e, mt_e, ti, sr, cnt);
+    if (!live) {
       __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): no copy may land after the block's LDS is released
       return;
     }
-    if (mt_e > 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    if (BY_HIT) w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+    if (BY_HIT || mt_e > 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_list(sr, n_ent, ti.e, mem);
     if (all_tokens) {
       // output row of token n: its group position, or -1 when it did not choose the expert
