@@ -313,6 +313,67 @@ __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes,
   }
 }
 
+// The same copies with each lane's source addresses of super-block 0 computed once (per
+// super-block only b times the op's stride is added): for the member tiles of 64 and more,
+// whose per-block address arithmetic would otherwise be a tenth of the VALU work.
+// One lane's copy of 16 (or 4) bytes from global memory into LDS (lane l at dst + 16l, or 4l).
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+}
+
+template <int DT, int MT>
+struct IssuePlan {
+  uint8_t* src[8];  // GemmCfg<DT, MT>::OPS <= 8 used
+
+  __device__ __forceinline__ void issue(int b, uint8_t* wb, uint8_t* xb, float* sb) {
+    using C = GemmCfg<DT, MT>;
+    constexpr int TB = C::TB;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int t = 0; t < C::OPS; ++t) {
+      const int j = w + 8 * t;
+      if (j < C::WCH) {
+        if (j * 64 + lane < C::W_UNITS)
+          lds_dma16(src[t] + (size_t)b * TB, wb + j * 1024);
+      } else if (j < C::WCH + C::XCH) {
+        lds_dma16(src[t] + (size_t)b * QK, xb + (j - C::WCH) * 1024);
+      } else {
+        lds_dma4(src[t] + 4 * b, reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH, C::SCH) * 64));
+      }
+    }
+  }
+};
+
+template <int DT, int MT>
+__device__ __forceinline__ void plan_build(IssuePlan<DT, MT>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
+                                           int n_in, const int32_t* rowidx) {
+  using C = GemmCfg<DT, MT>;
+  static_assert(C::OPS <= 8, "copy plan size");
+  constexpr int TB = C::TB;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = n_in / QK;
+#pragma unroll
+  for (int t = 0; t < C::OPS; ++t) {
+    const int j = w + 8 * t;
+    if (j < C::WCH) {
+      const int u = min(j * 64 + lane, C::W_UNITS - 1);
+      const int k = u / (TB / 16), o = u % (TB / 16);
+      p.src[t] = const_cast<uint8_t*>(w0 + (size_t)k * tile_bytes + 16 * o);
+    } else if (j < C::WCH + C::XCH) {
+      const int u = (j - C::WCH) * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
+      p.src[t] = (uint8_t*)(x.q + (size_t)rowidx[m] * n_in + 16 * c);
+    } else {
+      const int i = min(j - C::WCH - C::XCH, C::SCH);
+      const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
+      p.src[t] = (uint8_t*)(x.sx + (size_t)rowidx[m] * nb);
+    }
+    asm volatile("" : "+v"(p.src[t]));  // kept in registers, not recomputed in the loop
+  }
+}
+
 template <int DT, int KIND, int MT>
 __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
                                               int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
@@ -422,16 +483,24 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   lds_barrier();  // rowidx, outrow; the first block's copies stay in flight
   if (MT > 1 || !(KIND == GEMM_GATEUP && n_ent / K <= 16))
     gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+  IssuePlan<DT, MT> plan;
+  if constexpr (MT > 1) plan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, rowidx);
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
     __syncthreads();
-    if (b + 1 < nb) gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+    if (b + 1 < nb) {
+      if constexpr (MT > 1) plan.issue(b + 1, wb1, xb1, sb1);
+      else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+    }
     block(wb0, xb0, sb0);
     if (b + 1 >= nb) break;
     __builtin_amdgcn_s_waitcnt(0x3f70);
     __syncthreads();
-    if (b + 2 < nb) gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+    if (b + 2 < nb) {
+      if constexpr (MT > 1) plan.issue(b + 2, wb0, xb0, sb0);
+      else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+    }
     block(wb1, xb1, sb1);
   }
   if constexpr (KIND == GEMM_GATEUP) {
