@@ -75,6 +75,39 @@ def test_batched_zero_inputs(batched, oracle):
     check_moe(batched, oracle, w, x, 40, "batched zero/scaled")
 
 
+def test_fused_calls_of_other_shapes_in_turn(batched, oracle):
+    # one context's workspace is carved anew for each call's shape: calls of other shapes in
+    # turn leave an earlier call's rows where a later call's kernels read and write
+    shapes = [(51, 512, 512, 8, 4, 7), (53, 768, 1024, 16, 3, 16), (55, 512, 256, 32, 8, 13)]
+    cases = []
+    for seed, hidden, ff, n_exp, k, t in shapes:
+        w = synth.moe_weights(seed, hidden=hidden, moe_ff=ff, n_experts=n_exp, n_used=k)
+        cases.append((w, synth.hidden_states(seed + 1, t, hidden=hidden), t))
+    for rep in range(2):
+        for i, (w, x, t) in enumerate(cases):
+            check_moe(batched, oracle, w, x, t, f"shape {i} rep {rep} t={t}")
+
+
+@pytest.mark.parametrize("t", [3, 16])
+def test_batched_stack_leaves_slots_to_the_residual_kernel(batched, oracle, t):
+    # in the stack an MoE layer's expert outputs go to the residual kernel, not to a combine
+    from bebelm_amd.model import DenseLayer, FfnStack
+
+    layers = synth.stack_layers(seed=6, hidden=512, moe_ff=256, dense_ff=1024, n_experts=8, n_layers=4, n_dense=1)
+    objs = []
+    try:
+        for gain, w in layers:
+            objs.append((gain, MoeLayer(batched, w) if hasattr(w, "router") else DenseLayer(batched, w)))
+        stack = FfnStack(batched, objs)
+        x = synth.hidden_states(7, t, hidden=512).reshape(-1)
+        got = stack.forward(x, t, np.empty_like(x))
+        assert_bits(got, oracle.ffn_stack(layers, x, t), f"batched stack t={t}")
+        stack.close()
+    finally:
+        for _, o in objs:
+            o.close()
+
+
 @pytest.mark.parametrize("t", [33, 64])
 def test_gemv_path_many_members(gemv_only, oracle, t):
     # the per-expert GEMV kernels with more members than they stage at once
