@@ -144,16 +144,28 @@ __device__ __forceinline__ Q4kLane q4k_load(const uint8_t* __restrict__ block, i
   return r;
 }
 
+// The activations lane p of a group needs for one block: quants of its two 16-element pieces,
+// the Q8 sum of its sub-block 2(p>>1) + (p&1), and the block's scale.
+struct Q4kX {
+  uint4 xl, xh;
+  int32_t sum;
+  float sx;
+};
+__device__ __forceinline__ Q4kX q4k_xload(const int8_t* __restrict__ qxb, const int32_t* __restrict__ sumsb,
+                                          const float* __restrict__ sxp, int p) {
+  const int c = p >> 1, h = p & 1;
+  return Q4kX{*reinterpret_cast<const uint4*>(qxb + 64 * c + 16 * h),
+              *reinterpret_cast<const uint4*>(qxb + 64 * c + 32 + 16 * h), sumsb[2 * c + h], *sxp};
+}
+
 // Partial (sd, sm) of one block for this lane: sd_part = sc_2c·<lo, qx> + sc_2c+1·<hi, qx>,
 // sm_part = m_j·sums_j for the one sub-block this lane accounts for (j = 2c + h).
-__device__ __forceinline__ void q4k_lane_partial(const Q4kLane& w, int p, const int8_t* __restrict__ qxb,
-                                                 const int32_t* __restrict__ sumsb, int& sd, int& sm) {
+__device__ __forceinline__ void q4k_lane_partial_x(const Q4kLane& w, int p, uint4 xl, uint4 xh, int32_t sum, int& sd,
+                                                   int& sm) {
   const int c = p >> 1, h = p & 1;
   int sc0, m0, sc1, m1;
   q4k_scale_min(w.hd.y, w.hd.z, w.hd.w, 2 * c, sc0, m0);
   q4k_scale_min(w.hd.y, w.hd.z, w.hd.w, 2 * c + 1, sc1, m1);
-  const uint4 xl = *reinterpret_cast<const uint4*>(qxb + 64 * c + 16 * h);
-  const uint4 xh = *reinterpret_cast<const uint4*>(qxb + 64 * c + 32 + 16 * h);
   const uint32_t M = 0x0F0F0F0Fu;
   int dl = __builtin_amdgcn_sdot4((int)(w.qs.x & M), (int)xl.x, 0, false);
   dl = __builtin_amdgcn_sdot4((int)(w.qs.y & M), (int)xl.y, dl, false);
@@ -164,7 +176,14 @@ __device__ __forceinline__ void q4k_lane_partial(const Q4kLane& w, int p, const 
   dh = __builtin_amdgcn_sdot4((int)((w.qs.z >> 4) & M), (int)xh.z, dh, false);
   dh = __builtin_amdgcn_sdot4((int)((w.qs.w >> 4) & M), (int)xh.w, dh, false);
   sd = sc0 * dl + sc1 * dh;
-  sm = h == 0 ? m0 * sumsb[2 * c] : m1 * sumsb[2 * c + 1];
+  sm = (h == 0 ? m0 : m1) * sum;
+}
+
+__device__ __forceinline__ void q4k_lane_partial(const Q4kLane& w, int p, const int8_t* __restrict__ qxb,
+                                                 const int32_t* __restrict__ sumsb, int& sd, int& sm) {
+  const int c = p >> 1, h = p & 1;
+  q4k_lane_partial_x(w, p, *reinterpret_cast<const uint4*>(qxb + 64 * c + 16 * h),
+                     *reinterpret_cast<const uint4*>(qxb + 64 * c + 32 + 16 * h), sumsb[2 * c + h], sd, sm);
 }
 
 // matmul.rs:242: sx·(d·sd − dmin·sm), operation by operation.
@@ -210,18 +229,24 @@ __device__ __forceinline__ Q6kLane q6k_load(const uint8_t* __restrict__ block, i
 // bit 7 maps q+96 to q-32 mod 256.
 __device__ __forceinline__ int q6_center(uint32_t q) { return (int)((q + 0x60606060u) ^ 0x80808080u); }
 
-__device__ __forceinline__ int q6k_lane_partial(const Q6kLane& w, int p, const int8_t* __restrict__ qxb) {
-  const int n = p >> 2, l0 = 8 * (p & 3), s = (p & 3) >> 1;
+// The activations lane p needs for one block: four 8-element pieces, 32 apart, and the scale.
+struct Q6kX {
+  uint2 x0, x1, x2, x3;
+  float sx;
+};
+__device__ __forceinline__ Q6kX q6k_xload(const int8_t* __restrict__ qxb, const float* __restrict__ sxp, int p) {
+  const int8_t* xg = qxb + 128 * (p >> 2) + 8 * (p & 3);
+  return Q6kX{*reinterpret_cast<const uint2*>(xg), *reinterpret_cast<const uint2*>(xg + 32),
+              *reinterpret_cast<const uint2*>(xg + 64), *reinterpret_cast<const uint2*>(xg + 96), *sxp};
+}
+
+__device__ __forceinline__ int q6k_lane_partial_x(const Q6kLane& w, int p, uint2 x0, uint2 x1, uint2 x2, uint2 x3) {
+  const int s = (p & 3) >> 1;
   const uint32_t scw = s ? ((w.sc.x >> 8) | (w.sc.y << 24)) : w.sc.x;  // bytes s, s+2 in scw.x
   const uint32_t scv = s ? (w.sc.y >> 8) : w.sc.y;                      // bytes s+4, s+6
   const int sc0 = (int)(int8_t)(scw & 0xff), sc1 = (int)(int8_t)((scw >> 16) & 0xff);
   const int sc2 = (int)(int8_t)(scv & 0xff), sc3 = (int)(int8_t)((scv >> 16) & 0xff);
   const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x30303030u;
-  const int8_t* xg = qxb + 128 * n + l0;
-  const uint2 x0 = *reinterpret_cast<const uint2*>(xg);
-  const uint2 x1 = *reinterpret_cast<const uint2*>(xg + 32);
-  const uint2 x2 = *reinterpret_cast<const uint2*>(xg + 64);
-  const uint2 x3 = *reinterpret_cast<const uint2*>(xg + 96);
   int d0 = 0, d1 = 0, d2 = 0, d3 = 0;
 #define BB_Q6_STEP(A, B, H, X0, X1, X2, X3)                                                           \
   d0 = __builtin_amdgcn_sdot4(q6_center(((A) & M4) | (((H) << 4) & M2)), (int)(X0), d0, false);     \
@@ -232,6 +257,12 @@ __device__ __forceinline__ int q6k_lane_partial(const Q6kLane& w, int p, const i
   BB_Q6_STEP(w.a.y, w.b.y, w.h.y, x0.y, x1.y, x2.y, x3.y)
 #undef BB_Q6_STEP
   return sc0 * d0 + sc1 * d1 + sc2 * d2 + sc3 * d3;
+}
+
+__device__ __forceinline__ int q6k_lane_partial(const Q6kLane& w, int p, const int8_t* __restrict__ qxb) {
+  const int8_t* xg = qxb + 128 * (p >> 2) + 8 * (p & 3);
+  return q6k_lane_partial_x(w, p, *reinterpret_cast<const uint2*>(xg), *reinterpret_cast<const uint2*>(xg + 32),
+                            *reinterpret_cast<const uint2*>(xg + 64), *reinterpret_cast<const uint2*>(xg + 96));
 }
 
 // matmul.rs:641: sx·(d·s).
@@ -251,7 +282,19 @@ template <>
 struct RowDot<DT_Q4_K> {
   static constexpr int BLOCK_BYTES = Q4K_BYTES;
   using Lane = Q4kLane;
+  using X = Q4kX;
   static __device__ __forceinline__ Lane load(const uint8_t* block, int p) { return q4k_load(block, p); }
+  static __device__ __forceinline__ X xload(const int8_t* qxb, const int32_t* sumsb, const float* sxp, int p) {
+    return q4k_xload(qxb, sumsb, sxp, p);
+  }
+  // The block's value from registers only (all 8 lanes of the group return it).
+  static __device__ __forceinline__ float block_value_x(const Lane& w, int p, const X& x) {
+    int sd, sm;
+    q4k_lane_partial_x(w, p, x.xl, x.xh, x.sum, sd, sm);
+    sd = sum8(sd);
+    sm = sum8(sm);
+    return q4k_block_value(w.hd.x, sd, sm, x.sx);
+  }
   static __device__ __forceinline__ float block_value(const Lane& w, int p, const int8_t* qxb, const int32_t* sumsb,
                                                       float sx) {
     int sd, sm;
@@ -266,7 +309,15 @@ template <>
 struct RowDot<DT_Q6_K> {
   static constexpr int BLOCK_BYTES = Q6K_BYTES;
   using Lane = Q6kLane;
+  using X = Q6kX;
   static __device__ __forceinline__ Lane load(const uint8_t* block, int p) { return q6k_load(block, p); }
+  static __device__ __forceinline__ X xload(const int8_t* qxb, const int32_t*, const float* sxp, int p) {
+    return q6k_xload(qxb, sxp, p);
+  }
+  static __device__ __forceinline__ float block_value_x(const Lane& w, int p, const X& x) {
+    const int s = sum8(q6k_lane_partial_x(w, p, x.x0, x.x1, x.x2, x.x3));
+    return q6k_block_value(w.d, s, x.sx);
+  }
   static __device__ __forceinline__ float block_value(const Lane& w, int p, const int8_t* qxb, const int32_t*,
                                                       float sx) {
     int s = sum8(q6k_lane_partial(w, p, qxb));
