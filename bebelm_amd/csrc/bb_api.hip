@@ -376,15 +376,26 @@ void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* 
     }
     const int nz = T == 1;  // n_tokens == 1 takes matvec (-0.0-started sum), else matmul
     launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
-    launch(c, bb::K_ROWS_Q8, [&] {
-      return bb::launch_rows_q8(c->stream, (int)d->gate->dtype, d->gate->dev, (H / 256) * (d->gate->dtype == BB_Q4_K ? 144 : 210),
-                                (int)(H / 256), F, xq, H, T, gate, F, nz);
-    });
-    launch(c, bb::K_ROWS_Q8, [&] {
-      return bb::launch_rows_q8(c->stream, (int)d->up->dtype, d->up->dev, (H / 256) * (d->up->dtype == BB_Q4_K ? 144 : 210),
-                                (int)(H / 256), F, xq, H, T, up, F, nz);
-    });
-    launch(c, bb::K_ELEMWISE, [&] { return bb::launch_elementwise(c->stream, bb::EW_SWIGLU, gate, gate, up, 0.f, T * F); });
+    const size_t gate_rb = (H / 256) * (d->gate->dtype == BB_Q4_K ? 144 : 210);
+    if (d->gate->dtype == d->up->dtype && H / 256 <= 64) {
+      // gate, up and swiglu in one pass over both matrices
+      launch(c, bb::K_ROWS_Q8, [&] {
+        return bb::launch_rows_q8_swiglu(c->stream, (int)d->gate->dtype, d->gate->dev, d->up->dev, gate_rb,
+                                         (int)(H / 256), F, xq, H, T, gate, F, nz);
+      });
+    } else {
+      launch(c, bb::K_ROWS_Q8, [&] {
+        return bb::launch_rows_q8(c->stream, (int)d->gate->dtype, d->gate->dev, gate_rb, (int)(H / 256), F, xq, H, T,
+                                  gate, F, nz);
+      });
+      launch(c, bb::K_ROWS_Q8, [&] {
+        return bb::launch_rows_q8(c->stream, (int)d->up->dtype, d->up->dev,
+                                  (H / 256) * (d->up->dtype == BB_Q4_K ? 144 : 210), (int)(H / 256), F, xq, H, T, up,
+                                  F, nz);
+      });
+      launch(c, bb::K_ELEMWISE,
+             [&] { return bb::launch_elementwise(c->stream, bb::EW_SWIGLU, gate, gate, up, 0.f, T * F); });
+    }
     launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, gate, T, F, aq); });
     launch(c, bb::K_ROWS_Q8, [&] {
       return bb::launch_rows_q8(c->stream, (int)d->down->dtype, d->down->dev,

@@ -152,6 +152,11 @@ hipError_t launch_quantize(hipStream_t s, const float* x, size_t n_vec, size_t n
 
 hipError_t launch_rows_q8(hipStream_t s, int dtype, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows,
                           Q8Bufs q, size_t q_stride, size_t n_tok, float* y, size_t y_tok_stride, int neg_zero_start);
+// Dense FFN gate/up/swiglu in one pass: y[t][o] = silu(gate row o · x_t) * (up row o · x_t), both
+// sums as launch_rows_q8's (gate and up of one dtype and row length, nb <= 64).
+hipError_t launch_rows_q8_swiglu(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t row_bytes,
+                                 int nb, size_t n_rows, Q8Bufs q, size_t q_stride, size_t n_tok, float* y,
+                                 size_t y_tok_stride, int neg_zero_start);
 
 hipError_t launch_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t n_in, size_t n_rows, const float* x,
                            size_t n_tok, float* y);

@@ -96,20 +96,25 @@ __global__ void __launch_bounds__(256) k_rows_q8(const uint8_t* __restrict__ w, 
 // issued before the first is used, so a row costs a memory round trip per pass instead of one
 // per block. The groups' block values meet in LDS and lane 0 adds them left to right from the
 // start value (the reference's order). With at most 8J blocks the row's weights stay in
-// registers from token to token.
+// registers from token to token. With SWIGLU the wave also takes row o of w2 (same shape) against
+// the same activations and stores silu(row o of w · x) * (row o of w2 · x), the dense FFN's
+// gate, up and swiglu (model.rs:464-466) in one pass.
 constexpr int RW_MAX_NB = 64;
-template <int DT, int J>
-__global__ void __launch_bounds__(256) k_rows_q8w(const uint8_t* __restrict__ w, size_t row_bytes, int nb,
-                                                  size_t n_rows, Q8Bufs q, size_t q_stride, size_t n_tok,
-                                                  float* __restrict__ y, size_t y_tok_stride, int neg_zero_start) {
+template <int DT, int J, bool SWIGLU>
+__global__ void __launch_bounds__(256) k_rows_q8w(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2,
+                                                  size_t row_bytes, int nb, size_t n_rows, Q8Bufs q, size_t q_stride,
+                                                  size_t n_tok, float* __restrict__ y, size_t y_tok_stride,
+                                                  int neg_zero_start) {
   using R = RowDot<DT>;
   __shared__ float vals[4][RW_MAX_NB];
+  __shared__ float vals2[SWIGLU ? 4 : 1][SWIGLU ? RW_MAX_NB : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 3, p = lane & 7;
   const size_t o = (size_t)blockIdx.x * 4 + wave;
   if (o >= n_rows) return;  // (a whole wave: the block has no barrier)
   const uint8_t* row = w + o * row_bytes;
+  const uint8_t* row2 = SWIGLU ? w2 + o * row_bytes : nullptr;
   const bool resident = nb <= 8 * J;
-  typename R::Lane wl[J];
+  typename R::Lane wl[J], wl2[SWIGLU ? J : 1];
   for (size_t t = 0; t < n_tok; ++t) {
     const int8_t* qx = q.q + t * q_stride;
     const float* sx = q.scales + t * nb;
@@ -119,7 +124,10 @@ __global__ void __launch_bounds__(256) k_rows_q8w(const uint8_t* __restrict__ w,
 #pragma unroll
       for (int j = 0; j < J; ++j) {
         const int b = min(c0 + g + 8 * j, nb - 1);  // (past the row: a block of it again, value unused)
-        if (t == 0 || !resident) wl[j] = R::load(row + (size_t)b * R::BLOCK_BYTES, p);
+        if (t == 0 || !resident) {
+          wl[j] = R::load(row + (size_t)b * R::BLOCK_BYTES, p);
+          if constexpr (SWIGLU) wl2[j] = R::load(row2 + (size_t)b * R::BLOCK_BYTES, p);
+        }
         xv[j] = R::xload(qx + b * QK, sums + b * 8, sx + b, p);
       }
 #pragma unroll
@@ -127,31 +135,53 @@ __global__ void __launch_bounds__(256) k_rows_q8w(const uint8_t* __restrict__ w,
         const int b = c0 + g + 8 * j;
         const float v = R::block_value_x(wl[j], p, xv[j]);
         if (p == 0 && b < nb) vals[wave][b] = v;
+        if constexpr (SWIGLU) {
+          const float v2 = R::block_value_x(wl2[j], p, xv[j]);
+          if (p == 0 && b < nb) vals2[wave][b] = v2;
+        }
       }
     }
     // (one wave writes and reads its row of vals: its LDS accesses are performed in order)
     if (lane == 0) {
       float acc = neg_zero_start ? -0.0f : 0.0f;
       for (int b = 0; b < nb; ++b) acc += vals[wave][b];
+      if constexpr (SWIGLU) {
+        float acc2 = neg_zero_start ? -0.0f : 0.0f;
+        for (int b = 0; b < nb; ++b) acc2 += vals2[wave][b];
+        acc = silu(acc) * acc2;
+      }
       y[t * y_tok_stride + o] = acc;
     }
   }
 }
 
-template <int DT>
-static hipError_t launch_rows_q8w(hipStream_t s, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows, Q8Bufs q,
-                                  size_t q_stride, size_t n_tok, float* y, size_t y_tok_stride, int nz) {
+template <int DT, bool SWIGLU>
+static hipError_t launch_rows_q8w(hipStream_t s, const uint8_t* w, const uint8_t* w2, size_t row_bytes, int nb,
+                                  size_t n_rows, Q8Bufs q, size_t q_stride, size_t n_tok, float* y,
+                                  size_t y_tok_stride, int nz) {
   dim3 grid((unsigned)((n_rows + 3) / 4));
   if (nb <= 8)
-    BB_LAUNCH((k_rows_q8w<DT, 1>), grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
-              nz);
+    BB_LAUNCH((k_rows_q8w<DT, 1, SWIGLU>), grid, dim3(256), 0, s, w, w2, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
+              y_tok_stride, nz);
   else if (nb <= 16)
-    BB_LAUNCH((k_rows_q8w<DT, 2>), grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
-              nz);
+    BB_LAUNCH((k_rows_q8w<DT, 2, SWIGLU>), grid, dim3(256), 0, s, w, w2, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
+              y_tok_stride, nz);
   else
-    BB_LAUNCH((k_rows_q8w<DT, 4>), grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
-              nz);
+    BB_LAUNCH((k_rows_q8w<DT, 4, SWIGLU>), grid, dim3(256), 0, s, w, w2, row_bytes, nb, n_rows, q, q_stride, n_tok, y,
+              y_tok_stride, nz);
   return hipGetLastError();
+}
+
+hipError_t launch_rows_q8_swiglu(hipStream_t s, int dtype, const uint8_t* gate, const uint8_t* up, size_t row_bytes,
+                                 int nb, size_t n_rows, Q8Bufs q, size_t q_stride, size_t n_tok, float* y,
+                                 size_t y_tok_stride, int neg_zero_start) {
+  if (n_rows == 0) return hipSuccess;
+  if (nb < 1 || nb > RW_MAX_NB) return hipErrorInvalidValue;
+  if (dtype == DT_Q4_K)
+    return launch_rows_q8w<DT_Q4_K, true>(s, gate, up, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
+                                          neg_zero_start);
+  return launch_rows_q8w<DT_Q6_K, true>(s, gate, up, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
+                                        neg_zero_start);
 }
 
 hipError_t launch_rows_q8(hipStream_t s, int dtype, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows,
@@ -159,8 +189,10 @@ hipError_t launch_rows_q8(hipStream_t s, int dtype, const uint8_t* w, size_t row
   if (n_rows == 0) return hipSuccess;
   if (nb >= 1 && nb <= RW_MAX_NB) {
     if (dtype == DT_Q4_K)
-      return launch_rows_q8w<DT_Q4_K>(s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride, neg_zero_start);
-    return launch_rows_q8w<DT_Q6_K>(s, w, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride, neg_zero_start);
+      return launch_rows_q8w<DT_Q4_K, false>(s, w, nullptr, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
+                                             neg_zero_start);
+    return launch_rows_q8w<DT_Q6_K, false>(s, w, nullptr, row_bytes, nb, n_rows, q, q_stride, n_tok, y, y_tok_stride,
+                                           neg_zero_start);
   }
   dim3 grid((unsigned)((n_rows + 31) / 32));
   if (dtype == DT_Q4_K)

@@ -283,6 +283,24 @@ def test_dense_ffn(gpu_ctx, oracle):
         layer.close()
 
 
+@pytest.mark.parametrize("dts", [(Q6_K, Q6_K, Q6_K), (Q4_K, Q6_K, Q4_K)])
+def test_dense_ffn_other_dtypes(gpu_ctx, oracle, dts):
+    # gate and up of one dtype take the fused gate/up/swiglu pass; of two dtypes, separate passes
+    g = synth.rng(5, 0)
+    gate = synth.quant_tensor(g, dts[0], 512, 1024)
+    up = synth.quant_tensor(g, dts[1], 512, 1024)
+    down = synth.quant_tensor(g, dts[2], 1024, 512)
+    d = synth.DenseWeights(512, 1024, dts[0], dts[1], dts[2], gate, up, down)
+    layer = DenseLayer(gpu_ctx, d)
+    try:
+        x = synth.hidden_states(6, 2, hidden=512)
+        for t in (1, 2):
+            got = layer.forward(np.ascontiguousarray(x[:t].reshape(-1)), t, np.empty(t * 512, np.float32))
+            assert_bits(got, oracle.dense_ffn(d, x[:t].reshape(-1), t), f"dense {dts} t={t}")
+    finally:
+        layer.close()
+
+
 def test_ffn_stack_reduced(gpu_ctx, oracle):
     layers = synth.stack_layers(seed=4, hidden=512, moe_ff=256, dense_ff=1024, n_experts=8, n_layers=6, n_dense=2)
     objs = []
