@@ -130,8 +130,13 @@ struct bb_stack {
   float eps;
   int H;
   float* h = nullptr;
+  float* h2 = nullptr;      // h alternates with h2 at boundaries that also route the next layer
   float* normed = nullptr;
   float* ffn = nullptr;
+  float* logits = nullptr;  // the next MoE layer's router logits [T][32]
+  int8_t* xq_q = nullptr;   // and the XQ records of its input
+  float* xq_sx = nullptr;
+  uint32_t* xq_pairs = nullptr;
   size_t cap_T = 0;
 };
 
@@ -280,9 +285,16 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched) {
   return {};
 }
 
+// Router logits and XQ records of x computed before the call (by the stack's layer boundary).
+struct PreRoute {
+  const float* logits;
+  bb::XQBufs xq;
+};
+
 // With combine false the caller combines: the slots and weights stay in the returned workspace.
+// With pre set (a few tokens on the GEMV path only) the route's dots are already done.
 MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr,
-                      bool combine = true) {
+                      bool combine = true, const PreRoute* pre = nullptr) {
   need(T >= 1, BB_ERR_ARG, "T must be >= 1");
   const size_t n_ent = T * (size_t)m->K;
   const bool batched = n_ent >= c->batched_min_entries;
@@ -315,13 +327,19 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
   } else {
     const int batch_mode = T > 1;
     const int max_hit = (int)std::min<size_t>((size_t)m->E, n_ent);
-    // a few tokens: every gate/up block routes them itself
+    // a few tokens: every gate/up block routes them itself (or only gates them, from logits
+    // computed before the call)
     const bool route_in = T <= (size_t)bb::ROUTE_IN_GATEUP_MAX_T;
+    need(!pre || route_in, BB_ERR_ARG, "routes computed before the call serve at most 4 tokens");
     if (!route_in)
       launch(c, bb::K_ROUTE, [&] {
         return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, 1, w.xq, w.rb);
       });
     launch(c, bb::K_GATEUP, [&] {
+      if (pre)
+        return bb::launch_gate_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E,
+                                      m->K, max_hit, batch_mode, tr != nullptr, w.rb, pre->logits, m->bias_dev,
+                                      pre->xq, w.act);
       if (route_in)
         return bb::launch_route_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E,
                                        m->K, max_hit, batch_mode, tr != nullptr, w.rb, m->router_cm, m->bias_dev, x,
@@ -924,9 +942,9 @@ int bb_stack_destroy(bb_stack* s) {
     set_device(s->ctx);
     (void)hipStreamSynchronize(s->ctx->stream);
     for (float* g : s->gains) (void)hipFree(g);
-    if (s->h) (void)hipFree(s->h);
-    if (s->normed) (void)hipFree(s->normed);
-    if (s->ffn) (void)hipFree(s->ffn);
+    for (void* p : {(void*)s->h, (void*)s->h2, (void*)s->normed, (void*)s->ffn, (void*)s->logits, (void*)s->xq_q,
+                    (void*)s->xq_sx, (void*)s->xq_pairs})
+      if (p) (void)hipFree(p);
     delete s;
   });
 }
@@ -941,41 +959,68 @@ int bb_stack_forward(bb_ctx* c, bb_stack* s, const float* x, size_t T, float* h_
     const size_t H = s->H;
     if (T > s->cap_T) {
       check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-      for (float** p : {&s->h, &s->normed, &s->ffn}) {
+      for (void** p : {(void**)&s->h, (void**)&s->h2, (void**)&s->normed, (void**)&s->ffn, (void**)&s->logits,
+                       (void**)&s->xq_q, (void**)&s->xq_sx, (void**)&s->xq_pairs}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
       }
       s->cap_T = 0;
       s->h = static_cast<float*>(dev_alloc(T * H * 4));
+      s->h2 = static_cast<float*>(dev_alloc(T * H * 4));
       s->normed = static_cast<float*>(dev_alloc(T * H * 4));
       s->ffn = static_cast<float*>(dev_alloc(T * H * 4));
+      s->logits = static_cast<float*>(dev_alloc(T * 32 * 4));
+      s->xq_q = static_cast<int8_t*>(dev_alloc(T * H));
+      s->xq_sx = static_cast<float*>(dev_alloc(T * (H / 256) * 4));
+      s->xq_pairs = static_cast<uint32_t*>(dev_alloc(T * (H / 256) * 12 * 4));
       s->cap_T = T;
     }
     with_io(c, loc, {{x, T * H * 4, true, false}, {h_out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
-      check_hip(hipMemcpyAsync(s->h, d[0], T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+      float* h = s->h;       // the residual stream; at a boundary that routes, h_out is the other buffer
+      float* h_alt = s->h2;
+      check_hip(hipMemcpyAsync(h, d[0], T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
       const size_t nl = s->layers.size();
       if (nl)
         launch(c, bb::K_RMSNORM,
-               [&] { return bb::launch_rmsnorm(c->stream, s->h, s->layers[0].ffn_norm, s->eps, H, T, s->normed); });
+               [&] { return bb::launch_rmsnorm(c->stream, h, s->layers[0].ffn_norm, s->eps, H, T, s->normed); });
+      const PreRoute pre{s->logits, bb::XQBufs{s->xq_q, s->xq_sx, s->xq_pairs}};
+      bool routed = false;  // the current layer's logits and XQ records are in pre
       for (size_t l = 0; l < nl; ++l) {
         const bb_layer_desc& L = s->layers[l];
-        // the layer's FFN on normed, then h += its output and the next layer's rmsnorm, fused
+        // the layer's FFN on normed, then h += its output and the next layer's rmsnorm, fused;
+        // before an MoE layer of a few tokens on the GEMV path the same kernel also takes its
+        // router logits
         const float* next_gain = l + 1 < nl ? s->layers[l + 1].ffn_norm : nullptr;
+        const bb_moe* nm = l + 1 < nl ? s->layers[l + 1].moe : nullptr;
+        const bool route_next = nm && T <= (size_t)bb::ROUTE_IN_GATEUP_MAX_T &&
+                                T * (size_t)nm->K < c->batched_min_entries && H % 128 == 0 && nm->E <= 32 &&
+                                nm->K <= 8;
+        const float* slots = nullptr;
+        const float* wts = nullptr;
+        int K = 0;
         if (L.moe) {
-          MoeWs w = moe_forward_dev(c, L.moe, s->normed, T, nullptr, nullptr, false);
-          launch(c, bb::K_RESIDUAL_NORM, [&] {
-            return bb::launch_residual_norm(c->stream, s->h, w.slots, w.rb.wts, L.moe->K, nullptr, next_gain, s->eps, H,
-                                            T, s->normed);
-          });
+          MoeWs w = moe_forward_dev(c, L.moe, s->normed, T, nullptr, nullptr, false, routed ? &pre : nullptr);
+          slots = w.slots;
+          wts = w.rb.wts;
+          K = L.moe->K;
         } else {
           dense_forward_dev(c, L.dense, s->normed, T, s->ffn);
+        }
+        const float* ffn = L.moe ? nullptr : s->ffn;
+        if (route_next) {
+          launch(c, bb::K_RESIDUAL_ROUTE, [&] {
+            return bb::launch_residual_norm_route(c->stream, h, h_alt, slots, wts, K, ffn, next_gain, s->eps, (int)H,
+                                                  (int)T, s->normed, nm->router_cm, nm->E, s->logits, pre.xq);
+          });
+          std::swap(h, h_alt);
+        } else {
           launch(c, bb::K_RESIDUAL_NORM, [&] {
-            return bb::launch_residual_norm(c->stream, s->h, nullptr, nullptr, 0, s->ffn, next_gain, s->eps, H, T,
-                                            s->normed);
+            return bb::launch_residual_norm(c->stream, h, slots, wts, K, ffn, next_gain, s->eps, H, T, s->normed);
           });
         }
+        routed = route_next;
       }
-      check_hip(hipMemcpyAsync(d[1], s->h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+      check_hip(hipMemcpyAsync(d[1], h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
     });
   });
 }

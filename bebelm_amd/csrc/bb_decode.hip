@@ -307,6 +307,23 @@ __device__ void route_block(const float* __restrict__ Wr, const float* __restric
   lds_barrier();
 }
 
+// The gating alone (gate_halfwave per token), from logits computed before the launch (by
+// k_residual_norm_route at the layer boundary): selections into sel_lds, and the route's outputs
+// to rb when global_out.
+__device__ void gate_block(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
+                           bool global_out, RouteBufs rb, int32_t* sel_lds, uint64_t* exptab, uint64_t exp_e) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i = tid >> 5, e = lane & 31;  // half-wave i gates token i
+  const bool tok = i < T, live = tok && e < E;
+  const float lg = logits[min(i, T - 1) * E + min(e, E - 1)];
+  const float be = bias[min(e, E - 1)];
+  if (tid < 32) exptab[tid] = exp_e;
+  lds_barrier();
+  if (2 * wave < T) gate_halfwave(live ? lg : 0.0f, live, tok, be, i, E, K, exptab, rb, global_out, sel_lds);
+  if (global_out && live) rb.logits[(size_t)i * E + e] = lg;
+  lds_barrier();
+}
+
 // Wr[c][k][e][j] = W[e][32(4k + j) + c]: float4 k of dot chain c of expert e (elements
 // 128k + c, +32, +64, +96), the 32 experts of a chain step contiguous (layout only).
 __global__ void k_router_chain_major(const float* __restrict__ W, int H, int E, float* __restrict__ Wr) {
@@ -384,9 +401,12 @@ struct SmemT {
 // down the member's act row, quantised here (quantize_q8 per member, model.rs:530-534).
 enum : int { GEMV_GATEUP = 0, GEMV_DOWN = 1 };
 
-// With ROUTE (gate/up of at most RT_MAX tokens) the block routes the tokens itself
-// (route_block) from the router, bias and f32 rows x_in, and reads the XQ records from LDS.
-template <int DT, int KIND, bool ROUTE>
+// Route modes of the gate/up GEMV (at most RT_MAX tokens): RM_ROUTE, the block routes the tokens
+// itself (route_block) from the router, bias and f32 rows x_in, and reads the XQ records from
+// LDS; RM_GATE, the block gates the tokens (gate_block) from logits already computed (passed as
+// router) and reads the XQ records from memory; RM_NONE, the selections come from rb.
+enum : int { RM_NONE = 0, RM_ROUTE = 1, RM_GATE = 2 };
+template <int DT, int KIND, int RM>
 __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk, size_t stride_e, int T, int H,
                                                  int F, int K, int batch_mode, int publish, int E, RouteBufs rb,
                                                  const int8_t* __restrict__ xq_q, const float* __restrict__ xq_sx,
@@ -406,10 +426,15 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
   const int out_w = KIND == GEMV_GATEUP ? F : H;  // output row stride
   const int32_t* sel = rb.sel;
+  constexpr bool ROUTE = RM == RM_ROUTE;
   __shared__ __align__(16) typename std::conditional<ROUTE, SmemRoute, char>::type rt;
+  __shared__ int32_t gsel[RM == RM_GATE ? RT_MAX * 8 : 1];
   if constexpr (ROUTE) {
     route_block(router, bias, x_in, T, H, E, K, blockIdx.x == 0, rb, rt, exptab, exp_e);
     sel = rt.sel;
+  } else if constexpr (RM == RM_GATE) {
+    gate_block(router, bias, T, E, K, blockIdx.x == 0, rb, gsel, exptab, exp_e);
+    sel = gsel;
   }
   if (publish && blockIdx.x == 0) publish_dispatch(sel, n_ent, E, rb);
   SelRegs sr;
@@ -448,7 +473,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
     if (has_blk) R::prep(B, L);
-    if (KIND == GEMV_GATEUP && !ROUTE && unit == lo && tid < 32) exptab[tid] = exp_e;  // loaded before the weights
+    if (KIND == GEMV_GATEUP && RM == RM_NONE && unit == lo && tid < 32) exptab[tid] = exp_e;  // loaded before the weights
     // the next unit's weights go in flight before this tile is computed
     const bool more = unit + 1 < hi;
     const int tile_n = tile + 1 == tiles ? 0 : tile + 1;
@@ -508,27 +533,34 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
 template <int KIND>
 static hipError_t launch_experts(hipStream_t s, int dtype, const uint8_t* wpk, size_t stride_e, int T, int H, int F,
                                  int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
-                                 XQBufs xq, const float* act_in, float* out, const float* router = nullptr,
-                                 const float* bias = nullptr, const float* x_in = nullptr) {
+                                 XQBufs xq, const float* act_in, float* out, int rm = RM_NONE,
+                                 const float* router = nullptr, const float* bias = nullptr,
+                                 const float* x_in = nullptr) {
   const int tiles = KIND == GEMV_GATEUP ? F / 32 : H / 64;
   const int grid = min(GEMV_BLOCKS, max_hit * tiles);
   if constexpr (KIND == GEMV_GATEUP) {
-    if (router) {
+    if (rm != RM_NONE) {
       if (T > RT_MAX || E > 32 || K > 8 || H > GU_H_MAX) return hipErrorInvalidValue;
-      if (dtype == DT_Q4_K)
-        BB_LAUNCH((k_experts<DT_Q4_K, KIND, true>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+      if (rm == RM_ROUTE && dtype == DT_Q4_K)
+        BB_LAUNCH((k_experts<DT_Q4_K, KIND, RM_ROUTE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+                  batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
+      else if (rm == RM_ROUTE)
+        BB_LAUNCH((k_experts<DT_Q6_K, KIND, RM_ROUTE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+                  batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
+      else if (dtype == DT_Q4_K)
+        BB_LAUNCH((k_experts<DT_Q4_K, KIND, RM_GATE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
                   batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
       else
-        BB_LAUNCH((k_experts<DT_Q6_K, KIND, true>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
+        BB_LAUNCH((k_experts<DT_Q6_K, KIND, RM_GATE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K,
                   batch_mode, publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, router, bias, x_in);
       return hipGetLastError();
     }
   }
   if (dtype == DT_Q4_K)
-    BB_LAUNCH((k_experts<DT_Q4_K, KIND, false>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+    BB_LAUNCH((k_experts<DT_Q4_K, KIND, RM_NONE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
               publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, nullptr, nullptr, nullptr);
   else
-    BB_LAUNCH((k_experts<DT_Q6_K, KIND, false>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
+    BB_LAUNCH((k_experts<DT_Q6_K, KIND, RM_NONE>), dim3(grid), dim3(512), 0, s, wpk, stride_e, T, H, F, K, batch_mode,
               publish, E, rb, xq.q, xq.sx, xq.pairs, act_in, out, nullptr, nullptr, nullptr);
   return hipGetLastError();
 }
@@ -543,7 +575,14 @@ hipError_t launch_route_gateup(hipStream_t s, int dtype, const uint8_t* gu, size
                                int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
                                const float* router, const float* bias, const float* x, float* act) {
   return launch_experts<GEMV_GATEUP>(s, dtype, gu, stride_gu, T, H, F, E, K, max_hit, batch_mode, publish, rb,
-                                     XQBufs{}, nullptr, act, router, bias, x);
+                                     XQBufs{}, nullptr, act, RM_ROUTE, router, bias, x);
+}
+
+hipError_t launch_gate_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
+                              int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
+                              const float* logits, const float* bias, XQBufs xq, float* act) {
+  return launch_experts<GEMV_GATEUP>(s, dtype, gu, stride_gu, T, H, F, E, K, max_hit, batch_mode, publish, rb, xq,
+                                     nullptr, act, RM_GATE, logits, bias, nullptr);
 }
 
 hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,
@@ -600,6 +639,147 @@ hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const ui
   if (total == 0) return hipSuccess;
   BB_LAUNCH(k_pack_rows, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, dtype, a, b, stride_a,
                      stride_b, rows_a, nb, n_exp, dst);
+  return hipGetLastError();
+}
+
+// ---- layer boundary with the next layer's router logits (a stack of at most RT_MAX tokens) ------
+// k_residual_norm's work for token t (h_out = h_in + the combine of the K slot rows from +0.0 in
+// selection order, or + the dense output; then the next layer's rmsnorm with an f64 tree sum) on
+// ceil(E/4) blocks per token, block eb also taking the router logits of experts 4eb..4eb+3 of
+// the next (MoE) layer from the normed row, with k_route's arithmetic (matmul.rs:36-66: 32 fmaf
+// chains per expert, chain c over the elements i = c mod 32, then the lane combine and
+// reduce_add tree). The router is read as 32 KB per block instead of 256 KB in every gate/up
+// block. Every block recomputes the residual, so h_out must not alias h_in; block 0 of a token
+// writes h_out and normed, and the blocks share out the XQ records of normed (model.rs:501,
+// with the pair dwords).
+constexpr int RN_EXPERTS = 4;
+__global__ void __launch_bounds__(256) k_residual_norm_route(const float* __restrict__ h_in, float* __restrict__ h_out,
+                                                             const float* __restrict__ slots,
+                                                             const float* __restrict__ wts, int K,
+                                                             const float* __restrict__ ffn,
+                                                             const float* __restrict__ gain, float eps, int n,
+                                                             float* __restrict__ normed, const float* __restrict__ Wr,
+                                                             int E, float* __restrict__ logits, XQBufs xq) {
+  __shared__ __align__(16) float xs[GU_H_MAX];
+  __shared__ float part[RN_EXPERTS][33];
+  __shared__ double s_part[4];
+  __shared__ float s_scale;
+  const int t = blockIdx.y, eb = blockIdx.x, tid = threadIdx.x;
+  // the residual (thread j: elements j, j+256, ...), every load before the first use; the
+  // router's after them, so the residual waits for its own loads only
+  constexpr int NI = GU_H_MAX / 256;
+  float hr[NI], yr[NI], gr[NI];
+  const size_t row = (size_t)t * n;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) gr[it] = gain[min(tid + 256 * it, n - 1)];
+  if (slots) {
+    float wk[8], sv[8][NI];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const size_t srow = (size_t)t * K + min(k, K - 1);
+      wk[k] = wts[srow];
+#pragma unroll
+      for (int it = 0; it < NI; ++it) sv[k][it] = slots[srow * n + min(tid + 256 * it, n - 1)];
+    }
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      hr[it] = h_in[row + min(tid + 256 * it, n - 1)];
+      yr[it] = 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < K) {
+#pragma unroll
+        for (int it = 0; it < NI; ++it) yr[it] = yr[it] + wk[k] * sv[k][it];
+      }
+  } else {
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      hr[it] = h_in[row + min(tid + 256 * it, n - 1)];
+      yr[it] = ffn[row + min(tid + 256 * it, n - 1)];
+    }
+  }
+  // thread (el, c) runs chain c of expert 4eb + el (threads 128.. load the same values again
+  // and drop them)
+  const int el = (tid >> 5) & (RN_EXPERTS - 1), c = tid & 31, nm4 = n / 128;
+  const int e = min(RN_EXPERTS * eb + el, E - 1);
+  float4 wv[GU_H_MAX / 128];
+  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + e;
+#pragma unroll
+  for (int k = 0; k < GU_H_MAX / 128; ++k) wv[k] = wr[(size_t)min(k, nm4 - 1) * E];
+  double ss = 0.0;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int i = tid + 256 * it;
+    if (i >= n) break;
+    const float v = hr[it] + yr[it];
+    hr[it] = v;
+    ss += (double)(v * v);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+  lds_barrier();
+  if (tid == 0) {
+    const double tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float mean = (float)(tot / (double)n);
+    s_scale = 1.0f / sqrtf(mean + eps);
+  }
+  lds_barrier();
+  const float scale = s_scale;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int i = tid + 256 * it;
+    if (i >= n) break;
+    const float nv = hr[it] * scale * gr[it];
+    xs[i] = nv;
+    if (eb == 0) {
+      h_out[row + i] = hr[it];
+      normed[row + i] = nv;
+    }
+  }
+  lds_barrier();
+  {
+    // the XQ records of the normed row: 256-block bk by the last wave of block bk mod gridDim.x
+    // (the other waves run the chains meanwhile)
+    const int lane = tid & 63, nbx = n / QK;
+    if ((tid >> 6) == 3)
+      for (int bk = eb; bk < nbx; bk += gridDim.x) {
+        const float4 v = *reinterpret_cast<const float4*>(xs + bk * QK + 4 * lane);
+        wave_quantize_xq(v, xq.q + row + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                         xq.pairs + ((size_t)t * nbx + bk) * 12);
+      }
+  }
+  if (tid < 32 * RN_EXPERTS) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < GU_H_MAX / 128; ++k) {
+      if (k < nm4) {
+        const float* xk = xs + 128 * k + c;
+        acc = fmaf(wv[k].x, xk[0], acc);
+        acc = fmaf(wv[k].y, xk[32], acc);
+        acc = fmaf(wv[k].z, xk[64], acc);
+        acc = fmaf(wv[k].w, xk[96], acc);
+      }
+    }
+    part[el][c] = acc;
+  }
+  lds_barrier();
+  if (tid < RN_EXPERTS && RN_EXPERTS * eb + tid < E) {
+    const float* p = part[tid];
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (p[j] + p[j + 8]) + (p[j + 16] + p[j + 24]);
+    logits[(size_t)t * E + RN_EXPERTS * eb + tid] = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+  }
+}
+
+hipError_t launch_residual_norm_route(hipStream_t s, const float* h_in, float* h_out, const float* slots,
+                                      const float* wts, int K, const float* ffn, const float* gain, float eps, int n,
+                                      int T, float* normed, const float* router, int E, float* logits, XQBufs xq) {
+  if (n > GU_H_MAX || n % 128 != 0 || E > 32 || K > 8 || T < 1 || !gain || !xq.pairs) return hipErrorInvalidValue;
+  BB_LAUNCH(k_residual_norm_route, dim3((unsigned)((E + RN_EXPERTS - 1) / RN_EXPERTS), (unsigned)T), dim3(256), 0, s,
+            h_in, h_out, slots, wts, K, ffn, gain, eps, n, normed, router, E, logits, xq);
   return hipGetLastError();
 }
 

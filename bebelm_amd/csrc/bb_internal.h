@@ -59,6 +59,7 @@ enum KernelId : int {
   K_GEMM_DOWN,
   K_COMBINE,
   K_RESIDUAL_NORM,
+  K_RESIDUAL_ROUTE,
   K_COUNT
 };
 const char* kernel_name(int id);
@@ -112,6 +113,18 @@ constexpr int ROUTE_IN_GATEUP_MAX_T = 4;
 hipError_t launch_route_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
                                int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
                                const float* router, const float* bias, const float* x, float* act);
+// The same gate/up GEMV with the tokens gated in every block from router logits computed before
+// (launch_residual_norm_route) and their XQ records in xq: no launch_route before it.
+hipError_t launch_gate_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
+                              int E, int K, int max_hit, int batch_mode, int publish, const RouteBufs& rb,
+                              const float* logits, const float* bias, XQBufs xq, float* act);
+// The layer boundary of a stack of at most ROUTE_IN_GATEUP_MAX_T tokens before an MoE layer:
+// h_out = h_in + the combine of slots (or + ffn when slots is null), normed = its rmsnorm with
+// gain, and the next layer's router logits (router in k_route's chain-major layout, E experts)
+// and the XQ records (with pairs) of normed. h_out must not alias h_in.
+hipError_t launch_residual_norm_route(hipStream_t s, const float* h_in, float* h_out, const float* slots,
+                                      const float* wts, int K, const float* ffn, const float* gain, float eps, int n,
+                                      int T, float* normed, const float* router, int E, float* logits, XQBufs xq);
 
 // gu / dn: tile-packed gate+up and down tensors; stride_*: packed bytes per expert.
 hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F, int E,
