@@ -63,11 +63,13 @@ def kernel_names(T, K, E, batched):
     return GEMM_KERNELS if batched else DECODE_KERNELS
 
 
-def layer_work(w, counts, T, batched):
+def layer_work(w, counts, T, batched, prerouted=False):
     """Algorithmic bytes and int8 operations per kernel launch of one MoE layer.
 
     Bytes: weights of the hit experts (each read once), activations in, results out; no
-    intermediates re-read. Operations: 2 per multiply-add of the expert GEMMs."""
+    intermediates re-read. Operations: 2 per multiply-add of the expert GEMMs. prerouted: the
+    router logits and the XQ records come from the stack's layer boundary (the gate/up GEMV
+    reads them instead of the router and the f32 rows)."""
     from bebelm_amd import synth
 
     H, F, K = w.hidden, w.moe_ff, w.n_used
@@ -75,7 +77,9 @@ def layer_work(w, counts, T, batched):
     u_hit = int(np.count_nonzero(counts))
     gu = synth.byte_size(w.gate_dtype, H * F) + synth.byte_size(w.up_dtype, H * F)
     dn = synth.byte_size(w.down_dtype, F * H)
-    if not batched and T <= ROUTE_IN_GATEUP_MAX_T:
+    if not batched and T <= ROUTE_IN_GATEUP_MAX_T and prerouted:
+        gate_b = u_hit * gu + T * (q8_bytes(H) + H // 256 * 48) + T * w.n_experts * 4 + n_ent * F * 4
+    elif not batched and T <= ROUTE_IN_GATEUP_MAX_T:
         # the kernel also routes: the router and the f32 rows are its inputs
         gate_b = u_hit * gu + w.router.nbytes + T * H * 4 + n_ent * F * 4
     else:
@@ -170,7 +174,8 @@ def main():
             if isinstance(w, synth.MoeWeights):
                 tr = RouteTrace(1, w.n_experts, w.n_used)
                 layer.forward(normed, 1, y, tr)
-                layers_work.append(layer_work(w, tr.counts, 1, False))
+                # (every MoE layer follows a layer boundary that computes its logits)
+                layers_work.append(layer_work(w, tr.counts, 1, False, prerouted=True))
             else:
                 layer.forward(normed, 1, y)
             h = (h + y).astype(np.float32)
