@@ -17,79 +17,9 @@
 #include "bb_internal.h"
 #include "bb_members.h"
 #include "bb_rowlane.h"
+#include "bb_gating.h"
 
 namespace bb {
-
-// ---- gating ----------------------------------------------------------------------------------------
-// max over each 32-lane half of the wave (all 64 lanes active); lanes < 32 get the low half's
-__device__ __forceinline__ int half_max(int v) {
-  auto dpp = [](int x, auto ctrl) {
-    return __builtin_amdgcn_update_dpp(0, x, decltype(ctrl)::value, 0xf, 0xf, false);
-  };
-  v = max(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad [1,0,3,2]
-  v = max(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad [2,3,0,1]
-  v = max(v, dpp(v, std::integral_constant<int, 0x141>{}));  // half-row mirror
-  v = max(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row mirror
-  const int lo = max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16));
-  const int hi = max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48));
-  return (threadIdx.x & 32) ? hi : lo;
-}
-
-__device__ __forceinline__ float readlane_f(float v, int l) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-
-// Gating of one token per half-wave (model.rs:485-495): lane e of the half-wave holds expert e's
-// logit. sigmoid, key = score + bias, the top k by total_cmp in k rounds of a half-wave maximum
-// (the lowest expert index first among equal keys), weights = score / (scores summed in rank
-// order from -0.0, + 1e-6). Also the margin between the k-th and (k+1)-th keys and the number
-// of selected experts whose key another expert after them shares. Every lane of the wave
-// calls it; live is false for lanes of absent tokens or experts. The results go to rb when
-// global_out is set, and the selections also to lds_sel[t*K + rank] when it is not null.
-__device__ __forceinline__ void gate_halfwave(float logit, bool live, bool tok, float bias_e, int t, int E, int K,
-                                              const uint64_t* exptab, RouteBufs rb, bool global_out = true,
-                                              int32_t* lds_sel = nullptr) {
-  const int lane = threadIdx.x & 63, e = lane & 31;
-  const float s = live ? sigmoid_tab(logit, exptab) : 0.0f;
-  const float key = live ? s + bias_e : 0.0f;
-  const int32_t kk = total_key(key);
-  bool avail = live;
-  int rank = 64, ties = 0;
-  float denom = -0.0f, key_k1 = 0.0f, key_k = 0.0f;
-  const bool hi = (lane & 32) != 0;
-  const int nr = min(K + 1, E);
-  for (int rd = 0; rd < nr; ++rd) {
-    const int m = half_max(avail ? kk : -2147483647 - 1);
-    const uint64_t eq = __ballot(avail && kk == m);
-    const uint32_t e0 = (uint32_t)eq, e1 = (uint32_t)(eq >> 32);
-    const int f0 = e0 ? __builtin_ctz(e0) : 0, f1 = e1 ? __builtin_ctz(e1) : 0;
-    const float s0 = readlane_f(s, f0), s1 = readlane_f(s, 32 + f1);
-    const float k0 = readlane_f(key, f0), k1 = readlane_f(key, 32 + f1);
-    const uint32_t eh = hi ? e1 : e0;
-    if (eh != 0 && e == (hi ? f1 : f0)) {
-      rank = rd;
-      avail = false;
-    }
-    if (rd < K) {
-      if (eh != 0) denom += hi ? s1 : s0;
-      ties += __popc(eh) > 1 ? 1 : 0;
-    }
-    if (rd == K - 1) key_k1 = hi ? k1 : k0;
-    if (rd == K) key_k = hi ? k1 : k0;
-  }
-  denom = denom + 1e-6f;
-  if (live && rank < K) {
-    if (lds_sel) lds_sel[t * K + rank] = e;
-    if (global_out) {
-      rb.sel[(size_t)t * K + rank] = e;
-      rb.wts[(size_t)t * K + rank] = s / denom;
-    }
-  }
-  if (global_out && tok && e == 0) {
-    rb.margin[t] = K < E ? key_k1 - key_k : __builtin_inff();
-    rb.ties[t] = ties;
-  }
-}
 
 // ---- router + gating + XQ of x ------------------------------------------------------------------
 // Block of 1024 threads for tpb consecutive tokens. The router dot (matmul.rs:36-66) runs as 32
@@ -304,23 +234,6 @@ __device__ void route_block(const float* __restrict__ Wr, const float* __restric
     const bool tok = i < T, live = tok && e < E;
     gate_halfwave(live ? sm.lg[i][e] : 0.0f, live, tok, bias_i, i, E, K, exptab, rb, global_out, sm.sel);
   }
-  lds_barrier();
-}
-
-// The gating alone (gate_halfwave per token), from logits computed before the launch (by
-// k_residual_norm_route at the layer boundary): selections into sel_lds, and the route's outputs
-// to rb when global_out.
-__device__ void gate_block(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int K,
-                           bool global_out, RouteBufs rb, int32_t* sel_lds, uint64_t* exptab, uint64_t exp_e) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int i = tid >> 5, e = lane & 31;  // half-wave i gates token i
-  const bool tok = i < T, live = tok && e < E;
-  const float lg = logits[min(i, T - 1) * E + min(e, E - 1)];
-  const float be = bias[min(e, E - 1)];
-  if (tid < 32) exptab[tid] = exp_e;
-  lds_barrier();
-  if (2 * wave < T) gate_halfwave(live ? lg : 0.0f, live, tok, be, i, E, K, exptab, rb, global_out, sel_lds);
-  if (global_out && live) rb.logits[(size_t)i * E + e] = lg;
   lds_barrier();
 }
 
@@ -653,6 +566,58 @@ hipError_t launch_pack_rows(hipStream_t s, int dtype, const uint8_t* a, const ui
 // writes h_out and normed, and the blocks share out the XQ records of normed (model.rs:501,
 // with the pair dwords).
 constexpr int RN_EXPERTS = 4;
+
+// The router values of the chain a thread of a 256-thread block runs: chain c = tid % 32 of
+// expert 4eb + (tid / 32) % 4 (threads 128.. load the same values again and drop them).
+struct RouterChain {
+  float4 v[GU_H_MAX / 128];
+};
+__device__ __forceinline__ void rl_load(const float* __restrict__ Wr, int n, int E, int eb, RouterChain& rc) {
+  const int tid = threadIdx.x, el = (tid >> 5) & (RN_EXPERTS - 1), c = tid & 31, nm4 = n / 128;
+  const int e = min(RN_EXPERTS * eb + el, E - 1);
+  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + e;
+#pragma unroll
+  for (int k = 0; k < GU_H_MAX / 128; ++k) rc.v[k] = wr[(size_t)min(k, nm4 - 1) * E];
+}
+
+// From token t's row xs (LDS, after a barrier): the XQ records of 256-blocks eb, eb + nblk, ...
+// by the last wave (the pair dwords when xq.pairs is set), the logits of experts 4eb..4eb+3
+// (k_route's chains and tree) by the rest.
+__device__ __forceinline__ void rl_finish(const float* xs, const RouterChain& rc, int n, int E, int t, int eb,
+                                          int nblk, float* __restrict__ logits, XQBufs xq,
+                                          float (&part)[RN_EXPERTS][33]) {
+  const int tid = threadIdx.x, lane = tid & 63, el = (tid >> 5) & (RN_EXPERTS - 1), c = tid & 31;
+  const int nm4 = n / 128, nbx = n / QK;
+  if ((tid >> 6) == 3)
+    for (int bk = eb; bk < nbx; bk += nblk) {
+      const float4 v = *reinterpret_cast<const float4*>(xs + bk * QK + 4 * lane);
+      wave_quantize_xq(v, xq.q + (size_t)t * n + bk * QK, xq.sx + (size_t)t * nbx + bk,
+                       xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+    }
+  if (tid < 32 * RN_EXPERTS) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < GU_H_MAX / 128; ++k) {
+      if (k < nm4) {
+        const float* xk = xs + 128 * k + c;
+        acc = fmaf(rc.v[k].x, xk[0], acc);
+        acc = fmaf(rc.v[k].y, xk[32], acc);
+        acc = fmaf(rc.v[k].z, xk[64], acc);
+        acc = fmaf(rc.v[k].w, xk[96], acc);
+      }
+    }
+    part[el][c] = acc;
+  }
+  lds_barrier();
+  if (tid < RN_EXPERTS && RN_EXPERTS * eb + tid < E) {
+    const float* p = part[tid];
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (p[j] + p[j + 8]) + (p[j + 16] + p[j + 24]);
+    logits[(size_t)t * E + RN_EXPERTS * eb + tid] = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+  }
+}
+
 __global__ void __launch_bounds__(256) k_residual_norm_route(const float* __restrict__ h_in, float* __restrict__ h_out,
                                                              const float* __restrict__ slots,
                                                              const float* __restrict__ wts, int K,
@@ -699,14 +664,8 @@ __global__ void __launch_bounds__(256) k_residual_norm_route(const float* __rest
       yr[it] = ffn[row + min(tid + 256 * it, n - 1)];
     }
   }
-  // thread (el, c) runs chain c of expert 4eb + el (threads 128.. load the same values again
-  // and drop them)
-  const int el = (tid >> 5) & (RN_EXPERTS - 1), c = tid & 31, nm4 = n / 128;
-  const int e = min(RN_EXPERTS * eb + el, E - 1);
-  float4 wv[GU_H_MAX / 128];
-  const float4* wr = reinterpret_cast<const float4*>(Wr) + (size_t)c * nm4 * E + e;
-#pragma unroll
-  for (int k = 0; k < GU_H_MAX / 128; ++k) wv[k] = wr[(size_t)min(k, nm4 - 1) * E];
+  RouterChain rc;
+  rl_load(Wr, n, E, eb, rc);
   double ss = 0.0;
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
@@ -739,39 +698,7 @@ __global__ void __launch_bounds__(256) k_residual_norm_route(const float* __rest
     }
   }
   lds_barrier();
-  {
-    // the XQ records of the normed row: 256-block bk by the last wave of block bk mod gridDim.x
-    // (the other waves run the chains meanwhile)
-    const int lane = tid & 63, nbx = n / QK;
-    if ((tid >> 6) == 3)
-      for (int bk = eb; bk < nbx; bk += gridDim.x) {
-        const float4 v = *reinterpret_cast<const float4*>(xs + bk * QK + 4 * lane);
-        wave_quantize_xq(v, xq.q + row + bk * QK, xq.sx + (size_t)t * nbx + bk,
-                         xq.pairs + ((size_t)t * nbx + bk) * 12);
-      }
-  }
-  if (tid < 32 * RN_EXPERTS) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < GU_H_MAX / 128; ++k) {
-      if (k < nm4) {
-        const float* xk = xs + 128 * k + c;
-        acc = fmaf(wv[k].x, xk[0], acc);
-        acc = fmaf(wv[k].y, xk[32], acc);
-        acc = fmaf(wv[k].z, xk[64], acc);
-        acc = fmaf(wv[k].w, xk[96], acc);
-      }
-    }
-    part[el][c] = acc;
-  }
-  lds_barrier();
-  if (tid < RN_EXPERTS && RN_EXPERTS * eb + tid < E) {
-    const float* p = part[tid];
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (p[j] + p[j + 8]) + (p[j + 16] + p[j + 24]);
-    logits[(size_t)t * E + RN_EXPERTS * eb + tid] = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
-  }
+  rl_finish(xs, rc, n, E, t, eb, gridDim.x, logits, xq, part);
 }
 
 hipError_t launch_residual_norm_route(hipStream_t s, const float* h_in, float* h_out, const float* slots,
