@@ -303,6 +303,7 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
   else
     need(n_ent <= (size_t)bb::MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
   MoeWs w = carve_moe(c, m, T, batched);
+  const bool combine_in_down = !batched && combine && T == 1 && m->K <= 4 && m->H % 16 == 0 && m->F / 256 <= 8;
   if (batched) {
     // model.rs:286-371: route all tokens, group entries by expert, grouped GEMMs, combine
     launch(c, bb::K_ROUTE_LARGE, [&] {
@@ -347,12 +348,20 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
       return bb::launch_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
                                max_hit, batch_mode, tr != nullptr, w.rb, w.xq, w.act);
     });
-    launch(c, bb::K_DOWN, [&] {
-      return bb::launch_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->K, max_hit,
-                             batch_mode, w.rb, w.act, w.slots);
-    });
+    if (combine_in_down) {
+      // one token: the down GEMV also combines (no slot rows)
+      launch(c, bb::K_DOWN, [&] {
+        return bb::launch_down_combine1(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, m->H, m->F, m->K, w.rb,
+                                        w.act, out);
+      });
+    } else {
+      launch(c, bb::K_DOWN, [&] {
+        return bb::launch_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->K, max_hit,
+                               batch_mode, w.rb, w.act, w.slots);
+      });
+    }
   }
-  if (combine)
+  if (combine && !combine_in_down)
     launch(c, bb::K_COMBINE, [&] { return bb::launch_combine(c->stream, w.slots, w.rb.wts, (int)T, m->H, m->K, out); });
   if (tr) {
     const size_t E = m->E, K = m->K;

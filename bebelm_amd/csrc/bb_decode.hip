@@ -504,6 +504,72 @@ hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t strid
                                    slots);
 }
 
+// ---- down GEMV and combine of one token ---------------------------------------------------------
+// Block b takes output rows 16b..16b+15 for all K (<= 4) selected experts: lane l = (slot
+// k = l/16, row r = l%16) holds super-block w of row r of the expert of slot k, wave w owning
+// super-block w as in k_experts. The block first quantises the token's K act rows into LDS
+// (quantize_q8 per row, model.rs:530-534), sums each (slot, row)'s block values left to right
+// from -0.0 (the decode path's Iterator::sum, model.rs:529-548), and combines the slots in
+// selection order from +0.0 (k_combine, model.rs:550-553): every term of its outputs is in the
+// block, so the expert outputs make no round trip through memory and need no combine launch.
+template <int DT>
+__global__ void __launch_bounds__(512) k_down_combine1(const uint8_t* __restrict__ wpk, size_t stride_e, int H,
+                                                       int F, int K, RouteBufs rb, const float* __restrict__ act,
+                                                       float* __restrict__ out) {
+  using R = LaneRow<DT>;
+  __shared__ __align__(16) int8_t xq[4][DN_F_MAX];
+  __shared__ uint32_t pairs[4][DN_F_MAX / QK][12];
+  __shared__ float sxs[4][DN_F_MAX / QK];
+  __shared__ float tv[8][64];  // [super-block][lane]
+  __shared__ float slot[4][16];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int k = min(lane >> 4, K - 1), r = lane & 15;
+  const int nb = F / QK;
+  const int orow = 16 * blockIdx.x + r;
+  const int e = rb.sel[k];  // T = 1: entry k is slot k
+  const size_t tile_bytes = (size_t)nb * R::TB_BYTES;
+  const bool has_blk = w < nb;
+  typename R::Loaded L;
+  if (has_blk) R::load(L, wpk + (size_t)e * stride_e + (size_t)(orow / 64) * tile_bytes + (size_t)w * R::TB_BYTES,
+                       orow % 64);
+  // the act rows of the K entries, one wave per 256-block
+  for (int task = w; task < K * nb; task += 8) {
+    const int m = task / nb, b = task % nb;
+    const float4 v = *reinterpret_cast<const float4*>(act + (size_t)m * F + b * QK + 4 * lane);
+    wave_quantize_xq(v, xq[m] + b * QK, &sxs[m][b], pairs[m][b]);
+  }
+  lds_barrier();
+  float v = 0.0f;
+  if (has_blk) {
+    typename R::Blk B;
+    R::prep(B, L);
+    v = R::value(B, xq[k] + w * QK, pairs[k][w], sxs[k][w]);
+  }
+  tv[w][lane] = v;
+  lds_barrier();
+  if (w == 0) {
+    float acc = -0.0f;
+    for (int b = 0; b < nb; ++b) acc += tv[b][lane];
+    if ((lane >> 4) < K) slot[lane >> 4][r] = acc;
+  }
+  lds_barrier();
+  if (tid < 16) {
+    float y = 0.0f;
+    for (int j = 0; j < K; ++j) y = y + rb.wts[j] * slot[j][tid];
+    out[16 * blockIdx.x + tid] = y;
+  }
+}
+
+hipError_t launch_down_combine1(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int H, int F, int K,
+                                const RouteBufs& rb, const float* act, float* out) {
+  if (K < 1 || K > 4 || H % 16 != 0 || F % QK != 0 || F / QK > 8 || F > DN_F_MAX) return hipErrorInvalidValue;
+  if (dtype == DT_Q4_K)
+    BB_LAUNCH(k_down_combine1<DT_Q4_K>, dim3(H / 16), dim3(512), 0, s, dn, stride_dn, H, F, K, rb, act, out);
+  else
+    BB_LAUNCH(k_down_combine1<DT_Q6_K>, dim3(H / 16), dim3(512), 0, s, dn, stride_dn, H, F, K, rb, act, out);
+  return hipGetLastError();
+}
+
 // ---- tile packing ------------------------------------------------------------------------------
 // One thread per 16-byte chunk (and per tail u16) of the packed output; raw blocks are only
 // 2-byte aligned (Q6_K), so the chunk is read as eight u16.

@@ -132,6 +132,10 @@ hipError_t launch_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t str
 
 hipError_t launch_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int K,
                        int max_hit, int batch_mode, const RouteBufs& rb, const float* act, float* slots);
+// Down GEMV and combine of one token (K <= 4, F/256 <= 8): out[H] = Σ_k wts[k] · (down row of the
+// expert of slot k · Q8(act row k)), no slot rows written.
+hipError_t launch_down_combine1(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int H, int F, int K,
+                                const RouteBufs& rb, const float* act, float* out);
 
 // ---- batched (prefill) path ----------------------------------------------------------------------
 // Largest T*k of one call on this path (the dispatch keeps per-64-entry counts in LDS).

@@ -73,12 +73,11 @@ struct Q4Blk {
   float d, dmin;
 };
 
-// tb: the tile-block (tile-packed layout); chunk k of this lane's row block is at
-// tb + 1024k + 16·lane, so each load of the wave reads 1 KB of contiguous memory.
-__device__ __forceinline__ void q4_load(uint4 (&w)[9], const uint8_t* __restrict__ tb) {
-  const int lane = threadIdx.x & 63;
+// tb: the tile-block (tile-packed layout); chunk k of row j's block is at tb + 1024k + 16j.
+// Row = lane: each load of the wave reads 1 KB of contiguous memory.
+__device__ __forceinline__ void q4_load(uint4 (&w)[9], const uint8_t* __restrict__ tb, int row) {
 #pragma unroll
-  for (int k = 0; k < 9; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * lane);
+  for (int k = 0; k < 9; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * row);
 }
 
 // get_scale_min_k4 (dequant.rs:64-72) on four bytes at a time, then the nibble unpack
@@ -151,11 +150,10 @@ struct Q6Blk {
 };
 
 // Bytes 0..207 of the block (ql, qh, scales) in 13 chunks, then the f16 d from the tail.
-__device__ __forceinline__ void q6_load(uint4 (&w)[13], uint32_t& dbits, const uint8_t* __restrict__ tb) {
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void q6_load(uint4 (&w)[13], uint32_t& dbits, const uint8_t* __restrict__ tb, int row) {
 #pragma unroll
-  for (int k = 0; k < 13; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * lane);
-  dbits = *reinterpret_cast<const uint16_t*>(tb + 13 * 1024 + 2 * lane);
+  for (int k = 0; k < 13; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * row);
+  dbits = *reinterpret_cast<const uint16_t*>(tb + 13 * 1024 + 2 * row);
 }
 
 // dequant.rs:122-138 / matmul.rs:496-525: element 128n + 32g + l takes the low (g<2) or high
@@ -220,7 +218,10 @@ struct LaneRow<DT_Q4_K> {
   struct Loaded {
     uint4 w[9];
   };
-  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* blk) { q4_load(L.w, blk); }
+  // row j of the tile-block at blk (j = the lane when omitted)
+  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* blk, int j = threadIdx.x & 63) {
+    q4_load(L.w, blk, j);
+  }
   static __device__ __forceinline__ void prep(Blk& B, const Loaded& L) { q4_prep(B, L.w); }
   static __device__ __forceinline__ float value(const Blk& B, const int8_t* xq, const uint32_t* pairs, float sx) {
     return q4_value(B, xq, pairs, sx);
@@ -235,7 +236,9 @@ struct LaneRow<DT_Q6_K> {
     uint4 w[13];
     uint32_t dbits;
   };
-  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* tb) { q6_load(L.w, L.dbits, tb); }
+  static __device__ __forceinline__ void load(Loaded& L, const uint8_t* tb, int j = threadIdx.x & 63) {
+    q6_load(L.w, L.dbits, tb, j);
+  }
   static __device__ __forceinline__ void prep(Blk& B, const Loaded& L) { q6_prep(B, L.w, L.dbits); }
   static __device__ __forceinline__ float value(const Blk& B, const int8_t* xq, const uint32_t* pairs, float sx) {
     return q6_value(B, xq, pairs, sx);

@@ -84,7 +84,10 @@ def layer_work(w, counts, T, batched, prerouted=False):
         gate_b = u_hit * gu + w.router.nbytes + T * H * 4 + n_ent * F * 4
     else:
         gate_b = u_hit * gu + T * q8_bytes(H) + n_ent * F * 4
-    down_b = u_hit * dn + n_ent * (F * 4 if not batched else q8_bytes(F)) + n_ent * H * 4
+    # one token on its own (not in the stack): the down GEMV also combines, writing H outputs
+    # instead of K slot rows
+    combine_in_down = not batched and T == 1 and K <= 4 and not prerouted
+    down_b = u_hit * dn + n_ent * (F * 4 if not batched else q8_bytes(F)) + (T if combine_in_down else n_ent) * H * 4
     gate_ops = 2.0 * n_ent * 2 * F * H
     down_ops = 2.0 * n_ent * F * H
     names = kernel_names(T, K, w.n_experts, batched)
