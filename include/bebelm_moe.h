@@ -4,7 +4,7 @@
  * This is the drop-in boundary for the reference's (maximecb/bebelm 0.3.6, Rust) sparse-MoE
  * FFN path. The reference has no FFI of its own; each entry point below names the Rust
  * function or signature it replaces (paths relative to the reference's src/). A Rust caller
- * binds these with `extern "C"` declarations (INTEGRATION.md shows the binding).
+ * binds these with `extern "C"` declarations in an `unsafe` FFI module.
  *
  * Conventions
  *   - Every entry point returns int: 0 (BB_OK) on success, a BB_ERR_* code otherwise, with a
