@@ -60,6 +60,25 @@ def test_matvec_quantized(gpu_ctx, oracle, dtype, n_in, n_out):
 
 
 @pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n_in,nt", [(3072, 1), (12288, 1), (12288, 3), (16640, 2)])
+def test_rows_long(gpu_ctx, oracle, dtype, n_in, nt):
+    # rows of 12, 48 and 65 super-blocks: two blocks per lane group, two passes of loads per
+    # row (weights reloaded per token past 32 blocks), and past 64 blocks the 8-lane kernel
+    n_out = 40
+    w = synth.quant_tensor(synth.rng(7, dtype, n_in), dtype, n_in, n_out)
+    x = synth.hidden_states(8, nt, hidden=n_in).reshape(-1)
+    t = Tensor(gpu_ctx, dtype, w, (n_in, n_out))
+    y = np.empty(nt * n_out, np.float32)
+    if nt == 1:
+        K.matvec(gpu_ctx, dtype, t, n_in, n_out, x, y)
+        want = oracle.matvec(dtype, w, n_in, n_out, x)
+    else:
+        K.matmul(gpu_ctx, dtype, t, n_in, n_out, x, nt, y)
+        want = oracle.matmul(dtype, w, n_in, n_out, x, nt)
+    assert_bits(y, want, f"rows n_in={n_in} nt={nt}")
+
+
+@pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
 def test_matmul_quantized_and_expert_slice(gpu_ctx, oracle, dtype):
     n_in, n_out, n_exp, nt = 512, 96, 3, 5
     w = synth.quant_tensor(synth.rng(5, dtype), dtype, n_in, n_out, n_exp)
