@@ -79,6 +79,35 @@ def test_rows_long(gpu_ctx, oracle, dtype, n_in, nt):
 
 
 @pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n_in,n_out,nt", [(2048, 16384, 1), (512, 16390, 1), (2048, 16391, 3)])
+def test_rows_many(gpu_ctx, oracle, dtype, n_in, n_out, nt):
+    # matrices of 16384 rows and more take several rows per wave; 16390 and 16391 rows leave a
+    # last wave with rows past the matrix
+    w = synth.quant_tensor(synth.rng(9, dtype, n_out), dtype, n_in, n_out)
+    x = synth.hidden_states(10, nt, hidden=n_in).reshape(-1)
+    t = Tensor(gpu_ctx, dtype, w, (n_in, n_out))
+    y = np.empty(nt * n_out, np.float32)
+    if nt == 1:
+        K.matvec(gpu_ctx, dtype, t, n_in, n_out, x, y)
+        want = oracle.matvec(dtype, w, n_in, n_out, x)
+    else:
+        K.matmul(gpu_ctx, dtype, t, n_in, n_out, x, nt, y)
+        want = oracle.matmul(dtype, w, n_in, n_out, x, nt)
+    assert_bits(y, want, f"rows n_in={n_in} n_out={n_out} nt={nt}")
+
+
+def test_logits_head_shape(gpu_ctx, oracle):
+    # logits_from_hidden's matvec (model.rs:380-388): Q6_K 2048 -> 128000, 215 MB of rows
+    n_in, n_out = 2048, 128000
+    w = synth.quant_tensor(synth.rng(11, Q6_K), Q6_K, n_in, n_out)
+    x = synth.hidden_states(12, 1, hidden=n_in).reshape(-1)
+    t = Tensor(gpu_ctx, Q6_K, w, (n_in, n_out))
+    y = np.empty(n_out, np.float32)
+    K.matvec(gpu_ctx, Q6_K, t, n_in, n_out, x, y)
+    assert_bits(y, oracle.matvec(Q6_K, w, n_in, n_out, x), "logits head")
+
+
+@pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
 def test_matmul_quantized_and_expert_slice(gpu_ctx, oracle, dtype):
     n_in, n_out, n_exp, nt = 512, 96, 3, 5
     w = synth.quant_tensor(synth.rng(5, dtype), dtype, n_in, n_out, n_exp)
