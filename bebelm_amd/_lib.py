@@ -68,6 +68,7 @@ _SIGS = {
     "bb_add_scaled": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_size_t, c_int]),
     "bb_add_assign": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_int]),
     "bb_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_size_t, c_size_t, c_void_p, c_int]),
+    "bb_logits_from_hidden": (c_int, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int]),
     "bb_moe_create": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, P(c_void_p)]),
     "bb_moe_destroy": (c_int, [c_void_p]),
     "bb_moe_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int, P(RouteTrace)]),

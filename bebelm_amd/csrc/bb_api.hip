@@ -781,6 +781,34 @@ int bb_rmsnorm(bb_ctx* c, const float* x, const float* gain, float eps, size_t n
   });
 }
 
+int bb_logits_from_hidden(bb_ctx* c, const bb_tensor* tok_embd, const float* gain, float eps, const float* h,
+                          float* logits, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(tok_embd && gain && h && logits, BB_ERR_ARG, "null argument");
+    need(tok_embd->ndims == 2, BB_ERR_SHAPE, "token_embd must be [hidden, vocab]");
+    const size_t H = tok_embd->dims[0], V = tok_embd->dims[1];
+    set_device(c);
+    with_io(c, loc, {{h, H * 4, true, false}, {gain, H * 4, true, false}, {logits, V * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              // normed lives past the Q8 records matmul_dev carves from the workspace's start
+              Carve cv{nullptr};
+              cv.take<int8_t>(H);
+              cv.take<float>(H / 256);
+              cv.take<int32_t>(H / 32);
+              const size_t q8_bytes = cv.off;
+              cv.take<float>(H);
+              float* normed = reinterpret_cast<float*>(ensure_ws(c, cv.off) + q8_bytes);
+              launch(c, bb::K_RMSNORM, [&] {
+                return bb::launch_rmsnorm(c->stream, static_cast<const float*>(d[0]), static_cast<const float*>(d[1]),
+                                          eps, H, 1, normed);
+              });
+              matmul_dev(c, tok_embd->dtype, tok_embd, 0, H, V, normed, 1, static_cast<float*>(d[2]));
+            });
+  });
+}
+
 int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const bb_tensor* gate, const bb_tensor* up,
                   const bb_tensor* down, int n_used, bb_moe** out) {
   return guard([&] {

@@ -7,6 +7,7 @@
   swiglu / sigmoid_slice                   kernels/activation.rs:16, :25
   add_scaled / add_assign                  kernels/elementwise.rs:12, :4
   rmsnorm                                  kernels/rmsnorm.rs:10
+  logits_from_hidden                       model.rs:380-388
 Each function takes the Context first; `w` is an uploaded Tensor (plus a byte offset where the
 reference passes a sub-slice of the weight bytes).
 """
@@ -95,6 +96,13 @@ def rmsnorm(ctx, x, gain, eps, out, n_vec=1):
     check(lib().bb_rmsnorm(ctx.handle, _ptr(x)[0], _ptr(gain)[0], ctypes.c_float(eps), n, n_vec, _ptr(out)[0],
                            _same_loc(x, gain, out)))
     return out
+
+
+def logits_from_hidden(ctx, tok_embd, gain, eps, h, logits):
+    """Model::logits_from_hidden (model.rs:380-388): rmsnorm, then the token_embd matvec."""
+    loc = _same_loc(h, gain, logits)
+    check(lib().bb_logits_from_hidden(ctx.handle, tok_embd.handle, _ptr(gain)[0], eps, _ptr(h)[0], _ptr(logits)[0], loc))
+    return logits
 
 
 def _n(a):

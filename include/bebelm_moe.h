@@ -127,6 +127,12 @@ int bb_add_assign(bb_ctx* ctx, float* a, const float* b, size_t n, int loc);
 int bb_rmsnorm(bb_ctx* ctx, const float* x, const float* gain, float eps, size_t n, size_t n_vec, float* out,
                int loc);
 
+/* Model::logits_from_hidden(h) (model.rs:380-388): rmsnorm(h, gain, eps) (as bb_rmsnorm), then
+ * matvec(token_embd dtype, token_embd, hidden, vocab, normed, logits). token_embd is [hidden,
+ * vocab] (any dtype bb_matvec takes); h and gain f32[hidden], logits f32[vocab]. */
+int bb_logits_from_hidden(bb_ctx* ctx, const bb_tensor* tok_embd, const float* gain, float eps, const float* h,
+                          float* logits, int loc);
+
 /* ---- MoE layer (model.rs:473-555 decode, model.rs:286-371 batched) ----------------------- */
 /* Tensors as Model::moe_ffn resolves them (model.rs:474-478): router `ffn_gate_inp` F32
  * [hidden, E]; `exp_probs_b` f32[E] (host); stacked experts gate/up [hidden, ff, E] and

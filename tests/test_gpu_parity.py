@@ -107,6 +107,27 @@ def test_logits_head_shape(gpu_ctx, oracle):
     assert_bits(y, oracle.matvec(Q6_K, w, n_in, n_out, x), "logits head")
 
 
+@pytest.mark.parametrize("dtype,vocab,on_device", [(Q6_K, 32771, False), (Q6_K, 32771, True), (Q4_K, 5000, False)])
+def test_logits_from_hidden(gpu_ctx, oracle, dtype, vocab, on_device):
+    import torch
+    n_in = 2048
+    w = synth.quant_tensor(synth.rng(13, dtype, vocab), dtype, n_in, vocab)
+    h = synth.hidden_states(14, 1, hidden=n_in).reshape(-1) * 3.0
+    gain = synth.rng(15).uniform(0.5, 1.5, n_in).astype(np.float32)
+    t = Tensor(gpu_ctx, dtype, w, (n_in, vocab))
+    want = oracle.matvec(dtype, w, n_in, vocab, oracle.rmsnorm(h, gain, 1e-5))
+    if on_device:
+        hd, gd = torch.from_numpy(h).cuda(), torch.from_numpy(gain).cuda()
+        yd = torch.empty(vocab, dtype=torch.float32, device="cuda")
+        K.logits_from_hidden(gpu_ctx, t, gd, 1e-5, hd, yd)
+        gpu_ctx.synchronize()
+        y = yd.cpu().numpy()
+    else:
+        y = np.empty(vocab, np.float32)
+        K.logits_from_hidden(gpu_ctx, t, gain, 1e-5, h, y)
+    assert_bits(y, want, f"logits_from_hidden vocab={vocab}")
+
+
 @pytest.mark.parametrize("dtype", [Q4_K, Q6_K])
 def test_matmul_quantized_and_expert_slice(gpu_ctx, oracle, dtype):
     n_in, n_out, n_exp, nt = 512, 96, 3, 5
