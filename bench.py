@@ -50,7 +50,56 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--logits-head", action="store_true",
+                    help="time bb_logits_from_hidden (rmsnorm + Q6_K 2048 -> 128000 matvec) instead of a config")
     return ap.parse_args()
+
+
+def logits_head(args):
+    """One decode token's logits (model.rs:380-388) on the device: the token_embd matvec of
+    2048 -> 128000 Q6_K rows (215 MB) after the final rmsnorm. Prints one JSON line."""
+    import torch
+
+    from bebelm_amd import kernels as kops
+    from bebelm_amd import synth
+    from bebelm_amd.model import Context, Tensor
+
+    H, V = 2048, 128000
+    steps = args.steps if args.steps is not None else 200
+    warmup = args.warmup if args.warmup is not None else 20
+    ctx = Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    w = synth.quant_tensor(synth.rng(args.seed, synth.Q6_K, V), synth.Q6_K, H, V)
+    emb = Tensor(ctx, synth.Q6_K, w, (H, V))
+    h = torch.from_numpy(synth.hidden_states(args.seed, 1).reshape(-1)).cuda()
+    gain = torch.ones(H, dtype=torch.float32, device="cuda")
+    y = torch.empty(V, dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        kops.logits_from_hidden(ctx, emb, gain, 1e-5, h, y)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        kops.logits_from_hidden(ctx, emb, gain, 1e-5, h, y)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ctx.profile(True)
+    ctx.reset_stats()
+    for _ in range(steps):
+        kops.logits_from_hidden(ctx, emb, gain, 1e-5, h, y)
+    stats = ctx.kernel_stats()
+    ctx.profile(False)
+    kern_us = {n: v[0] * 1e3 / v[1] for n, v in stats.items()}
+    nbytes = synth.byte_size(synth.Q6_K, H * V) + q8_bytes(H) + V * 4
+    achieved = nbytes / (kern_us["rows_q8"] * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "logits head tok/s (rmsnorm + Q6_K token_embd matvec 2048 -> 128000)",
+        "value": 1e3 / ms, "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded Q6_K rows)", "config": {"workload": "logits_head_q6k_2048x128000"},
+        "kernel_us": kern_us,
+        "roofline": {"kernel": "rows_q8", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None, "algorithmic_bytes_per_launch": nbytes},
+    }), flush=True)
 
 
 def q8_bytes(n):
@@ -126,6 +175,9 @@ def main():
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
+    if args.logits_head:
+        logits_head(args)
+        return
     import torch
 
     from bebelm_amd import synth
