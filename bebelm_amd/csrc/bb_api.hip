@@ -792,6 +792,27 @@ int bb_logits_from_hidden(bb_ctx* c, const bb_tensor* tok_embd, const float* gai
     set_device(c);
     with_io(c, loc, {{h, H * 4, true, false}, {gain, H * 4, true, false}, {logits, V * 4, false, true}},
             [&](std::vector<void*>& d) {
+              const uint32_t dt = tok_embd->dtype;
+              if ((dt == BB_Q4_K || dt == BB_Q6_K) && H % 256 == 0 && H <= (size_t)bb::GU_H_MAX) {
+                // one launch for the rmsnorm and the Q8 of the normed row, then the rows
+                size_t row_bytes;
+                check_weight_range(tok_embd, dt, 0, H, V, row_bytes);
+                Carve cv{nullptr};
+                cv.take<int8_t>(H);
+                cv.take<float>(H / 256);
+                cv.take<int32_t>(H / 32);
+                Carve cv2{ensure_ws(c, cv.off)};
+                bb::Q8Bufs q{cv2.take<int8_t>(H), cv2.take<float>(H / 256), cv2.take<int32_t>(H / 32)};
+                launch(c, bb::K_RMSNORM, [&] {
+                  return bb::launch_rmsnorm_q8(c->stream, static_cast<const float*>(d[0]),
+                                               static_cast<const float*>(d[1]), eps, H, 1, nullptr, q);
+                });
+                launch(c, bb::K_ROWS_Q8, [&] {
+                  return bb::launch_rows_q8(c->stream, (int)dt, tok_embd->dev, row_bytes, (int)(H / 256), V, q, H, 1,
+                                            static_cast<float*>(d[2]), V, 1);
+                });
+                return;
+              }
               // normed lives past the Q8 records matmul_dev carves from the workspace's start
               Carve cv{nullptr};
               cv.take<int8_t>(H);

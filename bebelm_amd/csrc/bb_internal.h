@@ -184,6 +184,9 @@ hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a,
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
                           float* out);
+// The same, and the Q8 of each normed row into q (n <= GU_H_MAX, n % 256 == 0; out may be null).
+hipError_t launch_rmsnorm_q8(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
+                             float* out, Q8Bufs q);
 // h += (slots, wts, K) combine or ffn row; then normed = rmsnorm(h, gain) unless gain is null.
 hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
                                 const float* gain, float eps, size_t n, size_t n_vec, float* normed);

@@ -276,8 +276,10 @@ hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a,
 // rmsnorm.rs:10-21. The sum of the f32 squares is taken in f64 as a tree instead of the
 // reference's left-to-right f64 sum; after narrowing `mean` to f32 the two agree unless the
 // two f64 sums straddle an f32 rounding boundary. One block per vector.
+// With q.q set (rows of at most GU_H_MAX, n % 256 == 0) the normed row is also quantised to Q8
+// (k_quantize's arithmetic, one wave per 256-block, from a copy in LDS), and out may be null.
 __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, const float* __restrict__ gain,
-                                                 float eps, size_t n, float* __restrict__ out) {
+                                                 float eps, size_t n, float* __restrict__ out, Q8Bufs q) {
   const float* xv = x + (size_t)blockIdx.x * n;
   float* ov = out + (size_t)blockIdx.x * n;
   constexpr int NI = GU_H_MAX / 256;
@@ -315,7 +317,24 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
   }
   lds_barrier();
   const float scale = s_scale;
-  if (regs) {
+  if (q.q) {
+    __shared__ __align__(16) float s_norm[GU_H_MAX];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = threadIdx.x + 256 * it;
+      if (i >= n) break;
+      const float v = xr[it] * scale * gr[it];
+      s_norm[i] = v;
+      if (out) ov[i] = v;
+    }
+    lds_barrier();
+    const size_t nbk = n / QK, v = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    for (size_t b = threadIdx.x >> 6; b < nbk; b += 4) {
+      const float4 val = *reinterpret_cast<const float4*>(s_norm + b * QK + 4 * lane);
+      wave_quantize_block(val, q.q + v * n + b * QK, q.scales + v * nbk + b, q.sums + v * (n / 32) + b * 8);
+    }
+  } else if (regs) {
 #pragma unroll
     for (int it = 0; it < NI; ++it) {
       const size_t i = threadIdx.x + 256 * it;
@@ -422,7 +441,15 @@ hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, con
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
                           float* out) {
   if (n_vec == 0) return hipSuccess;
-  BB_LAUNCH(k_rmsnorm, dim3((unsigned)n_vec), dim3(256), 0, s, x, gain, eps, n, out);
+  BB_LAUNCH(k_rmsnorm, dim3((unsigned)n_vec), dim3(256), 0, s, x, gain, eps, n, out, Q8Bufs{});
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_q8(hipStream_t s, const float* x, const float* gain, float eps, size_t n, size_t n_vec,
+                             float* out, Q8Bufs q) {
+  if (n_vec == 0) return hipSuccess;
+  if (!q.q || n > (size_t)GU_H_MAX || n % QK != 0) return hipErrorInvalidValue;
+  BB_LAUNCH(k_rmsnorm, dim3((unsigned)n_vec), dim3(256), 0, s, x, gain, eps, n, out, q);
   return hipGetLastError();
 }
 
