@@ -548,11 +548,7 @@ template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
                               int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
   const int n_ent = T * K;
-  // (gate/up of mid-size batches: member tiles of 32, whose 16 KB less LDS per block buys a
-  // third block per CU; config 3's gate/up 92 -> 90 µs, its down 40 -> 42 µs, so down keeps 64)
-  const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8
-                 : KIND == GEMM_GATEUP && n_ent >= 16 * E && n_ent < 128 * E ? 2
-                                                                              : gemm_member_tiles(n_ent, E);
+  const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
   const int bn = 16 * mt;
   // enough member tiles: with tiles of 16, ceil(T/16) per expert (an expert has at most T
   // members); else every hit expert adds at most one partial tile
@@ -562,8 +558,6 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
     BB_LAUNCH((k_gemm<DT_Q6_K, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4)
     BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
-  else if (mt == 2)
-    BB_LAUNCH((k_gemm<DT, KIND, 2>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else
     BB_LAUNCH((k_gemm<DT, KIND, 1>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   return hipGetLastError();
