@@ -95,6 +95,7 @@ struct bb_ctx {
   double kernel_ms[bb::K_COUNT] = {};
   int64_t launches[bb::K_COUNT] = {};
   size_t batched_min_entries = 64;  // T*k from which MoE calls take the grouped-GEMM path
+  int n_cu = 256;                   // compute units of the device
 };
 
 struct bb_tensor {
@@ -307,9 +308,11 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
   if (batched) {
     // model.rs:286-371: route all tokens, group entries by expert, grouped GEMMs, combine
     launch(c, bb::K_ROUTE_LARGE, [&] {
-      // tokens per routing block: the router is read once per block, but there must be
-      // enough blocks to fill the GPU
-      const int tpb = (int)std::max<size_t>(1, std::min<size_t>(16, T / 256));
+      // tokens per routing block: each block reads the whole router once and then takes its
+      // tokens one after the other (~1 µs each), so about one block per CU: ceil(T / CUs),
+      // at most 16 (config 3 on 256 CUs: 2 tokens per block)
+      const size_t n_cu = (size_t)c->n_cu;
+      const int tpb = (int)std::max<size_t>(1, std::min<size_t>(16, (T + n_cu - 1) / n_cu));
       return bb::launch_route(c->stream, m->router_cm, m->bias_dev, x, (int)T, m->H, m->E, m->K, tpb, w.xq, w.rb);
     });
     // small batches: the GEMMs group the entries themselves; the dispatch kernel then only
@@ -527,6 +530,9 @@ int bb_ctx_create(int device, bb_ctx** out) {
       set_device(c);
       check_hip(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking), "hipStreamCreate");
       c->stream = c->own;
+      int n_cu = 0;
+      check_hip(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
+      c->n_cu = n_cu > 0 ? n_cu : 256;
       check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
     } catch (...) {
       if (c->own) (void)hipStreamDestroy(c->own);
@@ -967,10 +973,14 @@ int bb_stack_create(bb_ctx* c, const bb_layer_desc* layers, size_t n_layers, flo
     for (size_t i = 0; i < n_layers; ++i) {
       need((layers[i].moe != nullptr) != (layers[i].dense != nullptr), BB_ERR_ARG, "exactly one of moe/dense per layer");
       need(layers[i].ffn_norm != nullptr, BB_ERR_ARG, "ffn_norm is null");
+      need(layers[i].moe ? layers[i].moe->ctx == c : layers[i].dense->ctx == c, BB_ERR_ARG,
+           "a layer belongs to another context");
       const int h = layers[i].moe ? layers[i].moe->H : layers[i].dense->H;
       need(H < 0 || h == H, BB_ERR_SHAPE, "layers disagree on hidden size");
       H = h;
     }
+    // the layer-boundary kernels hold a row of h per block in LDS
+    need(H <= bb::GU_H_MAX, BB_ERR_RANGE, "the layer stack supports hidden sizes up to 2048");
     set_device(c);
     auto* s = new bb_stack();
     s->ctx = c;

@@ -149,16 +149,20 @@ class MoeLayer:
         self.down = Tensor(ctx, w.down_dtype, w.down_exps, (F, H, E))
         bias = np.ascontiguousarray(w.exp_probs_b, np.float32)
         h = ctypes.c_void_p()
-        check(lib().bb_moe_create(ctx.handle, self.router.handle, bias.ctypes.data, self.gate.handle, self.up.handle,
-                                  self.down.handle, self.n_used, ctypes.byref(h)))
+        try:
+            check(lib().bb_moe_create(ctx.handle, self.router.handle, bias.ctypes.data, self.gate.handle,
+                                      self.up.handle, self.down.handle, self.n_used, ctypes.byref(h)))
+        finally:
+            # the layer keeps its own regrouped copies: the uploads are freed at once, so each
+            # layer occupies its packed bytes in HBM only
+            for t in (self.router, self.gate, self.up, self.down):
+                t.close()
         self.handle = h
 
     def close(self):
         if self.handle:
             check(lib().bb_moe_destroy(self.handle))
             self.handle = None
-        for t in (self.router, self.gate, self.up, self.down):
-            t.close()
 
     def forward(self, x, t, out, trace=None):
         """x, out: token-major [t, hidden]; numpy (host) or torch CUDA (device, async)."""

@@ -17,7 +17,10 @@ The output is one JSON line with `value` in tok/s. It also carries:
                 (config 4) per launch divided by its mean launch time, measured with HIP events
                 on the stream the kernels run on, against MI355X's 8 TB/s or int8 MFMA peak
   cpu_baseline  the reference path (its C++ restatement, OpenMP over output rows as the
-                reference's rayon does) timed on this host on a bounded sample
+                reference's rayon does) timed on this host: the median of 20 timed repetitions
+                on all cores, the same on one core, and the CPU model
+  prefill       (default run only) config 4 measured in the same process the same way: tok/s,
+                ms per step, the grouped GEMMs' µs and their int8 / bf16 MFMA fractions
 """
 import argparse
 import json
@@ -50,6 +53,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill object of the default run")
+    ap.add_argument("--cpu-reps", type=int, default=20, help="timed repetitions of the CPU baseline")
     ap.add_argument("--logits-head", action="store_true",
                     help="time bb_logits_from_hidden (rmsnorm + Q6_K 2048 -> 128000 matvec) instead of a config")
     return ap.parse_args()
@@ -149,7 +154,10 @@ def layer_work(w, counts, T, batched, prerouted=False):
     }
 
 
-def cpu_baseline(run_one, T, seconds, what):
+def cpu_baseline(run_one, T, seconds, what, reps=20, one_core=True):
+    """The reference path's C++ restatement on this host's cores: `reps` timed repetitions of
+    about seconds / reps each (whole calls, at least one), tok/s as their median; then the same
+    on one core. run_one(i) runs call i (callers rotate weight sets by i)."""
     from oracle import bbo
 
     try:
@@ -157,66 +165,75 @@ def cpu_baseline(run_one, T, seconds, what):
     except AttributeError:
         cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+
+    def median_rate(threads, budget):
+        bbo.set_threads(threads)
+        run_one(0)  # warm-up: pages in weights, starts the thread pool
+        rates, calls = [], 1
+        per_rep = budget / reps
+        for _ in range(reps):
+            n = 0
+            t0 = time.perf_counter()
+            while True:
+                run_one(calls)
+                calls += 1
+                n += 1
+                el = time.perf_counter() - t0
+                if el >= per_rep:
+                    break
+            rates.append(n * T / el)
+        return float(np.median(rates)), calls - 1
+
+    value, n_all = median_rate(cores, seconds)
+    out = {"value": value, "unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": bbo.cpu_model(),
+           "oracle_build": os.path.basename(bbo.lib_path())}
+    each = "one call each" if seconds / reps < 0.01 else f"about {seconds / reps:.2f} s each"
+    sample = (f"median of {reps} repetitions ({n_all} calls, {each}) of the C++ "
+              f"restatement of {what}, OpenMP over output rows")
+    if one_core and cores > 1:
+        v1, n1 = median_rate(1, seconds)
+        out["value_1core"] = v1
+        sample += f"; 1 core: {n1} calls in {reps} repetitions"
     bbo.set_threads(cores)
-    calls = 0
-    t0 = time.perf_counter()
-    while True:
-        run_one(calls)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or calls >= 1_000_000:
-            break
-    return {"value": calls * T / el, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{calls} calls of the C++ restatement of {what} in {el:.1f} s, OpenMP over output rows"}
+    out["sample"] = sample
+    return out
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
-        sys.exit(2)
-    if args.logits_head:
-        logits_head(args)
-        return
+def run_config(args, ctx, config, steps, warmup, with_cpu):
+    """Times `steps` steps of one configuration (after `warmup`), then the same steps again with
+    per-kernel HIP events; returns the bench fields of that configuration."""
     import torch
 
     from bebelm_amd import synth
-    from bebelm_amd.model import Context, DenseLayer, FfnStack, MoeLayer, RouteTrace
+    from bebelm_amd.model import DenseLayer, FfnStack, MoeLayer, RouteTrace
 
-    cfg = synth.CONFIGS[args.config]
+    cfg = synth.CONFIGS[config]
     T = cfg.tokens
-    prefill = args.config in (3, 4)
-    steps = args.steps if args.steps is not None else (20 if args.config == 4 else 200)
-    warmup = args.warmup if args.warmup is not None else (3 if args.config == 4 else 20)
+    prefill = config in (3, 4)
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    ctx = Context(0)
-    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
     batched = T * 4 >= BATCHED_MIN_ENTRIES
 
     t_gen = time.perf_counter()
     x_host = synth.hidden_states(args.seed, T)
     x = torch.from_numpy(x_host).to(dev)
     out = torch.empty_like(x)
-    if args.config == 5:
+    if config == 5:
         spec = synth.stack_layers(seed=args.seed)
         built = [(g, MoeLayer(ctx, w) if isinstance(w, synth.MoeWeights) else DenseLayer(ctx, w)) for g, w in spec]
         stack = FfnStack(ctx, built)
-        moe_w = [w for _, w in spec if isinstance(w, synth.MoeWeights)]
         dense_w = [w for _, w in spec if not isinstance(w, synth.MoeWeights)]
         units = [stack]
         weight_bytes = int(sum(w.nbytes for _, w in spec))
         L = 1
     else:
         L = max(1, args.layers)
-        weights = [synth.config_layer(args.config, seed=args.seed, layer=l) for l in range(L)]
+        weights = [synth.config_layer(config, seed=args.seed, layer=l) for l in range(L)]
         units = [MoeLayer(ctx, w) for w in weights]
         weight_bytes = int(sum(w.nbytes for w in weights))
     t_gen = time.perf_counter() - t_gen
 
     # data-dependent hit counts (for the algorithmic byte counts)
-    if args.config == 5:
-        per_layer = [None]
+    if config == 5:
         from bebelm_amd import kernels as kops
         # routing of every MoE layer of the stack for this token, from the library's own route
         # trace, layer by layer on the host-side residual stream (run_layers, model.rs:105-130)
@@ -265,7 +282,7 @@ def main():
     ctx.profile(False)
     kern_us = {n: v[0] * 1e3 / v[1] for n, v in stats.items()}
 
-    if args.config == 5:
+    if config == 5:
         names = DECODE_KERNELS
         avg = {n: float(np.mean([lw[n][0] for lw in layers_work])) for n in names}
         avg_ops = {n: float(np.mean([lw[n][1] for lw in layers_work])) for n in names}
@@ -283,7 +300,7 @@ def main():
     tfile = os.path.join(ROOT, "profiles", f"traffic_{dominant}_{cfg.name}.json")
     if os.path.exists(tfile):
         traffic = json.load(open(tfile)).get("hbm_bytes_per_launch")
-    if args.config == 4:
+    if config == 4:
         achieved = avg_ops[dominant] / (dom_us * 1e-6) / 1e12
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS,
                     "unit": "TFLOP/s", "frac": achieved / INT8_PEAK_TOPS, "traffic": traffic,
@@ -295,24 +312,16 @@ def main():
                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                     "algorithmic_bytes_per_launch": avg[dominant]}
 
-    kind = "prefill" if prefill else ("FFN-stack decode" if args.config == 5 else "decode")
+    kind = "prefill" if prefill else ("FFN-stack decode" if config == 5 else "decode")
     result = {
-        "metric": f"MoE-block {kind} tok/s (config {args.config}: {T} token{'s' if T > 1 else ''}"
-                  f"{', 24-layer FFN stack' if args.config == 5 else ', one MoE FFN block'})",
+        "metric": f"MoE-block {kind} tok/s (config {config}: {T} token{'s' if T > 1 else ''}"
+                  f"{', 24-layer FFN stack' if config == 5 else ', one MoE FFN block'})",
         "value": T / (ms * 1e-3),
         "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
         "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic (seeded Q4_K/Q6_K experts, N(0,1) hidden states; no GGUF offline)",
-        "config": {"workload": f"config {args.config}: {cfg.description}", "tokens": T, "hidden": 2048,
+        "config": {"workload": f"config {config}: {cfg.description}", "tokens": T, "hidden": 2048,
                    "moe_ff": 1792, "experts": 32, "top_k": 4,
-                   "down": "Q4_K/Q6_K alternating" if args.config == 5 else
+                   "down": "Q4_K/Q6_K alternating" if config == 5 else
                            ("Q6_K" if cfg.down_dtype == 14 else "Q4_K"),
                    "path": "grouped int8-MFMA GEMMs" if batched else "per-expert GEMV",
                    "weight_sets_rotated": L, "weight_bytes_resident": weight_bytes},
@@ -326,30 +335,102 @@ def main():
     }
     if prefill:
         ops = float(np.mean([per_layer[i % L]["ops"] for i in range(steps)]))
+        gemm_us = sum(kern_us.get(n, 0.0) for n in GEMM_KERNELS)
+        gemm_tops = ops / (gemm_us * 1e-6) / 1e12
         result["block_tflops"] = ops / (ms * 1e-3) / 1e12
         result["block_frac_of_bf16_peak"] = result["block_tflops"] / BF16_PEAK_TFLOPS
-    if not args.no_cpu:
+        result["gemms"] = {"gateup_us": kern_us.get("gemm_gateup"), "down_us": kern_us.get("gemm_down"),
+                           "us": gemm_us, "ops": ops, "tops": gemm_tops,
+                           "frac_of_int8_peak": gemm_tops / INT8_PEAK_TOPS,
+                           "frac_of_bf16_peak": gemm_tops / BF16_PEAK_TFLOPS}
+    if with_cpu:
         from oracle import bbo
 
-        if args.config == 5:
-            from oracle import bbo as _b
+        if config == 5:
             layers_o = [(g, w) for g, w in spec]
-            result["cpu_baseline"] = cpu_baseline(lambda i: _b.ffn_stack(layers_o, x_host.reshape(-1), 1, 1e-5), T,
-                                                  args.cpu_seconds, "the 24-layer FFN stack (T=1)")
+            result["cpu_baseline"] = cpu_baseline(lambda i: bbo.ffn_stack(layers_o, x_host.reshape(-1), 1, 1e-5), T,
+                                                  args.cpu_seconds, "the 24-layer FFN stack (T=1)", args.cpu_reps)
+        elif prefill:
+            # one call takes seconds: a few repetitions of one call each, all cores only
+            sample = weights[: min(L, 4)]
+            xs = x_host.reshape(-1)
+            reps = 3
+            result["cpu_baseline"] = cpu_baseline(lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T), T,
+                                                  1e-3 * reps, f"moe_ffn_batch (T={T}, {len(sample)} rotated layers)",
+                                                  reps, one_core=False)
         else:
             sample = weights[: min(L, 4)]
             xs = x_host.reshape(-1)
             fn = (lambda i: bbo.moe_ffn(sample[i % len(sample)], xs)) if T == 1 else \
                 (lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T))
             result["cpu_baseline"] = cpu_baseline(fn, T, args.cpu_seconds,
-                                                  f"moe_ffn{'_batch' if T > 1 else ''} (T={T}, {len(sample)} rotated layers)")
-    if args.config == 5:
+                                                  f"moe_ffn{'_batch' if T > 1 else ''} (T={T}, {len(sample)} rotated layers)",
+                                                  args.cpu_reps)
+    if config == 5:
         stack.close()
         for _, l in built:
             l.close()
     else:
         for l in units:
             l.close()
+    return result, steps, warmup
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        sys.exit(2)
+    if args.logits_head:
+        logits_head(args)
+        return
+    import torch
+
+    from bebelm_amd.model import Context
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    def defaults(config):
+        steps = args.steps if args.steps is not None else (20 if config == 4 else 200)
+        warmup = args.warmup if args.warmup is not None else (3 if config == 4 else 20)
+        return steps, warmup
+
+    steps, warmup = defaults(args.config)
+    res, steps, warmup = run_config(args, ctx, args.config, steps, warmup, not args.no_cpu)
+    result = {
+        "metric": res.pop("metric"),
+        "value": res.pop("value"),
+        "unit": res.pop("unit"),
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": res.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Q4_K/Q6_K experts, N(0,1) hidden states; no GGUF offline)",
+        "config": res.pop("config"),
+        **res,
+    }
+    if args.config == 2 and not args.no_prefill:
+        # the metric's prefill half: config 4 in the same process, measured the same way
+        ps, pw = defaults(4)
+        if args.steps is not None:
+            ps = min(ps, args.steps)
+        if args.warmup is not None:
+            pw = min(pw, args.warmup)
+        p, ps, pw = run_config(args, ctx, 4, ps, pw, not args.no_cpu)
+        result["prefill"] = {
+            "metric": p["metric"], "value": p["value"], "unit": "tok/s", "steps": ps, "warmup": pw,
+            "ms_per_step": p["ms_per_step"], "config": p["config"], "gemms": p["gemms"],
+            "block_tflops": p["block_tflops"], "block_frac_of_bf16_peak": p["block_frac_of_bf16_peak"],
+            "kernel_us": p["kernel_us"], "roofline": p["roofline"], "cpu_baseline": p["cpu_baseline"],
+            "mean_hit_experts": p["mean_hit_experts"],
+        }
     ctx.close()
     print(json.dumps(result), flush=True)
 

@@ -161,13 +161,16 @@ int bb_moe_forward(bb_ctx* ctx, bb_moe* moe, const float* x, size_t T, float* ou
                    bb_route_trace* trace);
 
 /* ---- dense FFN and the FFN-path layer stack ---------------------------------------------- */
-/* dense_ffn (model.rs:459-469) / dense_ffn_batch (:262-278): gate/up [hidden, ff], down [ff, hidden]. */
+/* dense_ffn (model.rs:459-469) / dense_ffn_batch (:262-278): gate/up [hidden, ff], down [ff, hidden].
+ * Unlike bb_moe_create, the layer reads the three tensors in place: they must outlive it. */
 int bb_dense_create(bb_ctx* ctx, const bb_tensor* gate, const bb_tensor* up, const bb_tensor* down, bb_dense** out);
 int bb_dense_destroy(bb_dense* d);
 int bb_dense_forward(bb_ctx* ctx, bb_dense* d, const float* x, size_t T, float* out, int loc);
 
 /* run_layers (model.rs:105-130) with the operator sub-layer contributing nothing:
- * per layer h += FFN(rmsnorm(h, ffn_norm)). Exactly one of moe / dense is set per layer. */
+ * per layer h += FFN(rmsnorm(h, ffn_norm)). Exactly one of moe / dense is set per layer, created
+ * on the same context; the stack keeps copies of the gains but uses the layers in place, so
+ * they must outlive it. Hidden sizes up to 2048. */
 typedef struct {
   const float* ffn_norm; /* host f32[hidden] */
   bb_moe* moe;

@@ -199,6 +199,60 @@ float dot_f32(const float* a, const float* b, size_t n) {
   return sum;
 }
 
+// Other plausible evaluation orders of the same dot (matmul.rs:36-66), for the routing
+// robustness check (tests/test_router_orders.py): the `wide` crate's lane reduce and its
+// mul_add fallback differ by target, and the reference's CI also builds x86-64-v2 (no FMA,
+// .github/workflows/ci.yml:28-35), where mul_add is a rounded multiply, then an add.
+//   0  dot_f32: FMA chains, AVX reduce tree (the order the restatement assumes)
+//   1  multiply-then-add chains, AVX reduce tree
+//   2  FMA chains; lanes folded v_i + v_{i+4}, then (s0+s1)+(s2+s3) (a pairwise horizontal add)
+//   3  multiply-then-add chains; the 8 lanes summed left to right
+//   4  left-to-right f32 sum of rounded products (scalar loop)
+//   5  f64 sum of the exact products, rounded once to f32
+float dot_variant(const float* a, const float* b, size_t n, int variant) {
+  if (variant == 0) return dot_f32(a, b, n);
+  if (variant == 4) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += a[i] * b[i];
+    return s;
+  }
+  if (variant == 5) {
+    double s = 0.0;
+    for (size_t i = 0; i < n; ++i) s += double(a[i]) * double(b[i]);
+    return float(s);
+  }
+  const bool fma = variant == 2;
+  float acc[4][8] = {};
+  size_t i = 0;
+  while (i + 32 <= n) {
+    for (int k = 0; k < 4; ++k)
+      for (int l = 0; l < 8; ++l) {
+        const float p = a[i + 8 * k + l], q = b[i + 8 * k + l];
+        acc[k][l] = fma ? std::fmaf(p, q, acc[k][l]) : acc[k][l] + p * q;
+      }
+    i += 32;
+  }
+  while (i + 8 <= n) {
+    for (int l = 0; l < 8; ++l) acc[0][l] = fma ? std::fmaf(a[i + l], b[i + l], acc[0][l]) : acc[0][l] + a[i + l] * b[i + l];
+    i += 8;
+  }
+  float v[8];
+  for (int l = 0; l < 8; ++l) v[l] = (acc[0][l] + acc[1][l]) + (acc[2][l] + acc[3][l]);
+  float sum;
+  if (variant == 1) {
+    sum = reduce_add8(v);
+  } else if (variant == 2) {
+    float f[4];
+    for (int l = 0; l < 4; ++l) f[l] = v[l] + v[l + 4];
+    sum = (f[0] + f[1]) + (f[2] + f[3]);
+  } else {
+    sum = v[0];
+    for (int l = 1; l < 8; ++l) sum += v[l];
+  }
+  while (i < n) { sum += a[i] * b[i]; ++i; }
+  return sum;
+}
+
 // --- Q4_K x Q8 (matmul.rs:210-298) ---
 // Σ_j sc_j·<nib_j, qx_j>, exact i32 (q4k_block_sd_portable, :251-260; equal to the VNNI
 // and sdot variants by the reference's own tests :1456-1485).
@@ -766,6 +820,20 @@ void bbo_swiglu(const float* g, const float* u, float* o, size_t n) { swiglu(g, 
 void bbo_add_scaled(float* o, const float* b, float s, size_t n) { add_scaled(o, b, s, n); }
 void bbo_add_assign(float* a, const float* b, size_t n) { for (size_t i = 0; i < n; ++i) a[i] += b[i]; }
 void bbo_rmsnorm(const float* x, const float* g, float eps, size_t n, float* out) { rmsnorm(x, g, eps, n, out); }
+float bbo_dot_variant(const float* a, const float* b, size_t n, int variant) { return dot_variant(a, b, n, variant); }
+// logits[t][e] = dot_variant(W row e, x row t) for T tokens (W: E rows of H f32, as the router).
+void bbo_router_logits_variant(const float* W, const float* x, size_t T, int H, int E, int variant, float* logits) {
+  for_rows(T * size_t(E), true, [&](size_t i) {
+    const size_t t = i / E, e = i % E;
+    logits[i] = dot_variant(W + e * size_t(H), x + t * size_t(H), size_t(H), variant);
+  });
+}
+// model.rs:485-495 for T tokens from given logits: sel/w [T*k], ties [1] (accumulated), margin [T].
+void bbo_gate(const float* logits, const float* bias, size_t T, int E, int k, int32_t* sel, float* w, int32_t* ties,
+              float* margin) {
+  for (size_t t = 0; t < T; ++t)
+    gate_one(logits + t * E, bias, E, k, sel + t * k, w + t * k, ties, margin ? margin + t : nullptr);
+}
 int bbo_moe_ffn(const bbo_moe* m, const float* x, float* out, bbo_trace* tr) { return moe_ffn(m, x, out, tr); }
 int bbo_moe_ffn_batch(const bbo_moe* m, const float* x, size_t t, float* out, bbo_trace* tr) { return moe_ffn_batch(m, x, t, out, tr); }
 int bbo_dense_ffn(const bbo_dense* d, const float* x, size_t t, float* out) { return dense_ffn(d, x, t, out); }

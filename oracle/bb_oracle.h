@@ -119,6 +119,13 @@ void bbo_add_scaled(float* out, const float* b, float s, size_t n);
 void bbo_add_assign(float* a, const float* b, size_t n);
 void bbo_rmsnorm(const float* x, const float* gain, float eps, size_t n, float* out);
 
+/* Routing robustness (test infrastructure): the router dot under other plausible evaluation
+ * orders of matmul.rs:36-66 (variant 0 = bbo_dot; see dot_variant), and model.rs:485-495's
+ * gating of T tokens from given logits. */
+float bbo_dot_variant(const float* a, const float* b, size_t n, int variant);
+void bbo_router_logits_variant(const float* W, const float* x, size_t T, int H, int E, int variant, float* logits);
+void bbo_gate(const float* logits, const float* bias, size_t T, int E, int k, int32_t* sel, float* w, int32_t* ties,
+              float* margin);
 int bbo_moe_ffn(const bbo_moe* m, const float* x, float* out, bbo_trace* trace);
 int bbo_moe_ffn_batch(const bbo_moe* m, const float* x, size_t t, float* out, bbo_trace* trace);
 int bbo_dense_ffn(const bbo_dense* d, const float* x, size_t t, float* out);

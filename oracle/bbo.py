@@ -10,7 +10,12 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+LIB_PATH = os.path.join(HERE, "liboracle.so")  # x86-64-v3 (AVX2 + FMA): runs on any host here
+# The same source built for AVX-512 with VNNI (the reference's x86 build is target-cpu=native,
+# .cargo/config.toml, whose int8 dots take VNNI where the CPU has it). Loaded when the host has
+# those features; both give the same bits (no FP contraction or reassociation in either).
+LIB_AVX512_PATH = os.path.join(HERE, "liboracle_avx512.so")
+AVX512_FLAGS = ("avx512f", "avx512bw", "avx512vl", "avx512dq", "avx512cd", "avx512_vnni")
 
 F32, F16, Q4_K, Q6_K = 0, 1, 12, 14
 c_void_p, c_size_t, c_int, c_float = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
@@ -53,12 +58,45 @@ def build():
     return LIB_PATH
 
 
+def host_has_avx512_vnni():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return all(x in flags for x in AVX512_FLAGS)
+    except OSError:
+        pass
+    return False
+
+
+def lib_path():
+    """The build this host runs: BBO_ISA=v3 or avx512 forces one, else the widest it supports."""
+    isa = os.environ.get("BBO_ISA", "")
+    if isa == "v3":
+        return LIB_PATH
+    if isa == "avx512" or (isa == "" and host_has_avx512_vnni() and os.path.exists(LIB_AVX512_PATH)):
+        return LIB_AVX512_PATH
+    return LIB_PATH
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
+        L = ctypes.CDLL(lib_path())
         L.bbo_f16_to_f32.restype = c_float
         L.bbo_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.bbo_dot.restype = c_float
@@ -90,6 +128,10 @@ def lib():
         L.bbo_moe_ffn_batch.argtypes = [ctypes.POINTER(Moe), c_void_p, c_size_t, c_void_p, ctypes.POINTER(Trace)]
         L.bbo_dense_ffn.argtypes = [ctypes.POINTER(Dense), c_void_p, c_size_t, c_void_p]
         L.bbo_ffn_stack.argtypes = [ctypes.POINTER(Layer), c_size_t, c_void_p, c_size_t, c_float, c_void_p]
+        L.bbo_dot_variant.restype = c_float
+        L.bbo_dot_variant.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        L.bbo_router_logits_variant.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_int, c_int, c_void_p]
+        L.bbo_gate.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
         L.bbo_set_threads.argtypes = [c_int]
         L.bbo_get_threads.restype = c_int
         _lib = L
@@ -152,6 +194,41 @@ def dot(a, b):
     a = np.ascontiguousarray(a, np.float32)
     b = np.ascontiguousarray(b, np.float32)
     return lib().bbo_dot(_p(a), _p(b), a.size)
+
+
+# Router dot evaluation orders (bb_oracle.cpp dot_variant): 0 is the order the restatement
+# assumes for the reference; 1-5 are the other plausible ones.
+DOT_VARIANTS = {0: "FMA chains, AVX reduce tree", 1: "mul+add chains, AVX reduce tree",
+                2: "FMA chains, pairwise lane fold", 3: "mul+add chains, lanes left to right",
+                4: "scalar left-to-right f32", 5: "f64 exact products, one rounding"}
+
+
+def dot_variant(a, b, variant):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return lib().bbo_dot_variant(_p(a), _p(b), a.size, int(variant))
+
+
+def router_logits_variant(w, x, t, variant):
+    """[t, E] router logits of token-major x under dot variant `variant`."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    router = np.ascontiguousarray(w.router, np.float32)
+    out = np.zeros(t * w.n_experts, np.float32)
+    lib().bbo_router_logits_variant(_p(router), _p(x), t, w.hidden, w.n_experts, int(variant), _p(out))
+    return out.reshape(t, w.n_experts)
+
+
+def gate(logits, bias, k):
+    """model.rs:485-495 for each row of logits [t, E]: (sel [t,k], w [t,k], ties, margin [t])."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    t, E = logits.shape
+    bias = np.ascontiguousarray(bias, np.float32)
+    sel = np.zeros((t, k), np.int32)
+    w = np.zeros((t, k), np.float32)
+    ties = np.zeros(1, np.int32)
+    margin = np.zeros(t, np.float32)
+    lib().bbo_gate(_p(logits), _p(bias), t, E, k, _p(sel), _p(w), _p(ties), _p(margin))
+    return sel, w, int(ties[0]), margin
 
 
 def dot_q4k_block_q8(block, qx, sx, sums):
