@@ -72,6 +72,7 @@ _SIGS = {
     "bb_moe_create": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, P(c_void_p)]),
     "bb_moe_destroy": (c_int, [c_void_p]),
     "bb_moe_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int, P(RouteTrace)]),
+    "bb_moe_forward_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "bb_dense_create": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)]),
     "bb_dense_destroy": (c_int, [c_void_p]),
     "bb_dense_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int]),

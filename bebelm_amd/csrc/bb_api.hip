@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -75,6 +76,24 @@ void* dev_alloc(size_t bytes) {
 }
 
 
+}  // namespace
+
+// Workspace of bb_moe_forward_noalloc: a fixed area in the code object's static device memory,
+// one copy per GPU, held until the process ends. Host code never uses the name `scratch` as an
+// address (on the host it only names the symbol): each device's address comes from
+// hipGetSymbolAddress at context creation and is kept in g_scratch.
+static __device__ __align__(256) uint8_t scratch[BB_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[SCRATCH_MAX_DEVICES] = {};  // per device, set once under g_scratch_mu
+
+uint8_t* scratch_of(int device) {
+  if (device < 0 || device >= SCRATCH_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  return g_scratch[device];
+}
 }  // namespace
 
 struct bb_ctx {
@@ -230,14 +249,18 @@ struct Carve {
 void need(bool ok, int code, const std::string& msg) {
   if (!ok) fail(code, msg);
 }
+// string-literal form: builds no std::string unless the check fails
+void need(bool ok, int code, const char* msg) {
+  if (!ok) fail(code, msg);
+}
 
 void need_ctx(bb_ctx* c) { need(c != nullptr, BB_ERR_ARG, "null context"); }
 
 void need_loc(int loc) { need(loc == BB_LOC_HOST || loc == BB_LOC_DEVICE, BB_ERR_ARG, "loc must be BB_LOC_HOST or BB_LOC_DEVICE"); }
 
 void need_aligned(const void* p, const char* what) {
-  need(p != nullptr, BB_ERR_ARG, std::string(what) + " is null");
-  need((reinterpret_cast<uintptr_t>(p) & 15) == 0, BB_ERR_ARG, std::string(what) + " must be 16-byte aligned");
+  if (p == nullptr) fail(BB_ERR_ARG, std::string(what) + " is null");
+  if ((reinterpret_cast<uintptr_t>(p) & 15) != 0) fail(BB_ERR_ARG, std::string(what) + " must be 16-byte aligned");
 }
 
 size_t tensor_elems(const bb_tensor* t) {
@@ -257,10 +280,17 @@ struct MoeWs {
   float* aq_sx;
 };
 
-MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched) {
+// Workspace of one call: the context's (grown on demand) or a fixed region given by the caller
+// (base, cap), which is never grown: a call that needs more fails with BB_ERR_RANGE.
+struct WsRegion {
+  uint8_t* base = nullptr;
+  size_t cap = 0;
+};
+
+MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegion* fixed = nullptr) {
   const size_t H = m->H, F = m->F, E = m->E, K = m->K;
   for (int pass = 0; pass < 2; ++pass) {
-    Carve cv{pass ? c->ws : nullptr};
+    Carve cv{pass ? (fixed ? fixed->base : c->ws) : nullptr};
     MoeWs w{};
     w.xq.q = cv.take<int8_t>(T * H);
     w.xq.sx = cv.take<float>(T * H / 256);
@@ -280,8 +310,15 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched) {
       w.aq = cv.take<int8_t>(T * K * F);
       w.aq_sx = cv.take<float>(T * K * F / 256);
     }
-    if (pass == 0) ensure_ws(c, cv.off);
-    else return w;
+    if (pass == 0) {
+      if (fixed)
+        need(cv.off <= fixed->cap, BB_ERR_RANGE,
+             "the call's workspace exceeds the allocation-free scratch area (BB_NOALLOC_SCRATCH_BYTES)");
+      else
+        ensure_ws(c, cv.off);
+    } else {
+      return w;
+    }
   }
   return {};
 }
@@ -294,8 +331,9 @@ struct PreRoute {
 
 // With combine false the caller combines: the slots and weights stay in the returned workspace.
 // With pre set (a few tokens on the GEMV path only) the route's dots are already done.
+// With fixed set the workspace is that region (nothing is allocated).
 MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, bb_route_trace* tr,
-                      bool combine = true, const PreRoute* pre = nullptr) {
+                      bool combine = true, const PreRoute* pre = nullptr, const WsRegion* fixed = nullptr) {
   need(T >= 1, BB_ERR_ARG, "T must be >= 1");
   const size_t n_ent = T * (size_t)m->K;
   const bool batched = n_ent >= c->batched_min_entries;
@@ -303,7 +341,7 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
     need(n_ent <= (size_t)bb::PF_MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 32768 (token, slot) entries per call");
   else
     need(n_ent <= (size_t)bb::MAX_ENTRIES, BB_ERR_RANGE, "this path routes at most 1024 (token, slot) entries per call");
-  MoeWs w = carve_moe(c, m, T, batched);
+  MoeWs w = carve_moe(c, m, T, batched, fixed);
   const bool combine_in_down = !batched && combine && T == 1 && m->K <= 4 && m->H % 16 == 0 && m->F / 256 <= 8;
   if (batched) {
     // model.rs:286-371: route all tokens, group entries by expert, grouped GEMMs, combine
@@ -533,6 +571,17 @@ int bb_ctx_create(int device, bb_ctx** out) {
       int n_cu = 0;
       check_hip(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
       c->n_cu = n_cu > 0 ? n_cu : 256;
+      if (device < SCRATCH_MAX_DEVICES) {
+        // the device's copy of the allocation-free scratch area: its address, and cleared once
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch[device]) {
+          void* p = nullptr;
+          check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+          check_hip(hipMemsetAsync(p, 0, BB_NOALLOC_SCRATCH_BYTES, c->own), "scratch clear");
+          check_hip(hipStreamSynchronize(c->own), "hipStreamSynchronize");
+          g_scratch[device] = static_cast<uint8_t*>(p);
+        }
+      }
       check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize");
     } catch (...) {
       if (c->own) (void)hipStreamDestroy(c->own);
@@ -923,6 +972,31 @@ int bb_moe_forward(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out, i
     with_io(c, loc, {{x, T * m->H * 4, true, false}, {out, T * m->H * 4, false, true}}, [&](std::vector<void*>& d) {
       moe_forward_dev(c, m, static_cast<const float*>(d[0]), T, static_cast<float*>(d[1]), tr);
     });
+  });
+}
+
+int bb_moe_forward_noalloc(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr, BB_ERR_ARG, "null layer");
+    need(m->ctx == c, BB_ERR_ARG, "layer belongs to another context");
+    need(T >= 1, BB_ERR_ARG, "T must be >= 1");
+    need_aligned(x, "x");
+    need_aligned(out, "out");
+    uint8_t* base = scratch_of(c->device);
+    need(base != nullptr, BB_ERR_ARG, "no allocation-free scratch area on this device");
+    set_device(c);
+    // no events: profiling would take them from the context's pool, which may grow
+    const bool prof = c->profile;
+    c->profile = false;
+    const WsRegion fixed{base, BB_NOALLOC_SCRATCH_BYTES};
+    try {
+      moe_forward_dev(c, m, x, T, out, nullptr, true, nullptr, &fixed);
+    } catch (...) {
+      c->profile = prof;
+      throw;
+    }
+    c->profile = prof;
   });
 }
 

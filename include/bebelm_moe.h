@@ -160,6 +160,20 @@ typedef struct {
 int bb_moe_forward(bb_ctx* ctx, bb_moe* moe, const float* x, size_t T, float* out, int loc,
                    bb_route_trace* trace);
 
+/* No counterpart in the reference (its CPU path allocates per call). For callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc. bb_moe_forward on device pointers (x, out: f32[T*hidden], 16-byte aligned,
+ * on the context's device) with the same kernels and bits, whose workspace is a fixed scratch
+ * area of BB_NOALLOC_SCRATCH_BYTES in the library's static device memory (one per GPU, set up
+ * by bb_ctx_create and held until the process ends) instead of the context's workspace. It
+ * calls no hipMalloc, hipFree or other allocating routine. A call whose workspace exceeds the
+ * area returns BB_ERR_RANGE (at hidden = ff = 2048, k = 4: up to 440 tokens). Every call
+ * on one GPU shares that GPU's area: calls that overlap on one GPU (other contexts, other
+ * streams) race and must be ordered by the caller. No route trace; calls made while per-kernel
+ * profiling is on are not timed. */
+#define BB_NOALLOC_SCRATCH_BYTES (32u << 20)
+int bb_moe_forward_noalloc(bb_ctx* ctx, bb_moe* moe, const float* x, size_t T, float* out);
+
 /* ---- dense FFN and the FFN-path layer stack ---------------------------------------------- */
 /* dense_ffn (model.rs:459-469) / dense_ffn_batch (:262-278): gate/up [hidden, ff], down [ff, hidden].
  * Unlike bb_moe_create, the layer reads the three tensors in place: they must outlive it. */
