@@ -537,6 +537,416 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   }
 }
 
+// ---- grouped GEMM for large groups ------------------------------------------------------------
+// Block = up to 256 members (NT <= 16 member tiles of 16) x 128 weight rows (two 64-row packed
+// tiles), 8 waves, one block per CU (two waves per SIMD with up to 256 VGPRs each). Wave w owns
+// the 16 rows (w&3) of packed tile (w>>2) against all the block's members.
+// The GEMM is bound by VALU issue: per output and super-block the exact f32 epilogue takes 8
+// (Q4_K) or 5 (Q6_K) VALU instructions against 3 or 2 MFMA passes, and the nibble / scale
+// operand build (~100 VALU per lane and super-block) is shared by the wave's member tiles, so a
+// wave takes as many member tiles as its registers hold. Within a wave the work is
+// software-pipelined so that the MFMA unit and the VALU work side by side:
+//   * the epilogue of member tile t-1 is issued between the MFMAs of tile t;
+//   * the operands of super-block b+1 are built during the second half of b's member tiles,
+//     into a second operand set, from weight bytes loaded into registers at the start of b
+//     (no other wave reads a wave's weight rows, so they skip LDS).
+// Activations (the members' 256 quants per super-block, chunks XOR-swizzled as in k_gemm, and
+// their scales) are copied HBM -> LDS with buffer loads to LDS, double-buffered per super-block.
+// Nothing is in flight when a wave ends: the last super-block issues no copies or loads.
+// An expert's members are cut into chunks of 256 and the rest into chunks of 8, 4, 2 and 1
+// member tiles (a partial last tile wastes at most 15 members per expert); the tile loop of a
+// chunk is straight-line code. Epilogues and sums are those of k_gemm.
+constexpr int WIDE_LOG = 4;                // chunks of at most 2^WIDE_LOG member tiles
+constexpr int WIDE_NB = 16 << WIDE_LOG;    // members per block at most (256)
+constexpr int WIDE_WAVES = 8;
+constexpr int WIDE_PT = WIDE_WAVES / 4;    // 64-row packed tiles per block
+constexpr int WIDE_XS = WIDE_NB * QK;      // activation bytes per stage
+
+// A lane's weight bytes of one super-block: Q4_K the header and the 4 qs chunks its MFMA
+// operands come from, Q6_K its 2 ql, 2 qh and sc chunks and d.
+template <int DT>
+struct WideW;
+template <>
+struct WideW<DT_Q4_K> {
+  uint4 hd, q[4];
+};
+template <>
+struct WideW<DT_Q6_K> {
+  uint4 sc, ql[2], qh[2];
+  uint32_t d;
+};
+
+// Buffer resources (gfx9 raw buffers: base, byte size, word 3 = 0x00020000): loads through them
+// take a 32-bit per-lane offset and a wave-uniform one, so a lane keeps one register per stream
+// instead of a 64-bit address per load. An access at or past the size reads zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+// global_load_lds through a buffer: 16 (or 4) bytes a lane into dst + 16·lane (4·lane)
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, (int)voff, (int)soff, 0,
+                                           0);
+}
+__device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, (int)voff, (int)soff, 0,
+                                           0);
+}
+
+// A lane's offsets in its packed tile (row = its weight row, g = its K group): the row's 16
+// bytes of a 1 KB chunk, shifted by chunk g or g & 1; Q6_K's d field of the row.
+struct WideOff {
+  uint32_t row, g, g1, d;
+};
+
+// Loads super-block b's bytes (sb = b·TB, wave-uniform) from the wave's packed tile.
+template <int DT>
+__device__ __forceinline__ void wide_load(WideW<DT>& w, __amdgpu_buffer_rsrc_t r, const WideOff& o, uint32_t sb) {
+  if constexpr (DT == DT_Q4_K) {
+    w.hd = buf_load16(r, o.row, sb);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w.q[c] = buf_load16(r, o.g1, sb + 1024 * (1 + 2 * c));
+  } else {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      w.ql[n] = buf_load16(r, o.g, sb + 4096 * n);
+      w.qh[n] = buf_load16(r, o.g1, sb + 1024 * (8 + 2 * n));
+    }
+    w.sc = buf_load16(r, o.row, sb + 1024 * 12);
+    w.d = __builtin_amdgcn_raw_buffer_load_b16(r, (int)o.d, (int)sb, 0);
+  }
+}
+
+// The lane's MFMA weight operands of one super-block (as q4_block / q6_block build them):
+// B[0..3] the high, B[4..7] the low parts; Q4_K's min pass takes for chunk c the byte ms[c]
+// in every position (splat when used).
+template <int DT>
+struct WideB {
+  v4i B[8];
+  uint32_t ms[4];
+  float d, dm;
+};
+
+__device__ __forceinline__ void wide_build(const WideW<DT_Q4_K>& w, int g, WideB<DT_Q4_K>& o) {
+  o.d = f16_bits_to_f32(w.hd.x & 0xffff);
+  o.dm = f16_bits_to_f32(w.hd.x >> 16);
+  const uint32_t s0 = w.hd.y, s1 = w.hd.z, s2 = w.hd.w;
+  const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
+  const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+  const int hi = g >> 1;
+  const uint32_t nsh = 4 * hi;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int sh = 8 * (2 * (c & 1) + hi);
+    const uint4 qv = w.q[c];
+    const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
+                           (qv.w >> nsh) & 0x0F0F0F0Fu};
+    const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
+    const uint32_t hs = scv >> 3, ls = scv & 7u;
+    o.ms[c] = splat_byte(mw[c >> 1] >> sh);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o.B[c][k] = (int)mul_bytes(q[k], hs);
+      o.B[4 + c][k] = (int)mul_bytes(q[k], ls);
+    }
+  }
+}
+
+__device__ __forceinline__ void wide_build(const WideW<DT_Q6_K>& w, int g, WideB<DT_Q6_K>& o) {
+  o.d = f16_bits_to_f32(w.d & 0xffff);
+  o.dm = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    // elements 64c + 16g + t: ql chunk 4(c/2) + g (high nibbles when c is odd), qh chunk
+    // 8 + 2(c/2) + (g&1) bits 2·gq with gq = 2(c&1) + g/2; sub-block 4c + g (dequant.rs:122-138)
+    const int gq = 2 * (c & 1) + (g >> 1);
+    const uint4 qlv = w.ql[c >> 1], qhv = w.qh[c >> 1];
+    const uint32_t lsh = 4 * (c & 1), hsh = 2 * gq;
+    const uint32_t scd = c == 0 ? w.sc.x : c == 1 ? w.sc.y : c == 2 ? w.sc.z : w.sc.w;
+    const int scj = (int)(int8_t)((scd >> (8 * g)) & 0xffu);
+    const uint32_t scp = ((uint32_t)scj & 0xffffu) * 0x00010001u;
+    const uint32_t bias = ((uint32_t)(-32 * scj) & 0xffffu) * 0x00010001u;
+    const uint32_t qlw[4] = {qlv.x, qlv.y, qlv.z, qlv.w}, qhw[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t q = ((qlw[k] >> lsh) & 0x0F0F0F0Fu) | (((qhw[k] >> hsh) & 0x03030303u) << 4);
+      uint32_t hh, ll;
+      q6_split(q, scp, bias, hh, ll);
+      o.B[c][k] = (int)hh;
+      o.B[4 + c][k] = (int)ll;
+    }
+    o.ms[c] = 0;
+  }
+}
+
+// One member tile's integer sums of one super-block (16 members x 16 rows, 4 a lane): ax holds
+// the tile's four activation chunks; each is replaced by the next tile's (nx) once its MFMAs
+// are issued, so the LDS reads of tile t+1 are in flight during tile t.
+template <int DT, bool NEXT>
+__device__ __forceinline__ void wide_mfma(v4i (&ax)[4], const uint8_t* nx, const uint32_t (&xo)[4], const WideB<DT>& B,
+                                          v4i (&D)[3]) {
+  D[0] = D[1] = D[2] = (v4i){0, 0, 0, 0};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    D[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[c], B.B[c], D[0], 0, 0, 0);
+    D[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[c], B.B[4 + c], D[1], 0, 0, 0);
+    if constexpr (DT == DT_Q4_K) {
+      const int m = (int)B.ms[c];
+      D[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[c], ((v4i){m, m, m, m}), D[2], 0, 0, 0);
+    }
+    if constexpr (NEXT) ax[c] = *reinterpret_cast<const v4i*>(nx + xo[c]);
+  }
+}
+
+// The f32 epilogue of one member tile and super-block (matmul.rs:242 Q4_K, :641 Q6_K).
+template <int DT>
+__device__ __forceinline__ void wide_epi(float (&acc)[4], const v4i (&D)[3], const float4 sx4, float d, float dm) {
+  const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (DT == DT_Q4_K) {
+      const int sd = 8 * D[0][i] + D[1][i];
+      acc[i] += sxv[i] * ((d * (float)sd) - (dm * (float)D[2][i]));
+    } else {
+      const int sv = 64 * D[0][i] + D[1][i];
+      acc[i] += sxv[i] * (d * (float)sv);
+    }
+  }
+}
+
+// Chunk `tile` of the member chunks, enumerated class by class (every expert's chunks of 16
+// member tiles, then those of 8, 4, 2 and 1), so the largest blocks come first in the grid.
+struct WideTile {
+  int e, m0, cnt, base, g, nt;
+};
+
+__device__ bool find_wide_tile(const RouteBufs& rb, int E, int tile, WideTile& wt, int32_t* sh) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int c = lane < E ? rb.counts[lane] : 0;
+    const int st = (c + 15) >> 4;  // member tiles of the expert
+    int n[WIDE_LOG + 1];
+    n[0] = st >> WIDE_LOG;
+#pragma unroll
+    for (int k = 1; k <= WIDE_LOG; ++k) n[k] = (st >> (WIDE_LOG - k)) & 1;
+    int before = 0;  // chunks of the classes enumerated before class k
+    int m0 = 0;      // members of the expert's chunks of classes before k
+#pragma unroll
+    for (int k = 0; k <= WIDE_LOG; ++k) {
+      int incl = n[k];
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      const int total = __shfl(incl, 63);
+      const int excl = incl - n[k];
+      if (lane < E && tile >= before + excl && tile < before + incl) {
+        sh[0] = lane;
+        sh[1] = m0 + (tile - before - excl) * (WIDE_NB >> k);
+        sh[2] = c;
+        sh[3] = rb.offsets[lane];
+        sh[5] = (1 << WIDE_LOG) >> k;
+      }
+      before += total;
+      m0 += n[k] * (WIDE_NB >> k);
+    }
+    if (lane == 63) sh[4] = before;
+  }
+  __syncthreads();
+  if (tile >= sh[4]) return false;
+  wt.e = __builtin_amdgcn_readfirstlane(sh[0]);
+  wt.m0 = __builtin_amdgcn_readfirstlane(sh[1]);
+  wt.g = __builtin_amdgcn_readfirstlane(sh[2]);
+  wt.base = __builtin_amdgcn_readfirstlane(sh[3]);
+  wt.nt = __builtin_amdgcn_readfirstlane(sh[5]);
+  wt.cnt = min(16 * wt.nt, wt.g - wt.m0);
+  return true;
+}
+
+struct WideSmem {
+  uint8_t *xa0, *xa1;  // activation stages
+  float *sxa0, *sxa1;
+  uint8_t* trash;      // destination of the padding copies
+  int32_t *rowidx, *outrow;
+  uint64_t* exptab;
+};
+
+template <int DT, int KIND, int NT>
+__device__ __forceinline__ void wide_body(const WideTile wt, const uint8_t* __restrict__ wpk, size_t stride_e,
+                                          int n_rows, int n_in, int K, int n_out, int t64, const RouteBufs& rb, GemmX x,
+                                          float* __restrict__ out, const WideSmem& sm) {
+  constexpr int TB = GemmTraits<DT>::TB;
+  constexpr int NM = 16 * NT;                    // members of the chunk (the last tile may be partial)
+  constexpr int NW = WIDE_WAVES;
+  constexpr int XOPS = (NT * 4 + NW - 1) / NW;   // activation copies of 1 KB per wave and super-block
+  constexpr int SOPS = (NM + 63) / 64;           // scale copies (64 members each)
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(w);
+  const int nb = n_in / QK;
+  const int t16 = w & 3, row = 16 * t16 + r;
+  const size_t tile_bytes = (size_t)nb * TB;
+  // this lane's weight stream: its row in packed tile t64 of the expert
+  const uint8_t* wtile = wpk + (size_t)wt.e * stride_e + (size_t)t64 * tile_bytes;
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wtile, (uint32_t)tile_bytes);
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(x.q, (uint32_t)n_rows * (uint32_t)n_in);
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(x.sx, (uint32_t)n_rows * (uint32_t)nb * 4u);
+  const WideOff wo{(uint32_t)(16 * row), (uint32_t)(16 * row + 1024 * g), (uint32_t)(16 * row + 1024 * (g & 1)),
+                   (uint32_t)(1024 * 13 + 2 * row)};
+  WideW<DT> wq;
+  wide_load<DT>(wq, rw, wo, 0);
+  for (int n = tid; n < NM; n += blockDim.x) {
+    const int pos = wt.base + wt.m0 + min(n, wt.cnt - 1);  // padding repeats the last member
+    const int ent = rb.perm[pos];
+    sm.rowidx[n] = KIND == GEMM_GATEUP ? ent / K : pos;
+    sm.outrow[n] = n < wt.cnt ? (KIND == GEMM_GATEUP ? pos : ent) : -1;
+  }
+  lds_barrier();  // rowidx, outrow (and the exp table)
+  // per-lane source offsets of the wave's activation copies (copy j = wv + NW·t: members 4j..4j+3)
+  uint32_t xoff[XOPS];
+#pragma unroll
+  for (int t = 0; t < XOPS; ++t) {
+    const int j = min(wv + NW * t, NT * 4 - 1), m = 4 * j + (lane >> 4), c = (lane & 15) ^ (m & 15);
+    xoff[t] = (uint32_t)sm.rowidx[m] * (uint32_t)n_in + 16u * (uint32_t)c;
+  }
+  const uint32_t soff = (uint32_t)sm.rowidx[min(64 * min(wv, SOPS - 1) + lane, NM - 1)] * (uint32_t)nb * 4u;
+  // every wave issues XOPS + 1 copies per super-block (short lists are padded with copies into
+  // a scratch area)
+  auto issue_x = [&](int b, uint8_t* xd, float* sd) {
+#pragma unroll
+    for (int t = 0; t < XOPS; ++t) {
+      const int j = wv + NW * t;
+      buf_dma16(rx, xoff[t], (uint32_t)(b * QK), j < NT * 4 ? xd + j * 1024 : sm.trash);
+    }
+    buf_dma4(rs, soff, (uint32_t)(4 * b), wv < SOPS ? reinterpret_cast<uint8_t*>(sd + 64 * wv) : sm.trash);
+  };
+  issue_x(0, sm.xa0, sm.sxa0);
+  // per-lane LDS byte offsets of the activation chunk a lane reads at step c of a member tile
+  uint32_t xo[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xo[c] = (uint32_t)(r * QK + 16 * ((4 * c + g) ^ r));
+  const float start = wt.g > 1 ? 0.0f : -0.0f;
+  float acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[t][i] = start;
+  WideB<DT> B0, B1;
+  wide_build(wq, g, B0);
+  // super-block b: activations in (xb, sb), operands in Bc; the copies of b+1 go to (xn, sn) and
+  // its operands are built into Bn
+  auto step = [&](int b, const uint8_t* xb, const float* sb, uint8_t* xn, float* sn, const WideB<DT>& Bc,
+                  WideB<DT>& Bn) {
+    // this wave's copies of super-block b landed, then every wave's; the barrier orders LDS only
+    // (__syncthreads' release fence would also wait for the weight loads issued below)
+    __builtin_amdgcn_s_waitcnt(0x3f70);
+    lds_barrier();  // and the stages written next are no longer read
+    if (b + 1 < nb) {
+      wide_load<DT>(wq, rw, wo, (uint32_t)((b + 1) * TB));  // first: waiting for them leaves the copies in flight
+      issue_x(b + 1, xn, sn);
+    }
+    v4i ax[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ax[c] = *reinterpret_cast<const v4i*>(xb + xo[c]);
+    v4i Dp[3];
+    float4 sxp;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t == (NT + 1) / 2) {
+        // the second half of the tiles hides the build of b+1's operands
+        __builtin_amdgcn_sched_barrier(0);
+        wide_build(wq, g, Bn);
+      }
+      v4i D[3];
+      if (t + 1 < NT) wide_mfma<DT, true>(ax, xb + (t + 1) * 16 * QK, xo, Bc, D);
+      else wide_mfma<DT, false>(ax, xb, xo, Bc, D);
+      if (t > 0) wide_epi<DT>(acc[t - 1], Dp, sxp, Bc.d, Bc.dm);
+#pragma unroll
+      for (int k = 0; k < 3; ++k) Dp[k] = D[k];
+      sxp = *reinterpret_cast<const float4*>(sb + t * 16 + 4 * g);
+    }
+    if constexpr (NT == 1) wide_build(wq, g, Bn);
+    wide_epi<DT>(acc[NT - 1], Dp, sxp, Bc.d, Bc.dm);
+  };
+  for (int b = 0; b < nb; b += 2) {
+    step(b, sm.xa0, sm.sxa0, sm.xa1, sm.sxa1, B0, B1);
+    if (b + 1 >= nb) break;
+    step(b + 1, sm.xa1, sm.sxa1, sm.xa0, sm.sxa0, B1, B0);
+  }
+  if constexpr (KIND == GEMM_GATEUP) {
+    // the up waves hand their values to the gate waves of the same outputs (through the first
+    // activation stage, no longer read after this barrier)
+    __builtin_amdgcn_s_waitcnt(0x3f70);
+    __syncthreads();
+    const int k64 = w >> 2;
+    float* upv = reinterpret_cast<float*>(sm.xa0);  // 2PT up waves x 4NT values x 64 lanes <= 64 KB
+    if (t16 >= 2) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) upv[((k64 * 2 + (t16 - 2)) * (4 * NT) + t * 4 + i) * 64 + lane] = acc[t][i];
+    }
+    __syncthreads();
+    if (t16 < 2) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = t * 16 + 4 * g + i;
+          if (sm.outrow[n] < 0) continue;
+          const float up = upv[((k64 * 2 + t16) * (4 * NT) + t * 4 + i) * 64 + lane];
+          out[(size_t)sm.outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[t][i], sm.exptab) * up;
+        }
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = t * 16 + 4 * g + i;
+        if (sm.outrow[n] < 0) continue;
+        out[(size_t)sm.outrow[n] * n_out + 64 * t64 + 16 * t16 + r] = acc[t][i];
+      }
+  }
+}
+
+template <int DT, int KIND>
+__global__ void __launch_bounds__(64 * WIDE_WAVES, 2) k_gemm_wide(const uint8_t* __restrict__ wpk, size_t stride_e, int n_rows, int n_in, int K,
+                                                   int n_out, int E, RouteBufs rb, GemmX x, float* __restrict__ out) {
+  // every stage a separate array: the compiler then knows a copy into one stage does not write
+  // what is read from another, and waits for no copy in flight when it reads the current stage
+  __shared__ __align__(16) uint8_t xa0[WIDE_XS], xa1[WIDE_XS];
+  __shared__ __align__(16) float sxa0[WIDE_NB], sxa1[WIDE_NB];
+  __shared__ __align__(16) uint8_t trash[1024];
+  __shared__ int32_t rowidx[WIDE_NB], outrow[WIDE_NB];
+  __shared__ int32_t sh[8];
+  __shared__ uint64_t exptab[32];
+  const uint64_t exp_e = KIND == GEMM_GATEUP ? exp_table_entry() : 0;
+  // XCD k takes chunks k, k+8, ... and sweeps every row tile of one chunk before the next
+  // (snake order), so a chunk's activations are fetched into that XCD's L2 once
+  const int n_rt = gridDim.y, n_mt = gridDim.x;
+  const int lin = blockIdx.y * n_mt + blockIdx.x;
+  const int xcd = lin & 7, slot = lin >> 3;
+  const int mt_local = slot / n_rt, rt_step = slot % n_rt;
+  const int mtile = mt_local * 8 + xcd;
+  const int rtile = (mt_local & 1) ? n_rt - 1 - rt_step : rt_step;
+  WideTile wt;
+  if (!find_wide_tile(rb, E, mtile, wt, sh)) return;
+  if (KIND == GEMM_GATEUP && threadIdx.x < 32) exptab[threadIdx.x] = exp_e;  // published by wide_body's barrier
+  const int t64 = WIDE_PT * rtile + (__builtin_amdgcn_readfirstlane(threadIdx.x) >> 8);
+  const WideSmem sm{xa0, xa1, sxa0, sxa1, trash, rowidx, outrow, exptab};
+  static_assert(WIDE_LOG == 4, "chunk sizes of the switch below");
+  switch (wt.nt) {
+    case 16: wide_body<DT, KIND, 16>(wt, wpk, stride_e, n_rows, n_in, K, n_out, t64, rb, x, out, sm); break;
+    case 8: wide_body<DT, KIND, 8>(wt, wpk, stride_e, n_rows, n_in, K, n_out, t64, rb, x, out, sm); break;
+    case 4: wide_body<DT, KIND, 4>(wt, wpk, stride_e, n_rows, n_in, K, n_out, t64, rb, x, out, sm); break;
+    case 2: wide_body<DT, KIND, 2>(wt, wpk, stride_e, n_rows, n_in, K, n_out, t64, rb, x, out, sm); break;
+    default: wide_body<DT, KIND, 1>(wt, wpk, stride_e, n_rows, n_in, K, n_out, t64, rb, x, out, sm); break;
+  }
+}
+
 // Member tile (in units of 16 members): 16 for decode-sized batches (these tiles take their
 // grouping from the selections), else 64; Q6_K rows take 128 when the groups fill such tiles
 // on average. (A Q4_K block of 64 members leaves room for two blocks per CU, which beat one
@@ -544,10 +954,28 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
 // still fills a CU's LDS alone.)
 int gemm_member_tiles(int n_ent, int E) { return n_ent >= 16 * E ? 4 : 1; }
 
+// Q6_K down GEMMs whose groups hold this many members on average take k_gemm_wide (blocks of up
+// to 256 members). For config 4 (4096 tokens, Zipf-skewed groups) it runs the Q6_K down GEMM in
+// 228 µs against k_gemm's 274; the Q4_K gate/up GEMM, whose 3-pass epilogue and operand build
+// are heavier, runs in 578 µs against k_gemm's 442 at its two waves per SIMD, so gate/up and Q4_K
+// rows stay on k_gemm.
+constexpr int WIDE_MIN_AVG = 192;
+
 template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
                               int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
   const int n_ent = T * K;
+  if constexpr (DT == DT_Q6_K && KIND == GEMM_DOWN) {
+    // (the kernel addresses x with 32-bit byte offsets)
+    if (n_ent >= WIDE_MIN_AVG * E && (uint64_t)n_ent * (uint64_t)n_in < (1ull << 31)) {
+      // chunks: the expert's c members give at most c/256 chunks of 16 member tiles (summed
+      // over experts: n_ent/256 + E) and one chunk of each smaller size
+      const int n_mt = (n_ent / WIDE_NB + (WIDE_LOG + 1) * E + 7) / 8 * 8;
+      BB_LAUNCH((k_gemm_wide<DT, KIND>), dim3(n_mt, n_t64 / WIDE_PT), dim3(64 * WIDE_WAVES), 0, s, w, stride_e, n_ent,
+                n_in, K, n_out, E, rb, x, out);
+      return hipGetLastError();
+    }
+  }
   const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
   const int bn = 16 * mt;
   // enough member tiles: with tiles of 16, ceil(T/16) per expert (an expert has at most T

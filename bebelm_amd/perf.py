@@ -1,6 +1,6 @@
 """Profiling driver and counter post-processing for the MoE kernels (not part of the product path).
 
-Three subcommands:
+Four subcommands:
 
   python3 -m bebelm_amd.perf drive --config 2 [--steps 50] [--layers 12]
       Runs the config's MoE layer `steps` times on cuda:0 (rotating `layers` weight sets, as
@@ -19,6 +19,12 @@ Three subcommands:
       *_kernel_stats.csv of the `rocprofv3 --kernel-trace --stats` run CMD of bench.py, and the
       bench line B of the unprofiled run BCMD (the profiler's own completion signals slow the
       bench's event-timed pass, so its line comes from a run without it).
+
+  python3 -m bebelm_amd.perf pmc --csv P1.csv P2.csv ... --commands C1 C2 ... --config 4
+      Writes profiles/pmc_<workload>.md: per kernel whose name contains one of --kernels, the
+      mean per dispatch of every counter of the `rocprofv3 --pmc` passes (one CSV per pass;
+      the commands that made them are quoted), with instruction counts per wave and the
+      VALU : MFMA instruction ratio.
 """
 import argparse
 import collections
@@ -157,6 +163,56 @@ def stats(args):
     print(path)
 
 
+def pmc(args):
+    sys.path.insert(0, ROOT)
+    from bebelm_amd import synth
+
+    cfg = synth.CONFIGS[args.config]
+    # kernel -> counter -> per-dispatch totals (a dispatch's rows, one per XCD / SE instance,
+    # are summed)
+    per = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
+    names = {}
+    for path in args.csv:
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                k = row["Kernel_Name"]
+                if not any(s in k for s in args.kernels):
+                    continue
+                short = k.split("(")[0]
+                names[short] = k
+                per[short][row["Counter_Name"]][row.get("Dispatch_Id", "?")] += float(row["Counter_Value"])
+    lines = [f"# PMC counters — config {args.config} ({cfg.name}): {cfg.description}", "",
+             "Commands (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` first), one "
+             "`rocprofv3 --pmc` pass each:", "", "```"] + list(args.commands) + ["```", "",
+             "Mean per dispatch (each dispatch's rows summed over the counter's hardware instances):", ""]
+    for short, counters in sorted(per.items()):
+        mean = {c: sum(v.values()) / max(1, len(v)) for c, v in counters.items()}
+        n = max(len(v) for v in counters.values())
+        lines += [f"## `{short}` ({n} dispatches)", "", "| counter | per dispatch |", "|---|---|"]
+        for c in sorted(mean):
+            lines.append(f"| {c} | {mean[c]:,.0f} |")
+        waves = mean.get("SQ_WAVES")
+        derived = []
+        if "SQ_INSTS_VALU" in mean and "SQ_INSTS_MFMA" in mean and mean["SQ_INSTS_MFMA"]:
+            derived.append(f"VALU : MFMA instructions = {mean['SQ_INSTS_VALU'] / mean['SQ_INSTS_MFMA']:.2f}")
+        if waves:
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU"):
+                if c in mean:
+                    derived.append(f"{c} per wave = {mean[c] / waves:,.0f}")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and "SQ_BUSY_CYCLES" in mean and mean["SQ_BUSY_CYCLES"]:
+            derived.append(f"SQ_VALU_MFMA_BUSY_CYCLES / SQ_BUSY_CYCLES = "
+                           f"{mean['SQ_VALU_MFMA_BUSY_CYCLES'] / mean['SQ_BUSY_CYCLES']:.2f}")
+        if derived:
+            lines += [""] + [f"* {d}" for d in derived]
+        lines.append("")
+    if args.note:
+        lines += [args.note, ""]
+    path = os.path.join(ROOT, "profiles", f"pmc_{cfg.name}.md")
+    with open(path, "w") as f:
+        f.write("\n".join(lines))
+    print(path)
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -178,8 +234,14 @@ def main():
     st.add_argument("--config", type=int, default=2)
     st.add_argument("--command", required=True)
     st.add_argument("--bench-command", required=True)
+    pm = sub.add_parser("pmc")
+    pm.add_argument("--csv", nargs="+", required=True)
+    pm.add_argument("--commands", nargs="+", required=True)
+    pm.add_argument("--kernels", nargs="+", default=["k_gemm"])
+    pm.add_argument("--config", type=int, default=4)
+    pm.add_argument("--note", default=None)
     args = ap.parse_args()
-    {"drive": drive, "traffic": traffic, "stats": stats}[args.cmd](args)
+    {"drive": drive, "traffic": traffic, "stats": stats, "pmc": pmc}[args.cmd](args)
 
 
 if __name__ == "__main__":
