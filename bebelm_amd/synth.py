@@ -159,6 +159,75 @@ def dense_weights(seed, layer=0, hidden=HIDDEN, ff=DENSE_FF, dtype=Q4_K):
     return DenseWeights(hidden, ff, dtype, dtype, dtype, gate, up, down)
 
 
+# The decoder layer's operators (src/config.rs:20-31): GQA attention with 32 query heads, 8 kv
+# heads of 64 dims, NEOX RoPE base 5e6; the gated short conv with a 3-tap filter.
+N_HEADS = 32
+N_KV_HEADS = 8
+HEAD_DIM = HIDDEN // N_HEADS
+CONV_L_CACHE = 3
+ROPE_THETA = 5_000_000.0
+
+
+@dataclass
+class ConvWeights:
+    hidden: int
+    l_cache: int
+    in_dtype: int
+    out_dtype: int
+    in_proj: np.ndarray         # u8, [hidden, 3·hidden]: 3·hidden rows of hidden
+    out_proj: np.ndarray        # u8, [hidden, hidden]
+    conv_w: np.ndarray          # f32 [hidden·l_cache], tap-contiguous per channel
+
+
+@dataclass
+class AttnWeights:
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    q_dtype: int
+    k_dtype: int
+    v_dtype: int
+    o_dtype: int
+    q: np.ndarray               # u8, [hidden, n_heads·head_dim]
+    k: np.ndarray               # u8, [hidden, n_kv_heads·head_dim]
+    v: np.ndarray
+    o: np.ndarray               # u8, [n_heads·head_dim, hidden]
+    q_norm: np.ndarray          # f32 [head_dim]
+    k_norm: np.ndarray
+    eps: float = RMS_EPS
+    freq_base: float = ROPE_THETA
+
+    @property
+    def kv_dim(self):
+        return self.n_kv_heads * self.head_dim
+
+
+def conv_weights(seed, layer=0, hidden=HIDDEN, l_cache=CONV_L_CACHE, in_dtype=Q4_K, out_dtype=Q4_K):
+    """Short-conv operator: Q4_K/Q6_K projections as the expert tensors; filter taps ~ N(0, 0.5)."""
+    base = 100 * layer
+    in_proj = quant_tensor(rng(seed, base + 11), in_dtype, hidden, 3 * hidden)
+    out_proj = quant_tensor(rng(seed, base + 12), out_dtype, hidden, hidden)
+    conv_w = (rng(seed, base + 13).standard_normal(hidden * l_cache, dtype=np.float32) * np.float32(0.5)).astype(np.float32)
+    return ConvWeights(hidden, l_cache, in_dtype, out_dtype, in_proj, out_proj, conv_w)
+
+
+def attn_weights(seed, layer=0, hidden=HIDDEN, n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, head_dim=None,
+                 dtypes=(Q4_K, Q4_K, Q6_K, Q4_K), freq_base=ROPE_THETA):
+    """GQA attention operator: q/k/v/o in the given dtypes; q/k norm gains ~ 1 + N(0, 0.1)."""
+    hd = hidden // n_heads if head_dim is None else head_dim
+    base = 100 * layer
+    qd, kd, vd, od = dtypes
+    q = quant_tensor(rng(seed, base + 21), qd, hidden, n_heads * hd)
+    k = quant_tensor(rng(seed, base + 22), kd, hidden, n_kv_heads * hd)
+    v = quant_tensor(rng(seed, base + 23), vd, hidden, n_kv_heads * hd)
+    o = quant_tensor(rng(seed, base + 24), od, n_heads * hd, hidden)
+    g = rng(seed, base + 25)
+    q_norm = (1.0 + 0.1 * g.standard_normal(hd)).astype(np.float32)
+    k_norm = (1.0 + 0.1 * g.standard_normal(hd)).astype(np.float32)
+    return AttnWeights(hidden, n_heads, n_kv_heads, hd, qd, kd, vd, od, q, k, v, o, q_norm, k_norm, RMS_EPS, freq_base)
+
+
 def hidden_states(seed, t, hidden=HIDDEN, stream=0):
     return rng(seed, 7000 + stream).standard_normal((t, hidden), dtype=np.float32)
 

@@ -772,6 +772,147 @@ void rmsnorm(const float* x, const float* g, float eps, size_t n, float* out) {
   for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * g[i];
 }
 
+// ---- operators of the decoder layer (full decode layer and batched prefill) ----
+
+// conv.rs:18-39: causal depthwise conv, one token. The filter's last tap multiplies the current
+// column, earlier taps the cached columns (oldest first); sum = w[L-1]·bx, then += w[k]·state[k].
+void conv_step(const float* state, const float* bx, const float* w, size_t C, size_t L, float* out) {
+  for (size_t c = 0; c < C; ++c) {
+    const float* wc = w + c * L;
+    float sum = wc[L - 1] * bx[c];
+    for (size_t k = 0; k + 1 < L; ++k) sum += wc[k] * state[k * C + c];
+    out[c] = sum;
+  }
+}
+
+// conv.rs:48-68: conv_step per position, then the state slides one column and takes bx_t.
+// (The reference's slice ranges require L >= 2 here.)
+void conv_prefill(float* state, const float* bx, const float* w, size_t C, size_t L, size_t n, float* out) {
+  for (size_t t = 0; t < n; ++t) {
+    const float* bxt = bx + t * C;
+    conv_step(state, bxt, w, C, L, out + t * C);
+    std::memmove(state, state + C, (L - 2) * C * sizeof(float));
+    std::memcpy(state + (L - 2) * C, bxt, C * sizeof(float));
+  }
+}
+
+// softmax.rs:9-22: max by `if a >= b { a } else { b }` from the first element, exps of
+// (v - max) with f32 exp (libm expf), their sum in f64 left to right from 0.0, then each
+// value times (float)(1.0 / sum).
+void softmax(float* x, size_t n) {
+  if (n == 0) return;
+  float mx = x[0];
+  for (size_t i = 1; i < n; ++i) mx = mx >= x[i] ? mx : x[i];
+  double sum = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    x[i] = std::exp(x[i] - mx);
+    sum += double(x[i]);
+  }
+  const float inv = float(1.0 / sum);
+  for (size_t i = 0; i < n; ++i) x[i] *= inv;
+}
+
+// attention.rs:17-55: one query per head against n_ctx cached positions; kv head = h / group;
+// score = dot(q, k) * (1 / sqrt(head_dim)) with matmul.rs's dot; softmax; out = Σ_j w_j·v_j
+// accumulated in position order from 0.0 (a rounded multiply, then an add).
+void attention_decode(const float* q, const float* k, const float* v, size_t n_ctx, size_t n_heads, size_t n_kv,
+                      size_t hd, float* out) {
+  const float scale = 1.0f / std::sqrt(float(hd));
+  const size_t group = n_heads / n_kv;
+  std::vector<float> sc(n_ctx);
+  for (size_t h = 0; h < n_heads; ++h) {
+    const size_t kv = h / group;
+    const float* qh = q + h * hd;
+    for (size_t j = 0; j < n_ctx; ++j) sc[j] = dot_f32(qh, k + (j * n_kv + kv) * hd, hd) * scale;
+    softmax(sc.data(), n_ctx);
+    float* o = out + h * hd;
+    for (size_t d = 0; d < hd; ++d) o[d] = 0.0f;
+    for (size_t j = 0; j < n_ctx; ++j) {
+      const float* vj = v + (j * n_kv + kv) * hd;
+      for (size_t d = 0; d < hd; ++d) o[d] += sc[j] * vj[d];
+    }
+  }
+}
+
+// rope.rs:17-30: NEOX split-half rotation; theta_scale = powf(freq_base, -2/d), the angle
+// starts at (float)pos and is multiplied by theta_scale per pair (f32), sin/cos are libm's.
+void rope_neox(float* x, size_t d, size_t pos, float freq_base) {
+  const size_t half = d / 2;
+  const float theta_scale = std::pow(freq_base, -2.0f / float(d));
+  float theta = float(pos);
+  for (size_t i = 0; i < half; ++i) {
+    const float sn = std::sin(theta), cs = std::cos(theta);
+    const float a = x[i], b = x[i + half];
+    x[i] = a * cs - b * sn;
+    x[i + half] = a * sn + b * cs;
+    theta *= theta_scale;
+  }
+}
+
+// model.rs:692-701: per head rmsnorm over head_dim (into a temporary, copied back), then RoPE.
+void norm_rope_heads(float* buf, size_t n_heads, size_t hd, const float* gain, float eps, size_t pos,
+                     float freq_base) {
+  std::vector<float> tmp(hd);
+  for (size_t h = 0; h < n_heads; ++h) {
+    float* head = buf + h * hd;
+    rmsnorm(head, gain, eps, hd, tmp.data());
+    std::memcpy(head, tmp.data(), hd * sizeof(float));
+    rope_neox(head, hd, pos, freq_base);
+  }
+}
+
+// y = W·x for t token-major rows as the reference's operators call it: matvec1 for one token
+// (model.rs:557-560), matmul1 for a batch (model.rs:372-375).
+int project(uint32_t dt, const uint8_t* w, size_t n_in, size_t n_out, const float* x, size_t t, float* y) {
+  return t == 1 ? matvec(dt, w, n_in, n_out, x, y) : matmul(dt, w, n_in, n_out, x, t, y);
+}
+
+// model.rs:399-427 (one token, conv_step + the state shift) and :190-216 (a batch,
+// conv_prefill): in_proj -> (B, C, x_gate) chunks; Bx = B·x_gate; conv; y = C·conv; out_proj.
+int conv_op(const bbo_conv_op* op, float* state, const float* x, size_t t, float* out) {
+  const size_t H = size_t(op->hidden), L = size_t(op->l_cache);
+  std::vector<float> bcx(t * 3 * H), bx(t * H), conv(t * H), y(t * H);
+  if (project(op->in_dtype, op->in_proj, H, 3 * H, x, t, bcx.data())) return -1;
+  for (size_t i = 0; i < t; ++i)
+    for (size_t c = 0; c < H; ++c) bx[i * H + c] = bcx[i * 3 * H + c] * bcx[i * 3 * H + 2 * H + c];
+  if (t == 1) {
+    conv_step(state, bx.data(), op->conv_w, H, L, conv.data());
+    std::memmove(state, state + H, (L - 2) * H * sizeof(float));
+    std::memcpy(state + (L - 2) * H, bx.data(), H * sizeof(float));
+  } else {
+    conv_prefill(state, bx.data(), op->conv_w, H, L, t, conv.data());
+  }
+  for (size_t i = 0; i < t; ++i)
+    for (size_t c = 0; c < H; ++c) y[i * H + c] = bcx[i * 3 * H + H + c] * conv[i * H + c];
+  return project(op->out_dtype, op->out_proj, H, H, y.data(), t, out);
+}
+
+// model.rs:430-456 (one token) and :222-259 (a batch): q/k/v projections, per-head q/k norm
+// and RoPE at each token's position, k/v appended to the cache, each token attending over the
+// cache as it stands after its own append, o projection. The caches hold `cap` positions of
+// n_kv·head_dim floats; *n_cached grows by t.
+int attn_op(const bbo_attn_op* op, float* k_cache, float* v_cache, size_t cap, size_t* n_cached, size_t pos0,
+            const float* x, size_t t, float* out) {
+  const size_t H = size_t(op->hidden), NH = size_t(op->n_heads), NKV = size_t(op->n_kv_heads),
+               HD = size_t(op->head_dim), KV = NKV * HD;
+  if (*n_cached + t > cap) return -2;
+  std::vector<float> q(t * NH * HD), k(t * KV), v(t * KV), attn(t * NH * HD);
+  if (project(op->q_dtype, op->q, H, NH * HD, x, t, q.data())) return -1;
+  if (project(op->k_dtype, op->k, H, KV, x, t, k.data())) return -1;
+  if (project(op->v_dtype, op->v, H, KV, x, t, v.data())) return -1;
+  for (size_t i = 0; i < t; ++i) {
+    norm_rope_heads(q.data() + i * NH * HD, NH, HD, op->q_norm, op->eps, pos0 + i, op->freq_base);
+    norm_rope_heads(k.data() + i * KV, NKV, HD, op->k_norm, op->eps, pos0 + i, op->freq_base);
+  }
+  for (size_t i = 0; i < t; ++i) {
+    std::memcpy(k_cache + *n_cached * KV, k.data() + i * KV, KV * sizeof(float));
+    std::memcpy(v_cache + *n_cached * KV, v.data() + i * KV, KV * sizeof(float));
+    *n_cached += 1;
+    attention_decode(q.data() + i * NH * HD, k_cache, v_cache, *n_cached, NH, NKV, HD, attn.data() + i * NH * HD);
+  }
+  return project(op->o_dtype, op->o, NH * HD, H, attn.data(), t, out);
+}
+
 }  // namespace
 
 extern "C" {
@@ -856,6 +997,30 @@ int bbo_ffn_stack(const bbo_layer* layers, size_t n_layers, const float* x, size
     for (size_t i = 0; i < t * H; ++i) h[i] += ffn[i];
   }
   return 0;
+}
+
+void bbo_conv_step(const float* state, const float* bx, const float* w, size_t C, size_t L, float* out) {
+  conv_step(state, bx, w, C, L, out);
+}
+void bbo_conv_prefill(float* state, const float* bx, const float* w, size_t C, size_t L, size_t n, float* out) {
+  conv_prefill(state, bx, w, C, L, n, out);
+}
+void bbo_softmax(float* x, size_t n) { softmax(x, n); }
+void bbo_attention_decode(const float* q, const float* k, const float* v, size_t n_ctx, size_t n_heads, size_t n_kv,
+                          size_t hd, float* out) {
+  attention_decode(q, k, v, n_ctx, n_heads, n_kv, hd, out);
+}
+void bbo_rope_neox(float* x, size_t d, size_t pos, float freq_base) { rope_neox(x, d, pos, freq_base); }
+void bbo_norm_rope_heads(float* buf, size_t n_heads, size_t hd, const float* gain, float eps, size_t pos,
+                         float freq_base) {
+  norm_rope_heads(buf, n_heads, hd, gain, eps, pos, freq_base);
+}
+int bbo_conv_forward(const bbo_conv_op* op, float* state, const float* x, size_t t, float* out) {
+  return conv_op(op, state, x, t, out);
+}
+int bbo_attn_forward(const bbo_attn_op* op, float* k_cache, float* v_cache, size_t cap, size_t* n_cached, size_t pos0,
+                const float* x, size_t t, float* out) {
+  return attn_op(op, k_cache, v_cache, cap, n_cached, pos0, x, t, out);
 }
 
 }  // extern "C"

@@ -23,6 +23,17 @@
  *                                                  fmaf chains + the AVX reduce_add tree.
  *   sort tie order                                 PARITY UNPINNED for exactly equal keys
  *                                                  (sort_unstable_by); ties are counted.
+ *   conv_step / conv_prefill                       known answers conv.rs:77-144 (432, 400, 15,
+ *                                                  [12, 64]) and prefill == rolled steps
+ *   softmax                                        known answers softmax.rs:34-108, the f64-sum
+ *                                                  discrimination test, closed forms
+ *   attention_decode                               known answers attention.rs:64-92, brute force
+ *                                                  in f64, invariants (one position -> v)
+ *   rope_neox                                      rope.rs:37-78 (identity at 0, angle = pos for
+ *                                                  the first pair, split-half pairing, norm);
+ *                                                  sin/cos/pow are the platform libm's, as the
+ *                                                  reference's f32 sin_cos / powf
+ *   conv / attention operators                     batch == token by token (model.rs:668-705)
  */
 #ifndef BB_ORACLE_H
 #define BB_ORACLE_H
@@ -83,6 +94,26 @@ typedef struct {
   int hidden, ff;
 } bbo_dense;
 
+/* Gated short-conv operator weights (model.rs:399-427): in_proj [hidden, 3·hidden], conv filter
+ * f32[hidden·l_cache] (tap-contiguous), out_proj [hidden, hidden]. */
+typedef struct {
+  int hidden, l_cache;
+  uint32_t in_dtype, out_dtype;
+  const uint8_t* in_proj;
+  const uint8_t* out_proj;
+  const float* conv_w;
+} bbo_conv_op;
+
+/* GQA attention operator weights (model.rs:430-456): q [hidden, n_heads·head_dim], k/v [hidden,
+ * n_kv·head_dim], o [n_heads·head_dim, hidden]; q/k norm gains f32[head_dim]. */
+typedef struct {
+  int hidden, n_heads, n_kv_heads, head_dim;
+  uint32_t q_dtype, k_dtype, v_dtype, o_dtype;
+  const uint8_t *q, *k, *v, *o;
+  const float *q_norm, *k_norm;
+  float eps, freq_base;
+} bbo_attn_op;
+
 /* One FFN-path layer of the config-5 stack: rmsnorm gain + dense or MoE FFN. */
 typedef struct {
   const float* ffn_norm;   /* [hidden] */
@@ -131,6 +162,21 @@ int bbo_moe_ffn_batch(const bbo_moe* m, const float* x, size_t t, float* out, bb
 int bbo_dense_ffn(const bbo_dense* d, const float* x, size_t t, float* out);
 int bbo_ffn_stack(const bbo_layer* layers, size_t n_layers, const float* x, size_t t, float eps,
                   float* h_out);
+
+/* Operators of the decoder layer: conv.rs:18-39 / :48-68, softmax.rs:9-22, attention.rs:17-55,
+ * rope.rs:17-30, model.rs:692-701 (per-head norm + RoPE), model.rs:399-427 / :190-216 (gated
+ * short conv, one token / a batch), model.rs:430-456 / :222-259 (GQA attention). */
+void bbo_conv_step(const float* state, const float* bx, const float* w, size_t C, size_t L, float* out);
+void bbo_conv_prefill(float* state, const float* bx, const float* w, size_t C, size_t L, size_t n, float* out);
+void bbo_softmax(float* x, size_t n);
+void bbo_attention_decode(const float* q, const float* k, const float* v, size_t n_ctx, size_t n_heads, size_t n_kv,
+                          size_t hd, float* out);
+void bbo_rope_neox(float* x, size_t d, size_t pos, float freq_base);
+void bbo_norm_rope_heads(float* buf, size_t n_heads, size_t hd, const float* gain, float eps, size_t pos,
+                         float freq_base);
+int bbo_conv_forward(const bbo_conv_op* op, float* state, const float* x, size_t t, float* out);
+int bbo_attn_forward(const bbo_attn_op* op, float* k_cache, float* v_cache, size_t cap, size_t* n_cached, size_t pos0,
+                const float* x, size_t t, float* out);
 
 #ifdef __cplusplus
 }

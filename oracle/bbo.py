@@ -132,6 +132,16 @@ def lib():
         L.bbo_dot_variant.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
         L.bbo_router_logits_variant.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_int, c_int, c_void_p]
         L.bbo_gate.argtypes = [c_void_p, c_void_p, c_size_t, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p]
+        L.bbo_conv_step.argtypes = [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_void_p]
+        L.bbo_conv_prefill.argtypes = [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p]
+        L.bbo_softmax.argtypes = [c_void_p, c_size_t]
+        L.bbo_attention_decode.argtypes = [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t,
+                                           c_void_p]
+        L.bbo_rope_neox.argtypes = [c_void_p, c_size_t, c_size_t, c_float]
+        L.bbo_norm_rope_heads.argtypes = [c_void_p, c_size_t, c_size_t, c_void_p, c_float, c_size_t, c_float]
+        L.bbo_conv_forward.argtypes = [ctypes.POINTER(ConvOp), c_void_p, c_void_p, c_size_t, c_void_p]
+        L.bbo_attn_forward.argtypes = [ctypes.POINTER(AttnOp), c_void_p, c_void_p, c_size_t,
+                                       ctypes.POINTER(c_size_t), c_size_t, c_void_p, c_size_t, c_void_p]
         L.bbo_set_threads.argtypes = [c_int]
         L.bbo_get_threads.restype = c_int
         _lib = L
@@ -395,3 +405,109 @@ def ffn_stack(layers, x, t=1, eps=1e-5):
     h = np.zeros_like(x)
     _chk(lib().bbo_ffn_stack(arr, len(layers), _p(x), t, eps, _p(h)))
     return h
+
+
+# ---- operators of the decoder layer ------------------------------------------------------------
+
+class ConvOp(ctypes.Structure):
+    _fields_ = [("hidden", c_int), ("l_cache", c_int), ("in_dtype", ctypes.c_uint32), ("out_dtype", ctypes.c_uint32),
+                ("in_proj", c_void_p), ("out_proj", c_void_p), ("conv_w", c_void_p)]
+
+
+class AttnOp(ctypes.Structure):
+    _fields_ = [("hidden", c_int), ("n_heads", c_int), ("n_kv_heads", c_int), ("head_dim", c_int),
+                ("q_dtype", ctypes.c_uint32), ("k_dtype", ctypes.c_uint32), ("v_dtype", ctypes.c_uint32),
+                ("o_dtype", ctypes.c_uint32), ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("o", c_void_p),
+                ("q_norm", c_void_p), ("k_norm", c_void_p), ("eps", c_float), ("freq_base", c_float)]
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32).reshape(-1)
+
+
+def conv_step(state, bx, weight, channels, l_cache):
+    """conv.rs:18-39: out f32[channels]."""
+    state, bx, weight = _f32(state), _f32(bx), _f32(weight)
+    out = np.zeros(channels, np.float32)
+    lib().bbo_conv_step(_p(state), _p(bx), _p(weight), channels, l_cache, _p(out))
+    return out
+
+
+def conv_prefill(state, bx, weight, channels, l_cache, n_tokens):
+    """conv.rs:48-68: (out f32[n_tokens·channels], the updated state)."""
+    state, bx, weight = _f32(state).copy(), _f32(bx), _f32(weight)
+    out = np.zeros(n_tokens * channels, np.float32)
+    lib().bbo_conv_prefill(_p(state), _p(bx), _p(weight), channels, l_cache, n_tokens, _p(out))
+    return out, state
+
+
+def softmax(x):
+    """softmax.rs:9-22 over one row."""
+    x = _f32(x).copy()
+    lib().bbo_softmax(_p(x), x.size)
+    return x
+
+
+def attention_decode(q, k, v, n_ctx, n_heads, n_kv_heads, head_dim):
+    """attention.rs:17-55: out f32[n_heads·head_dim]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    lib().bbo_attention_decode(_p(q), _p(k), _p(v), n_ctx, n_heads, n_kv_heads, head_dim, _p(out))
+    return out
+
+
+def rope_neox(x, pos, freq_base):
+    """rope.rs:17-30 on one head vector."""
+    x = _f32(x).copy()
+    lib().bbo_rope_neox(_p(x), x.size, pos, freq_base)
+    return x
+
+
+def norm_rope_heads(buf, n_heads, head_dim, gain, eps, pos, freq_base):
+    """model.rs:692-701."""
+    buf, gain = _f32(buf).copy(), _f32(gain)
+    lib().bbo_norm_rope_heads(_p(buf), n_heads, head_dim, _p(gain), eps, pos, freq_base)
+    return buf
+
+
+def _conv_struct(w):
+    return ConvOp(w.hidden, w.l_cache, w.in_dtype, w.out_dtype, _p(w.in_proj), _p(w.out_proj), _p(w.conv_w))
+
+
+def conv_forward(w, state, x, t):
+    """Model::conv_step_op (t == 1, model.rs:399-427) or conv_batch (model.rs:190-216):
+    (out f32[t·hidden], the updated state)."""
+    state, x = _f32(state).copy(), _f32(x)
+    out = np.zeros(t * w.hidden, np.float32)
+    s = _conv_struct(w)
+    _chk(lib().bbo_conv_forward(ctypes.byref(s), _p(state), _p(x), t, _p(out)))
+    return out, state
+
+
+class KvCache:
+    """One attention layer's key/value history (model.rs:447-448): cap positions of kv_dim floats."""
+
+    def __init__(self, kv_dim, cap):
+        self.kv_dim, self.cap = kv_dim, cap
+        self.k = np.zeros(cap * kv_dim, np.float32)
+        self.v = np.zeros(cap * kv_dim, np.float32)
+        self.n = 0
+
+
+def _attn_struct(w):
+    return AttnOp(w.hidden, w.n_heads, w.n_kv_heads, w.head_dim, w.q_dtype, w.k_dtype, w.v_dtype, w.o_dtype,
+                  _p(w.q), _p(w.k), _p(w.v), _p(w.o), _p(w.q_norm), _p(w.k_norm), w.eps, w.freq_base)
+
+
+def attn_forward(w, cache, pos0, x, t):
+    """Model::attn_step (t == 1, model.rs:430-456) or attn_batch (model.rs:222-259); appends t
+    positions to `cache` and returns out f32[t·hidden]."""
+    x = _f32(x)
+    out = np.zeros(t * w.hidden, np.float32)
+    s = _attn_struct(w)
+    n = c_size_t(cache.n)
+    rc = lib().bbo_attn_forward(ctypes.byref(s), _p(cache.k), _p(cache.v), cache.cap, ctypes.byref(n), pos0, _p(x),
+                                t, _p(out))
+    _chk(rc)
+    cache.n = n.value
+    return out
