@@ -79,6 +79,25 @@ _SIGS = {
     "bb_stack_create": (c_int, [c_void_p, P(LayerDesc), c_size_t, c_float, P(c_void_p)]),
     "bb_stack_destroy": (c_int, [c_void_p]),
     "bb_stack_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int]),
+    "bb_conv_step": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_int]),
+    "bb_conv_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p,
+                                c_int]),
+    "bb_softmax": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_int]),
+    "bb_attention_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t,
+                                    c_void_p, c_int]),
+    "bb_rope_neox": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_float, c_int]),
+    "bb_conv_op_create": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, P(c_void_p)]),
+    "bb_conv_op_destroy": (c_int, [c_void_p]),
+    "bb_conv_op_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int]),
+    "bb_kv_cache_create": (c_int, [c_void_p, c_size_t, c_size_t, P(c_void_p)]),
+    "bb_kv_cache_destroy": (c_int, [c_void_p]),
+    "bb_kv_cache_length": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_kv_cache_read": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int]),
+    "bb_kv_cache_evict_front": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "bb_attn_op_create": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                  c_size_t, c_float, c_float, P(c_void_p)]),
+    "bb_attn_op_destroy": (c_int, [c_void_p]),
+    "bb_attn_op_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_int]),
 }
 
 _lib = None

@@ -2,6 +2,8 @@
 // host-side sequencing of the kernels in the order the reference's model.rs issues them.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <exception>
@@ -547,6 +549,173 @@ void matmul_dev(bb_ctx* c, uint32_t dtype, const bb_tensor* w, size_t byte_off, 
   } else {
     launch(c, bb::K_ROWS_F32, [&] { return bb::launch_rows_f32(c->stream, (int)dtype, wp, n_in, n_out, x, nt, y); });
   }
+}
+
+// ---- decoder-layer operators (bb_ops.hip) ----------------------------------------------------
+// Q8 buffers of one projection input (T rows of n_in), carved like the other workspaces.
+bb::Q8Bufs carve_q8(Carve& cv, size_t T, size_t n_in) {
+  return {cv.take<int8_t>(T * n_in), cv.take<float>(T * n_in / 256), cv.take<int32_t>(T * n_in / 32)};
+}
+
+// y = W·x for T token-major rows as the reference's operators call it: matvec1 for one token
+// (model.rs:557-560), matmul1 for a batch (:372-375); both are the row kernels (the one-token
+// form sums from -0.0 as matvec does). q: Q8 buffers for x when W is Q4_K / Q6_K.
+void project_dev(bb_ctx* c, const bb_tensor* w, size_t n_in, size_t n_out, const float* x, size_t T, float* y,
+                 bb::Q8Bufs q) {
+  size_t row_bytes;
+  check_weight_range(w, w->dtype, 0, n_in, n_out, row_bytes);
+  if (w->dtype == BB_Q4_K || w->dtype == BB_Q6_K) {
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, n_in, q); });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)w->dtype, w->dev, row_bytes, (int)(n_in / 256), n_out, q, n_in, T, y,
+                                n_out, T == 1);
+    });
+  } else {
+    launch(c, bb::K_ROWS_F32, [&] { return bb::launch_rows_f32(c->stream, (int)w->dtype, w->dev, n_in, n_out, x, T, y); });
+  }
+}
+
+void need_proj(const bb_tensor* t, uint64_t n_in, uint64_t n_out, const char* what) {
+  need(t != nullptr, BB_ERR_ARG, std::string(what) + " is null");
+  need(t->ndims == 2 && t->dims[0] == n_in && t->dims[1] == n_out, BB_ERR_SHAPE,
+       std::string(what) + " must be [" + std::to_string(n_in) + ", " + std::to_string(n_out) + "]");
+  need(t->dtype == BB_Q4_K || t->dtype == BB_Q6_K || t->dtype == BB_F32 || t->dtype == BB_F16, BB_ERR_DTYPE,
+       std::string(what) + ": dtype must be F32, F16, Q4_K or Q6_K");
+  if (t->dtype == BB_Q4_K || t->dtype == BB_Q6_K) need(n_in % 256 == 0, BB_ERR_SHAPE, "n_in must be a multiple of 256");
+}
+
+float* upload_f32(const float* host, size_t n) {
+  float* d = static_cast<float*>(dev_alloc(n * 4));
+  if (hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(d);
+    fail(BB_ERR_HIP, "hipMemcpy of a host array failed");
+  }
+  return d;
+}
+
+// (cos, sin) of RoPE pair i at `pos` as rope.rs:17-30 computes them: theta from (float)pos,
+// multiplied by powf(base, -2/d) after each pair; libm's sinf / cosf (what f32::sin_cos calls).
+void rope_rows(std::vector<float2>& out, size_t pos0, size_t n_pos, size_t hd, float freq_base) {
+  const size_t half = hd / 2;
+  const float theta_scale = std::pow(freq_base, -2.0f / float(hd));
+  out.resize(n_pos * half);
+  for (size_t p = 0; p < n_pos; ++p) {
+    float theta = float(pos0 + p);
+    for (size_t i = 0; i < half; ++i) {
+      out[p * half + i] = make_float2(std::cos(theta), std::sin(theta));
+      theta *= theta_scale;
+    }
+  }
+}
+
+}  // namespace
+
+struct bb_conv_op {
+  bb_ctx* ctx;
+  const bb_tensor* in_proj;
+  const bb_tensor* out_proj;
+  float* conv_w;  // device, [hidden][l_cache]
+  int H, L;
+};
+
+struct bb_kv_cache {
+  bb_ctx* ctx;
+  float* k;
+  float* v;
+  size_t kv_dim, cap, n;
+};
+
+struct bb_attn_op {
+  bb_ctx* ctx;
+  const bb_tensor *q, *k, *v, *o;
+  float *q_norm, *k_norm;  // device, [head_dim]
+  int H, NH, NKV, HD;
+  float eps, freq_base, scale;
+  float2* rope = nullptr;  // device (cos, sin) rows [rope_rows][head_dim/2] for positions 0..
+  size_t rope_rows = 0;
+};
+
+namespace {
+
+// model.rs:399-427 (T == 1) and :190-216 (T > 1) on device pointers; state [(L-1)][H] is updated.
+void conv_forward_dev(bb_ctx* c, bb_conv_op* op, float* state, const float* x, size_t T, float* out) {
+  const size_t H = op->H;
+  uint8_t* base = nullptr;
+  for (int pass = 0; pass < 2; ++pass) {
+    Carve cv{base};
+    bb::Q8Bufs xq = carve_q8(cv, T, H);
+    float* bcx = cv.take<float>(T * 3 * H);
+    float* y = cv.take<float>(T * H);
+    bb::Q8Bufs yq = carve_q8(cv, T, H);
+    if (pass == 0) {
+      base = ensure_ws(c, cv.off);
+      continue;
+    }
+    project_dev(c, op->in_proj, H, 3 * H, x, T, bcx, xq);
+    launch(c, bb::K_CONV, [&] { return bb::launch_conv(c->stream, true, bcx, state, op->conv_w, (int)H, op->L, (int)T, y); });
+    launch(c, bb::K_CONV_STATE, [&] { return bb::launch_conv_state(c->stream, true, bcx, state, (int)H, op->L, (int)T); });
+    project_dev(c, op->out_proj, H, H, y, T, out, yq);
+  }
+}
+
+// Grows the op's RoPE table to at least `rows` positions (recomputed on the host, uploaded once).
+void ensure_rope(bb_ctx* c, bb_attn_op* op, size_t rows) {
+  if (rows <= op->rope_rows) return;
+  const size_t n = std::max<size_t>({rows, 2 * op->rope_rows, 4096});
+  std::vector<float2> tab;
+  rope_rows(tab, 0, n, op->HD, op->freq_base);
+  auto* d = static_cast<float2*>(dev_alloc(tab.size() * sizeof(float2)));
+  if (hipMemcpy(d, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(d);
+    fail(BB_ERR_HIP, "RoPE table upload failed");
+  }
+  if (op->rope) {
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    (void)hipFree(op->rope);
+  }
+  op->rope = d;
+  op->rope_rows = n;
+}
+
+// model.rs:430-456 (T == 1) and :222-259 (T > 1) on device pointers: the T new keys / values
+// are projected straight into the cache rows n .. n+T-1.
+void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out) {
+  const size_t H = op->H, NH = op->NH, NKV = op->NKV, HD = op->HD, KV = NKV * HD, QD = NH * HD;
+  const size_t n0 = kv->n;
+  ensure_rope(c, op, pos0 + T);
+  uint8_t* base = nullptr;
+  for (int pass = 0; pass < 2; ++pass) {
+    Carve cv{base};
+    bb::Q8Bufs xq = carve_q8(cv, T, H);
+    float* q = cv.take<float>(T * QD);
+    float* scores = cv.take<float>(T * NH * (n0 + T));
+    float* attn = cv.take<float>(T * QD);
+    bb::Q8Bufs aq = carve_q8(cv, T, QD);
+    if (pass == 0) {
+      base = ensure_ws(c, cv.off);
+      continue;
+    }
+    float* kn = kv->k + n0 * KV;
+    float* vn = kv->v + n0 * KV;
+    project_dev(c, op->q, H, QD, x, T, q, xq);
+    project_dev(c, op->k, H, KV, x, T, kn, xq);
+    project_dev(c, op->v, H, KV, x, T, vn, xq);
+    const float2* rope = op->rope + pos0 * (HD / 2);
+    launch(c, bb::K_NORM_ROPE, [&] {
+      return bb::launch_norm_rope(c->stream, q, (int)T, (int)NH, (int)HD, op->q_norm, op->eps, rope);
+    });
+    launch(c, bb::K_NORM_ROPE, [&] {
+      return bb::launch_norm_rope(c->stream, kn, (int)T, (int)NKV, (int)HD, op->k_norm, op->eps, rope);
+    });
+    launch(c, bb::K_ATTN_SCORES, [&] {
+      return bb::launch_attn_scores(c->stream, q, kv->k, (int)n0, (int)T, (int)NH, (int)NKV, (int)HD, op->scale, scores);
+    });
+    launch(c, bb::K_ATTN_PV, [&] {
+      return bb::launch_attn_pv(c->stream, scores, kv->v, (int)n0, (int)T, (int)NH, (int)NKV, (int)HD, attn);
+    });
+    project_dev(c, op->o, QD, H, attn, T, out, aq);
+  }
+  kv->n = n0 + T;
 }
 
 }  // namespace
@@ -1163,6 +1332,328 @@ int bb_stack_forward(bb_ctx* c, bb_stack* s, const float* x, size_t T, float* h_
         routed = route_next;
       }
       check_hip(hipMemcpyAsync(d[1], h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+    });
+  });
+}
+
+// ---- decoder-layer operators -------------------------------------------------------------------
+
+int bb_conv_step(bb_ctx* c, const float* state, const float* bx, const float* weight, size_t channels, size_t l_cache,
+                 float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(channels >= 1 && l_cache >= 1, BB_ERR_ARG, "channels and l_cache must be >= 1");
+    need(channels * l_cache < (1u << 31), BB_ERR_RANGE, "conv too large");
+    set_device(c);
+    const size_t C = channels, L = l_cache;
+    with_io(c, loc,
+            {{state, (L - 1) * C * 4, true, false}, {bx, C * 4, true, false}, {weight, C * L * 4, true, false},
+             {out, C * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              launch(c, bb::K_CONV, [&] {
+                return bb::launch_conv(c->stream, false, static_cast<const float*>(d[1]),
+                                       static_cast<const float*>(d[0]), static_cast<const float*>(d[2]), (int)C, (int)L,
+                                       1, static_cast<float*>(d[3]));
+              });
+            });
+  });
+}
+
+int bb_conv_prefill(bb_ctx* c, float* state, const float* bx, const float* weight, size_t channels, size_t l_cache,
+                    size_t n_tokens, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(channels >= 1 && l_cache >= 2, BB_ERR_ARG, "channels >= 1 and l_cache >= 2 required (conv.rs:58-66)");
+    need(n_tokens >= 1, BB_ERR_ARG, "n_tokens must be >= 1");
+    need(channels * (l_cache + n_tokens) < (1u << 31), BB_ERR_RANGE, "conv too large");
+    set_device(c);
+    const size_t C = channels, L = l_cache, T = n_tokens;
+    with_io(c, loc,
+            {{state, (L - 1) * C * 4, true, true}, {bx, T * C * 4, true, false}, {weight, C * L * 4, true, false},
+             {out, T * C * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              float* st = static_cast<float*>(d[0]);
+              const float* b = static_cast<const float*>(d[1]);
+              launch(c, bb::K_CONV, [&] {
+                return bb::launch_conv(c->stream, false, b, st, static_cast<const float*>(d[2]), (int)C, (int)L, (int)T,
+                                       static_cast<float*>(d[3]));
+              });
+              launch(c, bb::K_CONV_STATE,
+                     [&] { return bb::launch_conv_state(c->stream, false, b, st, (int)C, (int)L, (int)T); });
+            });
+  });
+}
+
+int bb_softmax(bb_ctx* c, float* x, size_t n, size_t n_vec, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(n < (1u << 30) && n_vec < (1u << 30), BB_ERR_RANGE, "softmax too large");
+    if (n == 0 || n_vec == 0) return;
+    set_device(c);
+    with_io(c, loc, {{x, n * n_vec * 4, true, true}}, [&](std::vector<void*>& d) {
+      launch(c, bb::K_SOFTMAX, [&] { return bb::launch_softmax(c->stream, static_cast<float*>(d[0]), n, n_vec); });
+    });
+  });
+}
+
+int bb_attention_decode(bb_ctx* c, const float* q, const float* k, const float* v, size_t n_ctx, size_t n_heads,
+                        size_t n_kv_heads, size_t head_dim, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(n_ctx >= 1 && n_heads >= 1 && n_kv_heads >= 1 && head_dim >= 1, BB_ERR_ARG, "sizes must be >= 1");
+    need(n_heads % n_kv_heads == 0, BB_ERR_ARG, "n_heads must be a multiple of n_kv_heads");
+    need(head_dim <= (size_t)bb::OPS_HD_MAX, BB_ERR_RANGE, "head_dim above 256");
+    need(n_ctx * n_kv_heads * head_dim < (1u << 31) && n_ctx < (1u << 24), BB_ERR_RANGE, "context too large");
+    set_device(c);
+    const size_t QD = n_heads * head_dim, KVB = n_ctx * n_kv_heads * head_dim * 4;
+    const float scale = 1.0f / std::sqrt(float(head_dim));
+    with_io(c, loc, {{q, QD * 4, true, false}, {k, KVB, true, false}, {v, KVB, true, false}, {out, QD * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              float* scores = reinterpret_cast<float*>(ensure_ws(c, n_heads * n_ctx * 4));
+              const int n0 = (int)n_ctx - 1;
+              launch(c, bb::K_ATTN_SCORES, [&] {
+                return bb::launch_attn_scores(c->stream, static_cast<const float*>(d[0]),
+                                              static_cast<const float*>(d[1]), n0, 1, (int)n_heads, (int)n_kv_heads,
+                                              (int)head_dim, scale, scores);
+              });
+              launch(c, bb::K_ATTN_PV, [&] {
+                return bb::launch_attn_pv(c->stream, scores, static_cast<const float*>(d[2]), n0, 1, (int)n_heads,
+                                          (int)n_kv_heads, (int)head_dim, static_cast<float*>(d[3]));
+              });
+            });
+  });
+}
+
+int bb_rope_neox(bb_ctx* c, float* x, size_t head_dim, size_t n_vec, size_t pos, float freq_base, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need_loc(loc);
+    need(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= (size_t)bb::OPS_HD_MAX, BB_ERR_ARG,
+         "head_dim must be even and at most 256");
+    need(n_vec >= 1 && n_vec < (1u << 16), BB_ERR_RANGE, "n_vec must be in 1..65535");
+    set_device(c);
+    std::vector<float2> tab;
+    rope_rows(tab, pos, 1, head_dim, freq_base);
+    with_io(c, loc, {{x, n_vec * head_dim * 4, true, true}}, [&](std::vector<void*>& d) {
+      auto* t = reinterpret_cast<float2*>(ensure_ws(c, tab.size() * sizeof(float2)));
+      check_hip(hipMemcpyAsync(t, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice, c->stream),
+                "RoPE row upload");
+      // n_vec heads of one position: the heads are the kernel's head axis of one token
+      launch(c, bb::K_NORM_ROPE, [&] {
+        return bb::launch_norm_rope(c->stream, static_cast<float*>(d[0]), 1, (int)n_vec, (int)head_dim, nullptr, 0.0f,
+                                    t);
+      });
+      check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");  // tab is a host temporary
+    });
+  });
+}
+
+int bb_conv_op_create(bb_ctx* c, const bb_tensor* in_proj, const float* conv_w, size_t l_cache,
+                      const bb_tensor* out_proj, bb_conv_op** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(in_proj && out_proj && conv_w && out, BB_ERR_ARG, "null argument");
+    need(l_cache >= 2 && l_cache <= 64, BB_ERR_ARG, "l_cache must be in 2..64");
+    need(in_proj->ndims == 2, BB_ERR_SHAPE, "in_proj must be 2-D");
+    const uint64_t H = in_proj->dims[0];
+    need_proj(in_proj, H, 3 * H, "shortconv.in_proj");
+    need_proj(out_proj, H, H, "shortconv.out_proj");
+    need(H % 256 == 0 && H * 3 * 64 < (1u << 31), BB_ERR_SHAPE, "hidden must be a multiple of 256");
+    set_device(c);
+    auto* op = new bb_conv_op();
+    op->ctx = c;
+    op->in_proj = in_proj;
+    op->out_proj = out_proj;
+    op->H = (int)H;
+    op->L = (int)l_cache;
+    try {
+      op->conv_w = upload_f32(conv_w, H * l_cache);
+    } catch (...) {
+      delete op;
+      throw;
+    }
+    *out = op;
+  });
+}
+
+int bb_conv_op_destroy(bb_conv_op* op) {
+  return guard([&] {
+    if (!op) return;
+    set_device(op->ctx);
+    (void)hipFree(op->conv_w);
+    delete op;
+  });
+}
+
+int bb_conv_op_forward(bb_ctx* c, bb_conv_op* op, float* state, const float* x, size_t T, float* out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(op != nullptr && op->ctx == c, BB_ERR_ARG, "bad conv operator");
+    need_loc(loc);
+    need(T >= 1 && T <= (size_t)bb::PF_MAX_ENTRIES, BB_ERR_RANGE, "T must be in 1..32768");
+    set_device(c);
+    const size_t H = op->H;
+    with_io(c, loc,
+            {{state, (op->L - 1) * H * 4, true, true}, {x, T * H * 4, true, false}, {out, T * H * 4, false, true}},
+            [&](std::vector<void*>& d) {
+              conv_forward_dev(c, op, static_cast<float*>(d[0]), static_cast<const float*>(d[1]), T,
+                               static_cast<float*>(d[2]));
+            });
+  });
+}
+
+int bb_kv_cache_create(bb_ctx* c, size_t kv_dim, size_t capacity, bb_kv_cache** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(out != nullptr && kv_dim >= 1 && capacity >= 1, BB_ERR_ARG, "bad argument");
+    need(kv_dim * capacity < (1u << 29), BB_ERR_RANGE, "cache above 2 GB per array");
+    set_device(c);
+    auto* kv = new bb_kv_cache();
+    kv->ctx = c;
+    kv->kv_dim = kv_dim;
+    kv->cap = capacity;
+    kv->n = 0;
+    try {
+      kv->k = static_cast<float*>(dev_alloc(kv_dim * capacity * 4));
+      kv->v = static_cast<float*>(dev_alloc(kv_dim * capacity * 4));
+    } catch (...) {
+      if (kv->k) (void)hipFree(kv->k);
+      delete kv;
+      throw;
+    }
+    *out = kv;
+  });
+}
+
+int bb_kv_cache_destroy(bb_kv_cache* kv) {
+  return guard([&] {
+    if (!kv) return;
+    set_device(kv->ctx);
+    (void)hipFree(kv->k);
+    (void)hipFree(kv->v);
+    delete kv;
+  });
+}
+
+int bb_kv_cache_length(const bb_kv_cache* kv, size_t* n) {
+  return guard([&] {
+    need(kv != nullptr && n != nullptr, BB_ERR_ARG, "null argument");
+    *n = kv->n;
+  });
+}
+
+int bb_kv_cache_read(bb_ctx* c, const bb_kv_cache* kv, float* k, float* v, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(kv != nullptr && kv->ctx == c, BB_ERR_ARG, "bad cache");
+    need_loc(loc);
+    set_device(c);
+    const size_t bytes = kv->n * kv->kv_dim * 4;
+    if (bytes == 0) return;
+    need(k != nullptr && v != nullptr, BB_ERR_ARG, "null output");
+    const hipMemcpyKind kind = loc == BB_LOC_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    check_hip(hipMemcpyAsync(k, kv->k, bytes, kind, c->stream), "cache copy");
+    check_hip(hipMemcpyAsync(v, kv->v, bytes, kind, c->stream), "cache copy");
+    if (loc == BB_LOC_HOST) check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int bb_kv_cache_evict_front(bb_ctx* c, bb_kv_cache* kv, size_t n) {
+  return guard([&] {
+    need_ctx(c);
+    need(kv != nullptr && kv->ctx == c, BB_ERR_ARG, "bad cache");
+    set_device(c);
+    if (n == 0) return;
+    if (n >= kv->n) {
+      kv->n = 0;
+      return;
+    }
+    // positions n.. move to the front (device copies through a staging area: the ranges overlap)
+    const size_t keep = (kv->n - n) * kv->kv_dim * 4;
+    auto* tmp = ensure_ws(c, keep);
+    for (float* a : {kv->k, kv->v}) {
+      check_hip(hipMemcpyAsync(tmp, a + n * kv->kv_dim, keep, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+      check_hip(hipMemcpyAsync(a, tmp, keep, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+    }
+    kv->n -= n;
+  });
+}
+
+int bb_attn_op_create(bb_ctx* c, const bb_tensor* q, const bb_tensor* k, const bb_tensor* v, const bb_tensor* o,
+                      const float* q_norm, const float* k_norm, size_t n_heads, size_t n_kv_heads, float eps,
+                      float freq_base, bb_attn_op** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(q && k && v && o && q_norm && k_norm && out, BB_ERR_ARG, "null argument");
+    need(n_heads >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, BB_ERR_ARG,
+         "n_heads must be a positive multiple of n_kv_heads");
+    need(q->ndims == 2, BB_ERR_SHAPE, "attn_q must be 2-D");
+    const uint64_t H = q->dims[0], QD = q->dims[1];
+    need(QD % n_heads == 0, BB_ERR_SHAPE, "attn_q's output size must be n_heads * head_dim");
+    const uint64_t HD = QD / n_heads, KV = n_kv_heads * HD;
+    need(HD >= 2 && HD % 2 == 0 && HD <= (uint64_t)bb::OPS_HD_MAX, BB_ERR_RANGE, "head_dim must be even and <= 256");
+    need_proj(q, H, QD, "attn_q");
+    need_proj(k, H, KV, "attn_k");
+    need_proj(v, H, KV, "attn_v");
+    need_proj(o, QD, H, "attn_output");
+    set_device(c);
+    auto* op = new bb_attn_op();
+    op->ctx = c;
+    op->q = q;
+    op->k = k;
+    op->v = v;
+    op->o = o;
+    op->H = (int)H;
+    op->NH = (int)n_heads;
+    op->NKV = (int)n_kv_heads;
+    op->HD = (int)HD;
+    op->eps = eps;
+    op->freq_base = freq_base;
+    op->scale = 1.0f / std::sqrt(float(HD));  // attention.rs:35
+    try {
+      op->q_norm = upload_f32(q_norm, HD);
+      op->k_norm = upload_f32(k_norm, HD);
+      ensure_rope(c, op, 4096);
+    } catch (...) {
+      if (op->q_norm) (void)hipFree(op->q_norm);
+      if (op->k_norm) (void)hipFree(op->k_norm);
+      delete op;
+      throw;
+    }
+    *out = op;
+  });
+}
+
+int bb_attn_op_destroy(bb_attn_op* op) {
+  return guard([&] {
+    if (!op) return;
+    set_device(op->ctx);
+    (void)hipFree(op->q_norm);
+    (void)hipFree(op->k_norm);
+    if (op->rope) (void)hipFree(op->rope);
+    delete op;
+  });
+}
+
+int bb_attn_op_forward(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out,
+                       int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(op != nullptr && op->ctx == c, BB_ERR_ARG, "bad attention operator");
+    need(kv != nullptr && kv->ctx == c, BB_ERR_ARG, "bad cache");
+    need_loc(loc);
+    need(kv->kv_dim == (size_t)op->NKV * op->HD, BB_ERR_SHAPE, "cache kv_dim must be n_kv_heads * head_dim");
+    need(T >= 1 && T <= (size_t)bb::PF_MAX_ENTRIES, BB_ERR_RANGE, "T must be in 1..32768");
+    need(kv->n + T <= kv->cap, BB_ERR_RANGE, "the cache is full (evict positions first, cache.rs:40-50)");
+    need(pos0 + T < (1u << 24), BB_ERR_RANGE, "position beyond 2^24");
+    set_device(c);
+    const size_t H = op->H;
+    with_io(c, loc, {{x, T * H * 4, true, false}, {out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
+      attn_forward_dev(c, op, kv, pos0, static_cast<const float*>(d[0]), T, static_cast<float*>(d[1]));
     });
   });
 }

@@ -60,6 +60,12 @@ enum KernelId : int {
   K_COMBINE,
   K_RESIDUAL_NORM,
   K_RESIDUAL_ROUTE,
+  K_CONV,
+  K_CONV_STATE,
+  K_NORM_ROPE,
+  K_ATTN_SCORES,
+  K_ATTN_PV,
+  K_SOFTMAX,
   K_COUNT
 };
 const char* kernel_name(int id);
@@ -190,6 +196,26 @@ hipError_t launch_rmsnorm_q8(hipStream_t s, const float* x, const float* gain, f
 // h += (slots, wts, K) combine or ffn row; then normed = rmsnorm(h, gain) unless gain is null.
 hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
                                 const float* gain, float eps, size_t n, size_t n_vec, float* normed);
+
+// ---- decoder-layer operators (bb_ops.hip) ----
+constexpr int OPS_HD_MAX = 256;     // head_dim bound of the attention kernels
+constexpr int OPS_ROW_LDS = 15360;  // score rows up to this length are worked on in LDS (60 KB)
+// out[t][c] = causal conv of token t over [state; bx] (op: bx = B·x_gate from the in_proj output
+// src [T][3C], and out = C·conv); the state is read, not written.
+hipError_t launch_conv(hipStream_t s, bool op, const float* src, const float* state, const float* w, int C, int L,
+                       int T, float* out);
+// state <- the last L-1 columns of [state; bx] (run after launch_conv on the same batch).
+hipError_t launch_conv_state(hipStream_t s, bool op, const float* src, float* state, int C, int L, int T);
+// per-head rmsnorm (gain null: none) and RoPE from (cos, sin) rows [T][hd/2], in place on buf [T][n_heads][hd].
+hipError_t launch_norm_rope(hipStream_t s, float* buf, int T, int n_heads, int hd, const float* gain, float eps,
+                            const float2* rope);
+// scores [T][n_heads][n0+T]: token t's query against cached positions j < n0 + t + 1.
+hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
+                              int hd, float scale, float* scores);
+// softmax of each score row (in place), then out [T][n_heads][hd] = Σ_j w_j·v_j.
+hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0, int T, int n_heads, int n_kv, int hd,
+                          float* out);
+hipError_t launch_softmax(hipStream_t s, float* x, size_t n, size_t n_vec);
 
 }  // namespace bb
 #endif

@@ -21,7 +21,9 @@ const char* kernel_name(int id) {
   static const char* names[K_COUNT] = {"route_gating",  "gateup_swiglu", "down_combine", "quantize_q8",
                                        "rows_q8",      "rows_f32",      "elementwise",  "rmsnorm",
                                        "route_large",  "dispatch",      "gemm_gateup",  "gemm_down",
-                                       "combine",      "residual_norm", "residual_route"};
+                                       "combine",      "residual_norm", "residual_route", "conv",
+                                       "conv_state",   "norm_rope",     "attn_scores",  "attn_pv",
+                                       "softmax"};
   return (id >= 0 && id < K_COUNT) ? names[id] : "?";
 }
 

@@ -8,6 +8,10 @@
   add_scaled / add_assign                  kernels/elementwise.rs:12, :4
   rmsnorm                                  kernels/rmsnorm.rs:10
   logits_from_hidden                       model.rs:380-388
+  conv_step / conv_prefill                 kernels/conv.rs:18, :48
+  softmax                                  kernels/softmax.rs:9
+  attention_decode                         kernels/attention.rs:17
+  rope_neox                                kernels/rope.rs:17
 Each function takes the Context first; `w` is an uploaded Tensor (plus a byte offset where the
 reference passes a sub-slice of the weight bytes).
 """
@@ -103,6 +107,44 @@ def logits_from_hidden(ctx, tok_embd, gain, eps, h, logits):
     loc = _same_loc(h, gain, logits)
     check(lib().bb_logits_from_hidden(ctx.handle, tok_embd.handle, _ptr(gain)[0], eps, _ptr(h)[0], _ptr(logits)[0], loc))
     return logits
+
+
+def conv_step(ctx, state, bx, weight, channels, l_cache, out):
+    """conv.rs:18-39: out[c] = w[c, L-1]·bx[c] + Σ_k w[c, k]·state[k, c]."""
+    loc = _same_loc(state, bx, weight, out)
+    check(lib().bb_conv_step(ctx.handle, _ptr(state)[0], _ptr(bx)[0], _ptr(weight)[0], channels, l_cache, _ptr(out)[0],
+                             loc))
+    return out
+
+
+def conv_prefill(ctx, state, bx, weight, channels, l_cache, n_tokens, out):
+    """conv.rs:48-68 over n_tokens positions; state is updated in place."""
+    loc = _same_loc(state, bx, weight, out)
+    check(lib().bb_conv_prefill(ctx.handle, _ptr(state)[0], _ptr(bx)[0], _ptr(weight)[0], channels, l_cache, n_tokens,
+                                _ptr(out)[0], loc))
+    return out
+
+
+def softmax(ctx, x, n_vec=1):
+    """softmax.rs:9-22 on each of n_vec rows, in place."""
+    n = _n(x) // n_vec
+    check(lib().bb_softmax(ctx.handle, _ptr(x)[0], n, n_vec, _same_loc(x)))
+    return x
+
+
+def attention_decode(ctx, q, k, v, n_ctx, n_heads, n_kv_heads, head_dim, out):
+    """attention.rs:17-55."""
+    loc = _same_loc(q, k, v, out)
+    check(lib().bb_attention_decode(ctx.handle, _ptr(q)[0], _ptr(k)[0], _ptr(v)[0], n_ctx, n_heads, n_kv_heads,
+                                    head_dim, _ptr(out)[0], loc))
+    return out
+
+
+def rope_neox(ctx, x, head_dim, pos, freq_base):
+    """rope.rs:17-30 on each head vector of x, in place."""
+    check(lib().bb_rope_neox(ctx.handle, _ptr(x)[0], head_dim, _n(x) // head_dim, pos, ctypes.c_float(freq_base),
+                             _same_loc(x)))
+    return x
 
 
 def _n(a):

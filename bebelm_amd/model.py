@@ -4,6 +4,8 @@ Names follow the reference so call sites read alike:
   Model::moe_ffn / moe_ffn_batch (model.rs:473, :286)  -> MoeLayer.moe_ffn / moe_ffn_batch
   Model::dense_ffn (model.rs:459)                       -> DenseLayer.dense_ffn
   run_layers' FFN path (model.rs:105-130)               -> FfnStack.run_layers
+  Model::conv_step_op / conv_batch (model.rs:399, :190) -> ConvOp.forward
+  Model::attn_step / attn_batch (model.rs:430, :222)    -> AttnOp.forward (KvCache: cache.rs)
 Arrays are numpy (host memory, BB_LOC_HOST) or torch CUDA tensors (device memory,
 BB_LOC_DEVICE). Everything runs on the GPU through libbebelm_moe.so; there is no other path.
 """
@@ -248,3 +250,103 @@ class FfnStack:
         x = np.ascontiguousarray(x, np.float32).reshape(-1)
         out = np.empty_like(x)
         return self.forward(x, x.size // self.hidden, out)
+
+
+class ConvOp:
+    """The gated short-conv operator of one layer (model.rs:399-427 / :190-216)."""
+
+    def __init__(self, ctx, weights):
+        w = weights
+        self.ctx = ctx
+        self.hidden, self.l_cache = w.hidden, w.l_cache
+        self.in_proj = Tensor(ctx, w.in_dtype, w.in_proj, (w.hidden, 3 * w.hidden))
+        self.out_proj = Tensor(ctx, w.out_dtype, w.out_proj, (w.hidden, w.hidden))
+        conv_w = np.ascontiguousarray(w.conv_w, np.float32)
+        h = ctypes.c_void_p()
+        check(lib().bb_conv_op_create(ctx.handle, self.in_proj.handle, conv_w.ctypes.data, w.l_cache,
+                                      self.out_proj.handle, ctypes.byref(h)))
+        self.handle = h
+
+    def new_state(self):
+        """A fresh conv cache: l_cache - 1 zero columns (cache.rs:29)."""
+        return np.zeros((self.l_cache - 1) * self.hidden, np.float32)
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_conv_op_destroy(self.handle))
+            self.handle = None
+        for t in (self.in_proj, self.out_proj):
+            t.close()
+
+    def forward(self, state, x, t, out):
+        loc = _same_loc(state, x, out)
+        check(lib().bb_conv_op_forward(self.ctx.handle, self.handle, _ptr(state)[0], _ptr(x)[0], t, _ptr(out)[0], loc))
+        return out
+
+
+class KvCache:
+    """One attention layer's key/value history in device memory (cache.rs:10-17)."""
+
+    def __init__(self, ctx, kv_dim, capacity):
+        self.ctx, self.kv_dim, self.capacity = ctx, kv_dim, capacity
+        h = ctypes.c_void_p()
+        check(lib().bb_kv_cache_create(ctx.handle, kv_dim, capacity, ctypes.byref(h)))
+        self.handle = h
+
+    def __len__(self):
+        n = ctypes.c_size_t()
+        check(lib().bb_kv_cache_length(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def read(self):
+        n = len(self)
+        k = np.empty(n * self.kv_dim, np.float32)
+        v = np.empty(n * self.kv_dim, np.float32)
+        check(lib().bb_kv_cache_read(self.ctx.handle, self.handle, k.ctypes.data, v.ctypes.data, LOC_HOST))
+        return k, v
+
+    def evict_front(self, n):
+        check(lib().bb_kv_cache_evict_front(self.ctx.handle, self.handle, n))
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_kv_cache_destroy(self.handle))
+            self.handle = None
+
+
+class AttnOp:
+    """The GQA attention operator of one layer (model.rs:430-456 / :222-259)."""
+
+    def __init__(self, ctx, weights):
+        w = weights
+        self.ctx = ctx
+        self.hidden, self.n_heads, self.n_kv_heads, self.head_dim = w.hidden, w.n_heads, w.n_kv_heads, w.head_dim
+        qd, kvd = w.n_heads * w.head_dim, w.n_kv_heads * w.head_dim
+        self.kv_dim = kvd
+        self.q = Tensor(ctx, w.q_dtype, w.q, (w.hidden, qd))
+        self.k = Tensor(ctx, w.k_dtype, w.k, (w.hidden, kvd))
+        self.v = Tensor(ctx, w.v_dtype, w.v, (w.hidden, kvd))
+        self.o = Tensor(ctx, w.o_dtype, w.o, (qd, w.hidden))
+        qn = np.ascontiguousarray(w.q_norm, np.float32)
+        kn = np.ascontiguousarray(w.k_norm, np.float32)
+        h = ctypes.c_void_p()
+        check(lib().bb_attn_op_create(ctx.handle, self.q.handle, self.k.handle, self.v.handle, self.o.handle,
+                                      qn.ctypes.data, kn.ctypes.data, w.n_heads, w.n_kv_heads, w.eps, w.freq_base,
+                                      ctypes.byref(h)))
+        self.handle = h
+
+    def new_cache(self, capacity):
+        return KvCache(self.ctx, self.kv_dim, capacity)
+
+    def close(self):
+        if self.handle:
+            check(lib().bb_attn_op_destroy(self.handle))
+            self.handle = None
+        for t in (self.q, self.k, self.v, self.o):
+            t.close()
+
+    def forward(self, cache, pos0, x, t, out):
+        loc = _same_loc(x, out)
+        check(lib().bb_attn_op_forward(self.ctx.handle, self.handle, cache.handle, pos0, _ptr(x)[0], t, _ptr(out)[0],
+                                       loc))
+        return out

@@ -52,6 +52,9 @@ typedef struct bb_tensor bb_tensor;
 typedef struct bb_moe bb_moe;
 typedef struct bb_dense bb_dense;
 typedef struct bb_stack bb_stack;
+typedef struct bb_conv_op bb_conv_op;
+typedef struct bb_attn_op bb_attn_op;
+typedef struct bb_kv_cache bb_kv_cache;
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* bb_last_error(void);
@@ -193,6 +196,59 @@ typedef struct {
 int bb_stack_create(bb_ctx* ctx, const bb_layer_desc* layers, size_t n_layers, float eps, bb_stack** out);
 int bb_stack_destroy(bb_stack* s);
 int bb_stack_forward(bb_ctx* ctx, bb_stack* s, const float* x, size_t T, float* h_out, int loc);
+
+/* ---- the decoder layer's operators (model.rs:105-130) --------------------------------------- */
+/* Kernel-level mirrors. conv_step(state, bx, weight, channels, l_cache, out) (kernels/conv.rs:18):
+ * state f32[(l_cache-1)*channels] (oldest column first), bx and out f32[channels], weight
+ * f32[channels*l_cache] tap-contiguous; the last tap multiplies bx. */
+int bb_conv_step(bb_ctx* ctx, const float* state, const float* bx, const float* weight, size_t channels, size_t l_cache,
+                 float* out, int loc);
+/* conv_prefill(state, bx, weight, channels, l_cache, n_tokens, out) (kernels/conv.rs:48): token-major
+ * bx and out f32[n_tokens*channels]; state is updated in place to the batch's last l_cache-1
+ * columns. l_cache >= 2 (the reference's slice ranges panic below that). */
+int bb_conv_prefill(bb_ctx* ctx, float* state, const float* bx, const float* weight, size_t channels, size_t l_cache,
+                    size_t n_tokens, float* out, int loc);
+/* softmax(x) (kernels/softmax.rs:9) on each of n_vec rows of n, in place. */
+int bb_softmax(bb_ctx* ctx, float* x, size_t n, size_t n_vec, int loc);
+/* attention_decode(q, k, v, n_ctx, n_heads, n_kv_heads, head_dim, out) (kernels/attention.rs:17):
+ * q and out f32[n_heads*head_dim], k and v f32[n_ctx*n_kv_heads*head_dim]; head_dim <= 256. */
+int bb_attention_decode(bb_ctx* ctx, const float* q, const float* k, const float* v, size_t n_ctx, size_t n_heads,
+                        size_t n_kv_heads, size_t head_dim, float* out, int loc);
+/* rope_neox(x, pos, freq_base) (kernels/rope.rs:17) on each of n_vec head vectors of head_dim. */
+int bb_rope_neox(bb_ctx* ctx, float* x, size_t head_dim, size_t n_vec, size_t pos, float freq_base, int loc);
+
+/* Gated short-conv operator: Model::conv_step_op (model.rs:399-427) for T == 1 and conv_batch
+ * (model.rs:190-216) for T > 1, with the tensors Model resolves: in_proj [hidden, 3*hidden],
+ * the conv filter `shortconv.conv.weight` (host f32[hidden*l_cache], copied), out_proj
+ * [hidden, hidden] (projection tensors F32, F16, Q4_K or Q6_K; used in place, they must outlive
+ * the operator). state is the layer's conv cache f32[(l_cache-1)*hidden] (cache.rs:16-17),
+ * updated in place; x and out token-major f32[T*hidden]. */
+int bb_conv_op_create(bb_ctx* ctx, const bb_tensor* in_proj, const float* conv_w, size_t l_cache,
+                      const bb_tensor* out_proj, bb_conv_op** out);
+int bb_conv_op_destroy(bb_conv_op* op);
+int bb_conv_op_forward(bb_ctx* ctx, bb_conv_op* op, float* state, const float* x, size_t T, float* out, int loc);
+
+/* One attention layer's key/value history (cache.rs:10-17), resident in device memory:
+ * `capacity` positions of kv_dim floats each for k and v. bb_kv_cache_read copies the n cached
+ * positions out (k and v f32[n*kv_dim]); bb_kv_cache_evict_front drops the oldest n positions
+ * (Cache::evict_front, cache.rs:40-50). */
+int bb_kv_cache_create(bb_ctx* ctx, size_t kv_dim, size_t capacity, bb_kv_cache** out);
+int bb_kv_cache_destroy(bb_kv_cache* kv);
+int bb_kv_cache_length(const bb_kv_cache* kv, size_t* n);
+int bb_kv_cache_read(bb_ctx* ctx, const bb_kv_cache* kv, float* k, float* v, int loc);
+int bb_kv_cache_evict_front(bb_ctx* ctx, bb_kv_cache* kv, size_t n);
+
+/* GQA attention operator: Model::attn_step (model.rs:430-456) for T == 1 and attn_batch
+ * (model.rs:222-259) for T > 1: q [hidden, n_heads*head_dim], k and v [hidden, n_kv_heads*head_dim],
+ * o [n_heads*head_dim, hidden] (used in place), q/k norm gains host f32[head_dim] (copied),
+ * rmsnorm eps and RoPE base. Token t of the batch sits at position pos0 + t; its key and value
+ * are appended to `kv` and it attends over every cached position up to its own. */
+int bb_attn_op_create(bb_ctx* ctx, const bb_tensor* q, const bb_tensor* k, const bb_tensor* v, const bb_tensor* o,
+                      const float* q_norm, const float* k_norm, size_t n_heads, size_t n_kv_heads, float eps,
+                      float freq_base, bb_attn_op** out);
+int bb_attn_op_destroy(bb_attn_op* op);
+int bb_attn_op_forward(bb_ctx* ctx, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out,
+                       int loc);
 
 #ifdef __cplusplus
 }
