@@ -42,6 +42,11 @@ class LayerDesc(ctypes.Structure):
     _fields_ = [("ffn_norm", c_void_p), ("moe", c_void_p), ("dense", c_void_p)]
 
 
+class DecoderLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", c_void_p), ("ffn_norm", c_void_p), ("conv", c_void_p), ("attn", c_void_p),
+                ("moe", c_void_p), ("dense", c_void_p)]
+
+
 _SIGS = {
     "bb_last_error": (ctypes.c_char_p, []),
     "bb_version": (ctypes.c_char_p, []),
@@ -98,6 +103,17 @@ _SIGS = {
                                   c_size_t, c_float, c_float, P(c_void_p)]),
     "bb_attn_op_destroy": (c_int, [c_void_p]),
     "bb_attn_op_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_int]),
+    "bb_model_create": (c_int, [c_void_p, c_void_p, c_void_p, P(DecoderLayer), c_size_t, c_float, c_size_t,
+                                P(c_void_p)]),
+    "bb_model_destroy": (c_int, [c_void_p]),
+    "bb_model_reset": (c_int, [c_void_p, c_void_p]),
+    "bb_model_position": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_model_kv_length": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_model_layer_state": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_int]),
+    "bb_model_run_layers": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int]),
+    "bb_model_forward_step": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_int]),
+    "bb_model_absorb": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
+    "bb_model_evict_front": (c_int, [c_void_p, c_void_p, c_size_t]),
 }
 
 _lib = None

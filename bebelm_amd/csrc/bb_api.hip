@@ -166,6 +166,20 @@ namespace {
 
 void set_device(bb_ctx* c) { check_hip(hipSetDevice(c->device), "hipSetDevice"); }
 
+// Set-up copies and clears go on the context's stream, which is then drained. (The context's
+// stream does not wait for the null stream, so a plain hipMemcpy / hipMemset there may still
+// be running when the stream's kernels read or write the same memory.)
+void copy_to_dev(bb_ctx* c, void* dst, const void* src, size_t bytes, const char* what) {
+  if (bytes == 0) return;
+  check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), what);
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+void clear_dev(bb_ctx* c, void* dst, size_t bytes) {
+  if (bytes == 0) return;
+  check_hip(hipMemsetAsync(dst, 0, bytes, c->stream), "hipMemsetAsync");
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
 hipEvent_t take_event(bb_ctx* c) {
   if (!c->event_pool.empty()) {
     hipEvent_t e = c->event_pool.back();
@@ -218,8 +232,9 @@ uint8_t* ensure_ws(bb_ctx* c, size_t bytes) {
     c->ws_bytes = 0;
     c->ws = static_cast<uint8_t*>(dev_alloc(bytes));
     c->ws_bytes = bytes;
-    // selections read before any route wrote them must still name experts in range
-    check_hip(hipMemset(c->ws, 0, bytes), "hipMemset");
+    // selections read before any route wrote them must still name experts in range (cleared
+    // on the context's stream, so that the clear lands before the stream's next kernels)
+    check_hip(hipMemsetAsync(c->ws, 0, bytes, c->stream), "hipMemsetAsync");
   }
   return c->ws;
 }
@@ -250,6 +265,10 @@ struct Carve {
 
 void need(bool ok, int code, const std::string& msg) {
   if (!ok) fail(code, msg);
+}
+// A nested call of this library's C ABI failed: rethrow with its code and message.
+void check_code(int rc) {
+  if (rc != BB_OK) fail(rc, std::string(g_err));
 }
 // string-literal form: builds no std::string unless the check fails
 void need(bool ok, int code, const char* msg) {
@@ -584,11 +603,13 @@ void need_proj(const bb_tensor* t, uint64_t n_in, uint64_t n_out, const char* wh
   if (t->dtype == BB_Q4_K || t->dtype == BB_Q6_K) need(n_in % 256 == 0, BB_ERR_SHAPE, "n_in must be a multiple of 256");
 }
 
-float* upload_f32(const float* host, size_t n) {
+float* upload_f32(bb_ctx* c, const float* host, size_t n) {
   float* d = static_cast<float*>(dev_alloc(n * 4));
-  if (hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice) != hipSuccess) {
+  try {
+    copy_to_dev(c, d, host, n * 4, "host array upload");
+  } catch (...) {
     (void)hipFree(d);
-    fail(BB_ERR_HIP, "hipMemcpy of a host array failed");
+    throw;
   }
   return d;
 }
@@ -606,6 +627,39 @@ void rope_rows(std::vector<float2>& out, size_t pos0, size_t n_pos, size_t hd, f
       theta *= theta_scale;
     }
   }
+}
+
+// Model::logits_from_hidden (model.rs:380-388) on device pointers: rmsnorm(h, gain, eps), then
+// the token_embd matvec (hidden -> vocab).
+void logits_dev(bb_ctx* c, const bb_tensor* tok_embd, const float* gain, float eps, const float* h, float* logits) {
+  const size_t H = tok_embd->dims[0], V = tok_embd->dims[1];
+  const uint32_t dt = tok_embd->dtype;
+  if ((dt == BB_Q4_K || dt == BB_Q6_K) && H % 256 == 0 && H <= (size_t)bb::GU_H_MAX) {
+    // one launch for the rmsnorm and the Q8 of the normed row, then the rows
+    size_t row_bytes;
+    check_weight_range(tok_embd, dt, 0, H, V, row_bytes);
+    Carve cv{nullptr};
+    cv.take<int8_t>(H);
+    cv.take<float>(H / 256);
+    cv.take<int32_t>(H / 32);
+    Carve cv2{ensure_ws(c, cv.off)};
+    bb::Q8Bufs q{cv2.take<int8_t>(H), cv2.take<float>(H / 256), cv2.take<int32_t>(H / 32)};
+    launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm_q8(c->stream, h, gain, eps, H, 1, nullptr, q); });
+    launch(c, bb::K_ROWS_Q8, [&] {
+      return bb::launch_rows_q8(c->stream, (int)dt, tok_embd->dev, row_bytes, (int)(H / 256), V, q, H, 1, logits, V, 1);
+    });
+    return;
+  }
+  // normed lives past the Q8 records matmul_dev carves from the workspace's start
+  Carve cv{nullptr};
+  cv.take<int8_t>(H);
+  cv.take<float>(H / 256);
+  cv.take<int32_t>(H / 32);
+  const size_t q8_bytes = cv.off;
+  cv.take<float>(H);
+  float* normed = reinterpret_cast<float*>(ensure_ws(c, cv.off) + q8_bytes);
+  launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, h, gain, eps, H, 1, normed); });
+  matmul_dev(c, tok_embd->dtype, tok_embd, 0, H, V, normed, 1, logits);
 }
 
 }  // namespace
@@ -633,6 +687,32 @@ struct bb_attn_op {
   float eps, freq_base, scale;
   float2* rope = nullptr;  // device (cos, sin) rows [rope_rows][head_dim/2] for positions 0..
   size_t rope_rows = 0;
+};
+
+// The decoder (Model, model.rs:25-31, with the Cache of cache.rs:10-19): embedding, layers of
+// (attn_norm, conv or attention operator, ffn_norm, dense or MoE FFN), final norm and logits.
+struct bb_model {
+  bb_ctx* ctx;
+  const bb_tensor* tok_embd;
+  float* final_norm;  // device
+  float eps;
+  int H;
+  size_t vocab, row_bytes;
+  struct Layer {
+    float* attn_norm;  // device
+    float* ffn_norm;
+    bb_conv_op* conv;
+    bb_attn_op* attn;
+    bb_moe* moe;
+    bb_dense* dense;
+    float* conv_state;  // conv layers: [(L-1)][H]
+    bb_kv_cache* kv;    // attention layers
+  };
+  std::vector<Layer> layers;
+  size_t pos = 0;
+  float *h = nullptr, *normed = nullptr, *tmp = nullptr;
+  uint32_t* tok = nullptr;  // token ids of the current call
+  size_t cap_T = 0, tok_cap = 0;
 };
 
 namespace {
@@ -665,14 +745,13 @@ void ensure_rope(bb_ctx* c, bb_attn_op* op, size_t rows) {
   std::vector<float2> tab;
   rope_rows(tab, 0, n, op->HD, op->freq_base);
   auto* d = static_cast<float2*>(dev_alloc(tab.size() * sizeof(float2)));
-  if (hipMemcpy(d, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice) != hipSuccess) {
+  try {
+    copy_to_dev(c, d, tab.data(), tab.size() * sizeof(float2), "RoPE table upload");  // (drains the stream)
+  } catch (...) {
     (void)hipFree(d);
-    fail(BB_ERR_HIP, "RoPE table upload failed");
+    throw;
   }
-  if (op->rope) {
-    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    (void)hipFree(op->rope);
-  }
+  if (op->rope) (void)hipFree(op->rope);
   op->rope = d;
   op->rope_rows = n;
 }
@@ -862,8 +941,8 @@ int bb_tensor_upload(bb_ctx* c, uint32_t dtype, const void* bytes, size_t nbytes
     t->nbytes = nbytes;
     try {
       t->dev = static_cast<uint8_t*>(dev_alloc(nbytes));
-      check_hip(hipMemcpy(t->dev, bytes, nbytes, hipMemcpyHostToDevice), "upload");
-      check_hip(hipMemset(t->dev + nbytes, 0, round_up(nbytes, 256) + PAD - nbytes), "pad clear");
+      check_hip(hipMemsetAsync(t->dev + nbytes, 0, round_up(nbytes, 256) + PAD - nbytes, c->stream), "pad clear");
+      copy_to_dev(c, t->dev, bytes, nbytes, "upload");
     } catch (...) {
       if (t->dev) (void)hipFree(t->dev);
       delete t;
@@ -1016,40 +1095,8 @@ int bb_logits_from_hidden(bb_ctx* c, const bb_tensor* tok_embd, const float* gai
     set_device(c);
     with_io(c, loc, {{h, H * 4, true, false}, {gain, H * 4, true, false}, {logits, V * 4, false, true}},
             [&](std::vector<void*>& d) {
-              const uint32_t dt = tok_embd->dtype;
-              if ((dt == BB_Q4_K || dt == BB_Q6_K) && H % 256 == 0 && H <= (size_t)bb::GU_H_MAX) {
-                // one launch for the rmsnorm and the Q8 of the normed row, then the rows
-                size_t row_bytes;
-                check_weight_range(tok_embd, dt, 0, H, V, row_bytes);
-                Carve cv{nullptr};
-                cv.take<int8_t>(H);
-                cv.take<float>(H / 256);
-                cv.take<int32_t>(H / 32);
-                Carve cv2{ensure_ws(c, cv.off)};
-                bb::Q8Bufs q{cv2.take<int8_t>(H), cv2.take<float>(H / 256), cv2.take<int32_t>(H / 32)};
-                launch(c, bb::K_RMSNORM, [&] {
-                  return bb::launch_rmsnorm_q8(c->stream, static_cast<const float*>(d[0]),
-                                               static_cast<const float*>(d[1]), eps, H, 1, nullptr, q);
-                });
-                launch(c, bb::K_ROWS_Q8, [&] {
-                  return bb::launch_rows_q8(c->stream, (int)dt, tok_embd->dev, row_bytes, (int)(H / 256), V, q, H, 1,
-                                            static_cast<float*>(d[2]), V, 1);
-                });
-                return;
-              }
-              // normed lives past the Q8 records matmul_dev carves from the workspace's start
-              Carve cv{nullptr};
-              cv.take<int8_t>(H);
-              cv.take<float>(H / 256);
-              cv.take<int32_t>(H / 32);
-              const size_t q8_bytes = cv.off;
-              cv.take<float>(H);
-              float* normed = reinterpret_cast<float*>(ensure_ws(c, cv.off) + q8_bytes);
-              launch(c, bb::K_RMSNORM, [&] {
-                return bb::launch_rmsnorm(c->stream, static_cast<const float*>(d[0]), static_cast<const float*>(d[1]),
-                                          eps, H, 1, normed);
-              });
-              matmul_dev(c, tok_embd->dtype, tok_embd, 0, H, V, normed, 1, static_cast<float*>(d[2]));
+              logits_dev(c, tok_embd, static_cast<const float*>(d[1]), eps, static_cast<const float*>(d[0]),
+                         static_cast<float*>(d[2]));
             });
   });
 }
@@ -1095,7 +1142,7 @@ int bb_moe_create(bb_ctx* c, const bb_tensor* router, const float* bias, const b
     m->stride_dn = (H / 64) * (F / 256) * bb::pack_tile_block_bytes(m->dn_dtype);
     try {
       m->bias_dev = static_cast<float*>(dev_alloc(E * 4));
-      check_hip(hipMemcpy(m->bias_dev, bias, E * 4, hipMemcpyHostToDevice), "bias upload");
+      copy_to_dev(c, m->bias_dev, bias, E * 4, "bias upload");
       m->router_cm = static_cast<float*>(dev_alloc(E * H * 4));
       m->gu_packed = static_cast<uint8_t*>(dev_alloc(E * m->stride_gu));
       m->dn_packed = static_cast<uint8_t*>(dev_alloc(E * m->stride_dn));
@@ -1234,7 +1281,7 @@ int bb_stack_create(bb_ctx* c, const bb_layer_desc* layers, size_t n_layers, flo
         bb_layer_desc L = layers[i];
         float* g = static_cast<float*>(dev_alloc((size_t)H * 4));
         s->gains.push_back(g);
-        check_hip(hipMemcpy(g, layers[i].ffn_norm, (size_t)H * 4, hipMemcpyHostToDevice), "gain upload");
+        copy_to_dev(c, g, layers[i].ffn_norm, (size_t)H * 4, "gain upload");
         L.ffn_norm = g;
         s->layers.push_back(L);
       }
@@ -1471,7 +1518,7 @@ int bb_conv_op_create(bb_ctx* c, const bb_tensor* in_proj, const float* conv_w, 
     op->H = (int)H;
     op->L = (int)l_cache;
     try {
-      op->conv_w = upload_f32(conv_w, H * l_cache);
+      op->conv_w = upload_f32(c, conv_w, H * l_cache);
     } catch (...) {
       delete op;
       throw;
@@ -1615,8 +1662,8 @@ int bb_attn_op_create(bb_ctx* c, const bb_tensor* q, const bb_tensor* k, const b
     op->freq_base = freq_base;
     op->scale = 1.0f / std::sqrt(float(HD));  // attention.rs:35
     try {
-      op->q_norm = upload_f32(q_norm, HD);
-      op->k_norm = upload_f32(k_norm, HD);
+      op->q_norm = upload_f32(c, q_norm, HD);
+      op->k_norm = upload_f32(c, k_norm, HD);
       ensure_rope(c, op, 4096);
     } catch (...) {
       if (op->q_norm) (void)hipFree(op->q_norm);
@@ -1655,6 +1702,266 @@ int bb_attn_op_forward(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, 
     with_io(c, loc, {{x, T * H * 4, true, false}, {out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
       attn_forward_dev(c, op, kv, pos0, static_cast<const float*>(d[0]), T, static_cast<float*>(d[1]));
     });
+  });
+}
+
+// ---- the decoder ---------------------------------------------------------------------------------
+namespace {
+
+size_t model_kv_len(const bb_model* m) {
+  size_t n = 0;
+  for (const auto& L : m->layers)
+    if (L.kv) n = std::max(n, L.kv->n);
+  return n;
+}
+
+void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
+  if (T <= m->cap_T) return;
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  for (void** p : {(void**)&m->h, (void**)&m->normed, (void**)&m->tmp}) {
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+  }
+  m->cap_T = 0;
+  const size_t H = m->H;
+  m->h = static_cast<float*>(dev_alloc(T * H * 4));
+  m->normed = static_cast<float*>(dev_alloc(T * H * 4));
+  m->tmp = static_cast<float*>(dev_alloc(T * H * 4));
+  m->cap_T = T;
+}
+
+// The token ids of one call, checked and copied to the device once. The stream is drained
+// first: the buffer is reused by every call, and an earlier call's embedding may still read it
+// (a copy from pageable host memory is not guaranteed to wait for the stream's earlier work).
+const uint32_t* model_tokens(bb_ctx* c, bb_model* m, const uint32_t* host, size_t n) {
+  for (size_t i = 0; i < n; ++i) need(host[i] < m->vocab, BB_ERR_ARG, "token id beyond the vocabulary");
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  if (n > m->tok_cap) {
+    if (m->tok) (void)hipFree(m->tok);
+    m->tok = nullptr;
+    m->tok_cap = 0;
+    m->tok = static_cast<uint32_t*>(dev_alloc(n * 4));
+    m->tok_cap = n;
+  }
+  copy_to_dev(c, m->tok, host, n * 4, "token copy");
+  return m->tok;
+}
+
+// Model::run_layers (T == 1, model.rs:105-130) / run_layers_batch (T > 1, :146-181): embeds
+// the tokens (device ids) at positions pos.., runs every layer (updating the conv states and
+// KV caches) and leaves the final hidden states in m->h.
+void model_run_dev(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T) {
+  for (const auto& L : m->layers)
+    if (L.kv) need(L.kv->n + T <= L.kv->cap, BB_ERR_RANGE, "a KV cache is full (evict positions first)");
+  model_buffers(c, m, T);
+  const size_t H = m->H;
+  launch(c, bb::K_EMBED, [&] {
+    return bb::launch_embed(c->stream, m->tok_embd->dev, (int)m->tok_embd->dtype, m->row_bytes, tokens, (int)T, (int)H,
+                            m->h);
+  });
+  for (auto& L : m->layers) {
+    launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, m->h, L.attn_norm, m->eps, H, T, m->normed); });
+    if (L.conv) conv_forward_dev(c, L.conv, L.conv_state, m->normed, T, m->tmp);
+    else attn_forward_dev(c, L.attn, L.kv, m->pos, m->normed, T, m->tmp);
+    launch(c, bb::K_ELEMWISE, [&] {
+      return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, m->h, m->tmp, nullptr, 0.0f, T * H);
+    });
+    launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, m->h, L.ffn_norm, m->eps, H, T, m->normed); });
+    if (L.moe) moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr);
+    else dense_forward_dev(c, L.dense, m->normed, T, m->tmp);
+    launch(c, bb::K_ELEMWISE, [&] {
+      return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, m->h, m->tmp, nullptr, 0.0f, T * H);
+    });
+  }
+  m->pos += T;
+}
+
+void model_evict(bb_ctx* c, bb_model* m, size_t n) {
+  if (n == 0) return;
+  for (auto& L : m->layers)
+    if (L.kv) check_code(bb_kv_cache_evict_front(c, L.kv, n));
+}
+
+}  // namespace
+
+int bb_model_create(bb_ctx* c, const bb_tensor* token_embd, const float* final_norm, const bb_decoder_layer* layers,
+                    size_t n_layers, float eps, size_t kv_capacity, bb_model** out) {
+  return guard([&] {
+    need_ctx(c);
+    need(token_embd && final_norm && layers && out && n_layers > 0, BB_ERR_ARG, "null argument");
+    need(token_embd->ndims == 2, BB_ERR_SHAPE, "token_embd must be [hidden, vocab]");
+    const size_t H = token_embd->dims[0], V = token_embd->dims[1];
+    size_t be, bb_;
+    need(block_of(token_embd->dtype, be, bb_) && H % be == 0, BB_ERR_DTYPE, "unsupported token_embd dtype or shape");
+    need(kv_capacity >= 1, BB_ERR_ARG, "kv_capacity must be >= 1");
+    for (size_t i = 0; i < n_layers; ++i) {
+      const bb_decoder_layer& D = layers[i];
+      need(D.attn_norm && D.ffn_norm, BB_ERR_ARG, "layer norms must be set");
+      need((D.conv != nullptr) != (D.attn != nullptr), BB_ERR_ARG, "exactly one of conv/attn per layer");
+      need((D.moe != nullptr) != (D.dense != nullptr), BB_ERR_ARG, "exactly one of moe/dense per layer");
+      const int oh = D.conv ? D.conv->H : D.attn->H;
+      const int fh = D.moe ? D.moe->H : D.dense->H;
+      need(oh == (int)H && fh == (int)H, BB_ERR_SHAPE, "layers disagree with token_embd on the hidden size");
+      need((D.conv ? D.conv->ctx : D.attn->ctx) == c && (D.moe ? D.moe->ctx : D.dense->ctx) == c, BB_ERR_ARG,
+           "a layer belongs to another context");
+    }
+    set_device(c);
+    auto* m = new bb_model();
+    m->ctx = c;
+    m->tok_embd = token_embd;
+    m->eps = eps;
+    m->H = (int)H;
+    m->vocab = V;
+    m->row_bytes = H / be * bb_;
+    try {
+      m->final_norm = upload_f32(c, final_norm, H);
+      for (size_t i = 0; i < n_layers; ++i) {
+        const bb_decoder_layer& D = layers[i];
+        bb_model::Layer L{};
+        L.conv = D.conv;
+        L.attn = D.attn;
+        L.moe = D.moe;
+        L.dense = D.dense;
+        m->layers.push_back(L);
+        bb_model::Layer& B = m->layers.back();
+        B.attn_norm = upload_f32(c, D.attn_norm, H);
+        B.ffn_norm = upload_f32(c, D.ffn_norm, H);
+        if (D.conv) {
+          const size_t n = (size_t)(D.conv->L - 1) * H;
+          B.conv_state = static_cast<float*>(dev_alloc(n * 4));
+          clear_dev(c, B.conv_state, n * 4);
+        } else {
+          check_code(bb_kv_cache_create(c, (size_t)D.attn->NKV * D.attn->HD, kv_capacity, &B.kv));
+        }
+      }
+    } catch (...) {
+      (void)bb_model_destroy(m);
+      throw;
+    }
+    *out = m;
+  });
+}
+
+int bb_model_destroy(bb_model* m) {
+  return guard([&] {
+    if (!m) return;
+    set_device(m->ctx);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    for (auto& L : m->layers) {
+      if (L.attn_norm) (void)hipFree(L.attn_norm);
+      if (L.ffn_norm) (void)hipFree(L.ffn_norm);
+      if (L.conv_state) (void)hipFree(L.conv_state);
+      if (L.kv) (void)bb_kv_cache_destroy(L.kv);
+    }
+    for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok})
+      if (p) (void)hipFree(p);
+    delete m;
+  });
+}
+
+int bb_model_reset(bb_ctx* c, bb_model* m) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    set_device(c);
+    for (auto& L : m->layers) {
+      if (L.conv_state)
+        launch(c, bb::K_ELEMWISE, [&] { return bb::launch_zero(c->stream, L.conv_state, (size_t)(L.conv->L - 1) * m->H); });
+      if (L.kv) L.kv->n = 0;
+    }
+    m->pos = 0;
+  });
+}
+
+int bb_model_position(const bb_model* m, size_t* pos) {
+  return guard([&] {
+    need(m != nullptr && pos != nullptr, BB_ERR_ARG, "null argument");
+    *pos = m->pos;
+  });
+}
+
+int bb_model_kv_length(const bb_model* m, size_t* n) {
+  return guard([&] {
+    need(m != nullptr && n != nullptr, BB_ERR_ARG, "null argument");
+    *n = model_kv_len(m);
+  });
+}
+
+int bb_model_layer_state(bb_ctx* c, const bb_model* m, size_t layer, float* conv_state, float* k, float* v, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c && layer < m->layers.size(), BB_ERR_ARG, "bad model or layer");
+    need_loc(loc);
+    set_device(c);
+    const auto& L = m->layers[layer];
+    const hipMemcpyKind kind = loc == BB_LOC_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    if (L.conv_state && conv_state)
+      check_hip(hipMemcpyAsync(conv_state, L.conv_state, (size_t)(L.conv->L - 1) * m->H * 4, kind, c->stream), "copy");
+    if (L.kv && L.kv->n) {
+      const size_t bytes = L.kv->n * L.kv->kv_dim * 4;
+      if (k) check_hip(hipMemcpyAsync(k, L.kv->k, bytes, kind, c->stream), "copy");
+      if (v) check_hip(hipMemcpyAsync(v, L.kv->v, bytes, kind, c->stream), "copy");
+    }
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int bb_model_run_layers(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T, float* h_out, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need_loc(loc);
+    need(tokens != nullptr && T >= 1 && T <= (size_t)bb::PF_MAX_ENTRIES / 8, BB_ERR_RANGE, "T must be in 1..4096");
+    set_device(c);
+    const size_t H = m->H;
+    with_io(c, loc, {{h_out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
+      model_run_dev(c, m, model_tokens(c, m, tokens, T), T);
+      if (h_out) check_hip(hipMemcpyAsync(d[0], m->h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
+    });
+  });
+}
+
+int bb_model_forward_step(bb_ctx* c, bb_model* m, uint32_t token, float* logits, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need_loc(loc);
+    set_device(c);
+    with_io(c, loc, {{logits, m->vocab * 4, false, true}}, [&](std::vector<void*>& d) {
+      model_run_dev(c, m, model_tokens(c, m, &token, 1), 1);
+      logits_dev(c, m->tok_embd, m->final_norm, m->eps, m->h, static_cast<float*>(d[0]));
+    });
+  });
+}
+
+int bb_model_absorb(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t n, size_t max_context) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need(tokens != nullptr || n == 0, BB_ERR_ARG, "null tokens");
+    set_device(c);
+    const size_t chunk = 512;  // agent.rs:31 PREFILL_CHUNK
+    if (n == 0) return;
+    const uint32_t* dt = model_tokens(c, m, tokens, n);
+    if (model_kv_len(m) + n <= max_context) {
+      for (size_t i = 0; i < n; i += chunk) model_run_dev(c, m, dt + i, std::min(chunk, n - i));
+    } else {
+      for (size_t i = 0; i < n; ++i) {
+        model_run_dev(c, m, dt + i, 1);
+        const size_t len = model_kv_len(m);
+        if (len > max_context) model_evict(c, m, len - max_context);
+      }
+    }
+    check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int bb_model_evict_front(bb_ctx* c, bb_model* m, size_t n) {
+  return guard([&] {
+    need_ctx(c);
+    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    set_device(c);
+    model_evict(c, m, n);
   });
 }
 

@@ -66,6 +66,7 @@ enum KernelId : int {
   K_ATTN_SCORES,
   K_ATTN_PV,
   K_SOFTMAX,
+  K_EMBED,
   K_COUNT
 };
 const char* kernel_name(int id);
@@ -216,6 +217,10 @@ hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, in
 hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0, int T, int n_heads, int n_kv, int hd,
                           float* out);
 hipError_t launch_softmax(hipStream_t s, float* x, size_t n, size_t n_vec);
+hipError_t launch_zero(hipStream_t s, float* x, size_t n);
+// out [T][H] = rows tokens[t] (device) of an embedding table in F32 / F16 / Q4_K / Q6_K rows.
+hipError_t launch_embed(hipStream_t s, const uint8_t* te, int dtype, size_t row_bytes, const uint32_t* tokens, int T,
+                        int H, float* out);
 
 }  // namespace bb
 #endif

@@ -23,7 +23,7 @@ const char* kernel_name(int id) {
                                        "route_large",  "dispatch",      "gemm_gateup",  "gemm_down",
                                        "combine",      "residual_norm", "residual_route", "conv",
                                        "conv_state",   "norm_rope",     "attn_scores",  "attn_pv",
-                                       "softmax"};
+                                       "softmax",      "embed"};
   return (id >= 0 && id < K_COUNT) ? names[id] : "?";
 }
 

@@ -252,4 +252,66 @@ hipError_t launch_softmax(hipStream_t s, float* x, size_t n, size_t n_vec) {
   return hipGetLastError();
 }
 
+// ---- embedding lookup -------------------------------------------------------------------------
+// Element i of a row in the GGUF block layouts, as dequantize_into produces it (dequant.rs:75-175):
+// Q4_K (d·sc)·q - dmin·m, Q6_K (d·sc)·(q - 32), F16 widened, F32 as is.
+__device__ __forceinline__ float dequant_elem(int dtype, const uint8_t* __restrict__ row, int i) {
+  if (dtype == DT_F32) return reinterpret_cast<const float*>(row)[i];
+  if (dtype == DT_F16) return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[i]);
+  const int e = i & 255;
+  if (dtype == DT_Q4_K) {
+    const uint8_t* b = row + (size_t)(i >> 8) * 144;
+    const float d = f16_bits_to_f32(b[0] | (b[1] << 8)), dmin = f16_bits_to_f32(b[2] | (b[3] << 8));
+    const uint8_t* sc = b + 4;
+    const int chunk = e >> 6, hi = (e >> 5) & 1, l = e & 31, j = 2 * chunk + hi;
+    int s, m;
+    if (j < 4) {
+      s = sc[j] & 63;
+      m = sc[j + 4] & 63;
+    } else {
+      s = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
+      m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+    const uint8_t qb = b[16 + chunk * 32 + l];
+    const int q = hi ? (qb >> 4) : (qb & 15);
+    return (d * (float)s) * (float)q - dmin * (float)m;
+  }
+  // Q6_K
+  const uint8_t* b = row + (size_t)(i >> 8) * 210;
+  const int n = e >> 7, r = e & 127, qtr = r >> 5, l = r & 31, is = l >> 4;
+  const uint8_t* ql = b + 64 * n;
+  const uint8_t* qh = b + 128 + 32 * n;
+  const int8_t* sc = reinterpret_cast<const int8_t*>(b + 192 + 8 * n);
+  const float d = f16_bits_to_f32(b[208] | (b[209] << 8));
+  const int lo = (qtr & 1) ? ql[l + 32] : ql[l];
+  const int q = ((qtr & 2) ? (lo >> 4) : (lo & 15)) | (((qh[l] >> (2 * qtr)) & 3) << 4);
+  return d * (float)sc[is + 2 * qtr] * (float)(q - 32);
+}
+
+// out[t] = row tokens[t] of the embedding table (Model::embed_token, model.rs:390-397).
+__global__ void __launch_bounds__(256) k_embed(const uint8_t* __restrict__ te, int dtype, size_t row_bytes,
+                                               const uint32_t* __restrict__ tokens, int H, float* __restrict__ out) {
+  const int t = blockIdx.y;
+  const uint8_t* row = te + (size_t)tokens[t] * row_bytes;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < H; i += gridDim.x * 256) out[(size_t)t * H + i] = dequant_elem(dtype, row, i);
+}
+
+hipError_t launch_embed(hipStream_t s, const uint8_t* te, int dtype, size_t row_bytes, const uint32_t* tokens, int T,
+                        int H, float* out) {
+  BB_LAUNCH(k_embed, dim3((unsigned)((H + 255) / 256), T), dim3(256), 0, s, te, dtype, row_bytes, tokens, H, out);
+  return hipGetLastError();
+}
+
+// x[0..n) = 0 (a kernel rather than a memset, so that the clear can sit in a captured graph).
+__global__ void __launch_bounds__(256) k_zero(float* x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) x[i] = 0.0f;
+}
+
+hipError_t launch_zero(hipStream_t s, float* x, size_t n) {
+  if (n == 0) return hipSuccess;
+  BB_LAUNCH(k_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
 }  // namespace bb

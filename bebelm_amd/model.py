@@ -6,6 +6,7 @@ Names follow the reference so call sites read alike:
   run_layers' FFN path (model.rs:105-130)               -> FfnStack.run_layers
   Model::conv_step_op / conv_batch (model.rs:399, :190) -> ConvOp.forward
   Model::attn_step / attn_batch (model.rs:430, :222)    -> AttnOp.forward (KvCache: cache.rs)
+  Model::run_layers(_batch) / forward_step, Agent::absorb -> Model (model.rs:99-181, agent.rs:454)
 Arrays are numpy (host memory, BB_LOC_HOST) or torch CUDA tensors (device memory,
 BB_LOC_DEVICE). Everything runs on the GPU through libbebelm_moe.so; there is no other path.
 """
@@ -350,3 +351,95 @@ class AttnOp:
         check(lib().bb_attn_op_forward(self.ctx.handle, self.handle, cache.handle, pos0, _ptr(x)[0], t, _ptr(out)[0],
                                        loc))
         return out
+
+
+class Model:
+    """The decoder with its caches (Model + Cache, model.rs:25-31, cache.rs:10-19) built from a
+    bebelm_amd.synth.ModelWeights: every operator, FFN and the logits head run on the GPU."""
+
+    def __init__(self, ctx, weights, kv_capacity):
+        mw = weights
+        self.ctx, self.hidden, self.vocab = ctx, mw.hidden, mw.vocab
+        self.token_embd = Tensor(ctx, mw.embd_dtype, mw.token_embd, (mw.hidden, mw.vocab))
+        self.ops, self.ffns, self._keep = [], [], []
+        descs = (_lib.DecoderLayer * len(mw.layers))()
+        try:
+            for i, L in enumerate(mw.layers):
+                op = ConvOp(ctx, L.op) if hasattr(L.op, "conv_w") else AttnOp(ctx, L.op)
+                self.ops.append(op)
+                ffn = MoeLayer(ctx, L.ffn) if hasattr(L.ffn, "router") else DenseLayer(ctx, L.ffn)
+                self.ffns.append(ffn)
+                an = np.ascontiguousarray(L.attn_norm, np.float32)
+                fn = np.ascontiguousarray(L.ffn_norm, np.float32)
+                self._keep += [an, fn]
+                descs[i].attn_norm, descs[i].ffn_norm = an.ctypes.data, fn.ctypes.data
+                descs[i].conv = op.handle if isinstance(op, ConvOp) else None
+                descs[i].attn = op.handle if isinstance(op, AttnOp) else None
+                descs[i].moe = ffn.handle if isinstance(ffn, MoeLayer) else None
+                descs[i].dense = ffn.handle if isinstance(ffn, DenseLayer) else None
+            fin = np.ascontiguousarray(mw.final_norm, np.float32)
+            h = ctypes.c_void_p()
+            check(lib().bb_model_create(ctx.handle, self.token_embd.handle, fin.ctypes.data, descs, len(mw.layers),
+                                        mw.eps, kv_capacity, ctypes.byref(h)))
+            self.handle = h
+        except Exception:
+            self.handle = None
+            self.close()
+            raise
+
+    def close(self):
+        if getattr(self, "handle", None):
+            check(lib().bb_model_destroy(self.handle))
+            self.handle = None
+        for o in self.ops + self.ffns:
+            o.close()
+        self.ops, self.ffns = [], []
+        self.token_embd.close()
+
+    @property
+    def pos(self):
+        n = ctypes.c_size_t()
+        check(lib().bb_model_position(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def kv_len(self):
+        n = ctypes.c_size_t()
+        check(lib().bb_model_kv_length(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def reset(self):
+        check(lib().bb_model_reset(self.ctx.handle, self.handle))
+
+    def run_layers(self, tokens):
+        """run_layers / run_layers_batch: the final hidden states f32[T*hidden]."""
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(tok.size * self.hidden, np.float32)
+        check(lib().bb_model_run_layers(self.ctx.handle, self.handle, tok.ctypes.data, tok.size, out.ctypes.data,
+                                        LOC_HOST))
+        return out
+
+    def forward_step(self, token):
+        logits = np.empty(self.vocab, np.float32)
+        check(lib().bb_model_forward_step(self.ctx.handle, self.handle, int(token), logits.ctypes.data, LOC_HOST))
+        return logits
+
+    def absorb(self, tokens, max_context):
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        check(lib().bb_model_absorb(self.ctx.handle, self.handle, tok.ctypes.data, tok.size, max_context))
+
+    def evict_front(self, n):
+        check(lib().bb_model_evict_front(self.ctx.handle, self.handle, n))
+
+    def layer_state(self, layer):
+        """(conv state, k, v) of one layer; the absent ones are None."""
+        op = self.ops[layer]
+        if isinstance(op, ConvOp):
+            st = np.empty((op.l_cache - 1) * self.hidden, np.float32)
+            check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, st.ctypes.data, None, None, LOC_HOST))
+            return st, None, None
+        n = self.kv_len()
+        k = np.empty(n * op.kv_dim, np.float32)
+        v = np.empty(n * op.kv_dim, np.float32)
+        check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, None, k.ctypes.data, v.ctypes.data,
+                                         LOC_HOST))
+        return None, k, v

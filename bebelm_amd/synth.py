@@ -272,3 +272,52 @@ def stack_layers(seed=0, hidden=HIDDEN, moe_ff=MOE_FF, dense_ff=DENSE_FF, n_expe
             dd = Q4_K if layer % 2 == 0 else Q6_K
             out.append((gain, moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=dd)))
     return out
+
+
+# ---- the whole decoder (model.rs:25-31, 105-130) -------------------------------------------------
+ATTENTION_LAYERS = (2, 6, 10, 14, 18, 21)   # src/config.rs:37
+VOCAB = 128_000
+
+
+@dataclass
+class DecoderLayerWeights:
+    attn_norm: np.ndarray       # f32 [hidden]
+    ffn_norm: np.ndarray
+    op: object                  # ConvWeights | AttnWeights
+    ffn: object                 # MoeWeights | DenseWeights
+
+
+@dataclass
+class ModelWeights:
+    hidden: int
+    vocab: int
+    embd_dtype: int
+    token_embd: np.ndarray      # u8, [hidden, vocab]: vocab rows of hidden
+    final_norm: np.ndarray      # f32 [hidden]
+    layers: list
+    eps: float = RMS_EPS
+
+
+def model_weights(seed=0, hidden=HIDDEN, vocab=VOCAB, n_layers=N_LAYERS, n_dense=N_DENSE,
+                  attention_layers=ATTENTION_LAYERS, moe_ff=MOE_FF, dense_ff=DENSE_FF, n_experts=N_EXPERTS,
+                  n_heads=N_HEADS, n_kv_heads=N_KV_HEADS, embd_dtype=Q6_K):
+    """LFM2.5-8B-A1B's layer schedule at any size: attention on `attention_layers`, the gated
+    short conv elsewhere, dense FFN below n_dense, MoE above (down Q4_K on even layers, Q6_K on
+    odd); norm gains ~ 1 + N(0, 0.05)."""
+    g = rng(seed, 9100)
+    layers = []
+    for layer in range(n_layers):
+        an = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
+        fn = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
+        if layer in attention_layers:
+            op = attn_weights(seed, layer, hidden, n_heads, n_kv_heads)
+        else:
+            op = conv_weights(seed, layer, hidden, in_dtype=Q4_K, out_dtype=Q6_K if layer % 2 else Q4_K)
+        if layer < n_dense:
+            ffn = dense_weights(seed, layer, hidden, dense_ff)
+        else:
+            ffn = moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=Q4_K if layer % 2 == 0 else Q6_K)
+        layers.append(DecoderLayerWeights(an, fn, op, ffn))
+    te = quant_tensor(rng(seed, 9101), embd_dtype, hidden, vocab)
+    final = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
+    return ModelWeights(hidden, vocab, embd_dtype, te, final, layers)

@@ -55,6 +55,7 @@ typedef struct bb_stack bb_stack;
 typedef struct bb_conv_op bb_conv_op;
 typedef struct bb_attn_op bb_attn_op;
 typedef struct bb_kv_cache bb_kv_cache;
+typedef struct bb_model bb_model;
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* bb_last_error(void);
@@ -249,6 +250,47 @@ int bb_attn_op_create(bb_ctx* ctx, const bb_tensor* q, const bb_tensor* k, const
 int bb_attn_op_destroy(bb_attn_op* op);
 int bb_attn_op_forward(bb_ctx* ctx, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out,
                        int loc);
+
+/* ---- the decoder (Model, model.rs:25-31; Cache, cache.rs:10-19) ------------------------------- */
+/* One decoder layer (run_layers, model.rs:114-127): attn_norm and ffn_norm gains (host
+ * f32[hidden], copied), exactly one operator (conv or attn) and exactly one FFN (moe or dense),
+ * all created on the model's context and used in place (they must outlive the model). */
+typedef struct {
+  const float* attn_norm;
+  const float* ffn_norm;
+  bb_conv_op* conv;
+  bb_attn_op* attn;
+  bb_moe* moe;
+  bb_dense* dense;
+} bb_decoder_layer;
+/* token_embd [hidden, vocab] (embedding rows and the tied logits head), final norm gain host
+ * f32[hidden] (`token_embd_norm`), rmsnorm eps. The model owns the caches: a conv state per conv
+ * layer and a device KV cache of kv_capacity positions per attention layer, starting empty at
+ * position 0 (Cache::new). */
+int bb_model_create(bb_ctx* ctx, const bb_tensor* token_embd, const float* final_norm, const bb_decoder_layer* layers,
+                    size_t n_layers, float eps, size_t kv_capacity, bb_model** out);
+int bb_model_destroy(bb_model* m);
+/* Cache::new again: zero conv states, empty KV caches, position 0. */
+int bb_model_reset(bb_ctx* ctx, bb_model* m);
+/* cache.pos (the next token's position) and Cache::kv_len (cache.rs:32-35). */
+int bb_model_position(const bb_model* m, size_t* pos);
+int bb_model_kv_length(const bb_model* m, size_t* n);
+/* Copies layer `layer`'s caches out: its conv state (conv layers, f32[(l_cache-1)*hidden]) or its
+ * n cached keys and values (attention layers, f32[n*kv_dim] each); NULL outputs are skipped. */
+int bb_model_layer_state(bb_ctx* ctx, const bb_model* m, size_t layer, float* conv_state, float* k, float* v, int loc);
+/* Model::run_layers (model.rs:105-130) for T == 1 and run_layers_batch (model.rs:146-181) for
+ * T > 1: host token ids[T] at positions pos.., caches updated, final hidden states into h_out
+ * f32[T*hidden] (may be NULL). */
+int bb_model_run_layers(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t T, float* h_out, int loc);
+/* Model::forward_step (model.rs:99-103): run_layers for one token, then logits_from_hidden
+ * into logits f32[vocab]. */
+int bb_model_forward_step(bb_ctx* ctx, bb_model* m, uint32_t token, float* logits, int loc);
+/* Agent::absorb (agent.rs:454-465): when the whole batch fits max_context, run_layers_batch over
+ * chunks of 512 tokens (agent.rs:31); otherwise token by token, sliding the KV window down to
+ * max_context after each (Agent::trim_context, agent.rs:471-476). */
+int bb_model_absorb(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t n, size_t max_context);
+/* Cache::evict_front (cache.rs:40-50) on every attention layer. */
+int bb_model_evict_front(bb_ctx* ctx, bb_model* m, size_t n);
 
 #ifdef __cplusplus
 }

@@ -511,3 +511,79 @@ def attn_forward(w, cache, pos0, x, t):
     _chk(rc)
     cache.n = n.value
     return out
+
+
+# ---- the decoder (model.rs:99-181, agent.rs:454-476), composed from the restated pieces ----------
+
+class Model:
+    """Model + Cache over a bebelm_amd.synth.ModelWeights: the reference's forward pass with its
+    caches, each piece a call of the C restatement above (the loop order of model.rs:105-181)."""
+
+    def __init__(self, mw, kv_capacity):
+        self.mw, self.cap = mw, kv_capacity
+        self.reset()
+
+    def reset(self):
+        self.pos = 0
+        self.state = {}
+        for i, L in enumerate(self.mw.layers):
+            if hasattr(L.op, "conv_w"):
+                self.state[i] = np.zeros((L.op.l_cache - 1) * self.mw.hidden, np.float32)
+            else:
+                self.state[i] = KvCache(L.op.kv_dim, self.cap)
+
+    def kv_len(self):
+        return max([c.n for c in self.state.values() if isinstance(c, KvCache)] or [0])
+
+    def embed(self, tokens):
+        H = self.mw.hidden
+        be, bb = {12: (256, 144), 14: (256, 210), 0: (1, 4)}[self.mw.embd_dtype]
+        rb = H // be * bb
+        return np.concatenate([dequantize(self.mw.embd_dtype, self.mw.token_embd[t * rb:(t + 1) * rb], H)
+                               for t in tokens]).astype(np.float32)
+
+    def run_layers(self, tokens):
+        """run_layers (one token, model.rs:105-130) or run_layers_batch (model.rs:146-181)."""
+        t, H = len(tokens), self.mw.hidden
+        h = self.embed(tokens)
+        for i, L in enumerate(self.mw.layers):
+            normed = np.concatenate([rmsnorm(h[r * H:(r + 1) * H], L.attn_norm, self.mw.eps) for r in range(t)])
+            if hasattr(L.op, "conv_w"):
+                op, self.state[i] = conv_forward(L.op, self.state[i], normed, t)
+            else:
+                op = attn_forward(L.op, self.state[i], self.pos, normed, t)
+            h = (h + op).astype(np.float32)
+            normed = np.concatenate([rmsnorm(h[r * H:(r + 1) * H], L.ffn_norm, self.mw.eps) for r in range(t)])
+            if hasattr(L.ffn, "router"):
+                ffn = moe_ffn(L.ffn, normed) if t == 1 else moe_ffn_batch(L.ffn, normed, t)
+            else:
+                ffn = dense_ffn(L.ffn, normed, t)
+            h = (h + ffn).astype(np.float32)
+        self.pos += t
+        return h
+
+    def forward_step(self, token):
+        """model.rs:99-103: run_layers, then logits_from_hidden (model.rs:380-388)."""
+        h = self.run_layers([token])
+        normed = rmsnorm(h, self.mw.final_norm, self.mw.eps)
+        return matvec(self.mw.embd_dtype, self.mw.token_embd, self.mw.hidden, self.mw.vocab, normed)
+
+    def evict_front(self, n):
+        for c in self.state.values():
+            if isinstance(c, KvCache) and c.n >= n:
+                keep = (c.n - n) * c.kv_dim
+                c.k[:keep] = c.k[n * c.kv_dim:c.n * c.kv_dim].copy()
+                c.v[:keep] = c.v[n * c.kv_dim:c.n * c.kv_dim].copy()
+                c.n -= n
+
+    def absorb(self, tokens, max_context, chunk=512):
+        """agent.rs:454-476."""
+        if self.kv_len() + len(tokens) <= max_context:
+            for a in range(0, len(tokens), chunk):
+                self.run_layers(tokens[a:a + chunk])
+        else:
+            for tok in tokens:
+                self.run_layers([tok])
+                n = self.kv_len()
+                if n > max_context:
+                    self.evict_front(n - max_context)
