@@ -2,6 +2,9 @@
 
 Four subcommands:
 
+  python3 -m bebelm_amd.perf drive --decoder [--steps 16]
+      The whole decoder at full size: a 512-token prompt absorbed, then `steps` forward_steps.
+
   python3 -m bebelm_amd.perf drive --config 2 [--steps 50] [--layers 12]
       Runs the config's MoE layer `steps` times on cuda:0 (rotating `layers` weight sets, as
       bench.py does), then a device-to-device copy of CAL_BYTES with a known byte count. Meant
@@ -38,9 +41,34 @@ CAL_BYTES = 512 << 20
 COPY_KERNEL = "copyBuffer"
 
 
+def drive_decoder(args):
+    """The whole decoder at full size: a 512-token prompt absorbed, then `steps` forward_steps."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from bebelm_amd import synth
+    from bebelm_amd.model import Context, Model
+
+    ctx = Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    mw = synth.model_weights(seed=0)
+    m = Model(ctx, mw, 4096)
+    g = np.random.default_rng(1)
+    m.absorb(g.integers(0, mw.vocab, 512).astype(np.uint32), 4096)
+    for t in g.integers(0, mw.vocab, args.steps):
+        m.forward_step(int(t))
+    torch.cuda.synchronize()
+    m.close()
+    ctx.close()
+
+
 def drive(args):
     import torch
 
+    if args.decoder:
+        drive_decoder(args)
+        return
     sys.path.insert(0, ROOT)
     from bebelm_amd import synth
     from bebelm_amd.model import Context, MoeLayer
@@ -220,6 +248,7 @@ def main():
     d.add_argument("--config", type=int, default=2)
     d.add_argument("--steps", type=int, default=48)
     d.add_argument("--layers", type=int, default=12)
+    d.add_argument("--decoder", action="store_true", help="the whole decoder at full size instead of one MoE block")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)

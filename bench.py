@@ -21,6 +21,11 @@ The output is one JSON line with `value` in tok/s. It also carries:
                 on all cores, the same on one core, and the CPU model
   prefill       (default run only) config 4 measured in the same process the same way: tok/s,
                 ms per step, the grouped GEMMs' µs and their int8 / bf16 MFMA fractions
+  decoder       (default run only) the whole decoder at LFM2.5-8B-A1B's full shape (24 layers:
+                short conv / GQA attention operators, 2 dense + 22 MoE FFNs, the 128000-row
+                logits head): a 512-token prompt absorbed as one prefill chunk, then one-token
+                forward_steps at that context; per-kernel times of a decode step; the C++
+                restatement's forward_step timed on this host at a short context
 """
 import argparse
 import json
@@ -54,6 +59,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill object of the default run")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the whole-decoder object of the default run")
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed repetitions of the CPU baseline")
     ap.add_argument("--logits-head", action="store_true",
                     help="time bb_logits_from_hidden (rmsnorm + Q6_K 2048 -> 128000 matvec) instead of a config")
@@ -376,6 +382,70 @@ def run_config(args, ctx, config, steps, warmup, with_cpu):
     return result, steps, warmup
 
 
+def decoder_bench(args, ctx, with_cpu):
+    """The whole decoder (Model::forward_step, Agent::absorb) at full size on the GPU."""
+    import torch
+
+    from bebelm_amd import synth
+    from bebelm_amd.model import Model
+
+    mw = synth.model_weights(seed=args.seed)
+    m = Model(ctx, mw, 4096)
+    prompt = np.random.default_rng(args.seed + 1).integers(0, mw.vocab, 512).astype(np.uint32)
+
+    def prefill_once():
+        m.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.absorb(prompt, 4096)  # one chunk of 512 (agent.rs:31); returns after the stream drained
+        return time.perf_counter() - t0
+
+    prefill_once()
+    pre = sorted(prefill_once() for _ in range(3))[1]
+    # decode at a 512-token context: the one-token step with its logits back on the host
+    n_dec = 32
+    toks = np.random.default_rng(args.seed + 2).integers(0, mw.vocab, n_dec + 4)
+    for t in toks[:4]:
+        m.forward_step(int(t))
+    t0 = time.perf_counter()
+    for t in toks[4:]:
+        m.forward_step(int(t))
+    dec = (time.perf_counter() - t0) / n_dec
+    # per-kernel times of decode steps (events stamped by each dispatch)
+    ctx.reset_stats()
+    ctx.profile(True)
+    for t in toks[:8]:
+        m.forward_step(int(t))
+    stats = ctx.kernel_stats()
+    ctx.profile(False)
+    total = sum(v[0] for v in stats.values()) or 1.0
+    per_step = {k: round(v[0] / 8 * 1e3, 1) for k, v in sorted(stats.items(), key=lambda kv: -kv[1][0]) if v[1]}
+    out = {
+        "workload": "LFM2.5-8B-A1B shape: 24 layers (6 GQA attention, 18 short conv), 2 dense + 22 MoE FFNs, "
+                    "vocab 128000, Q4_K/Q6_K synthetic weights",
+        "prefill_512": {"ms": round(pre * 1e3, 2), "tok_s": round(512 / pre, 1)},
+        "decode_t1_ctx512": {"ms_per_token": round(dec * 1e3, 3), "tok_s": round(1.0 / dec, 1),
+                             "includes": "host call, logits copied back to the host"},
+        "decode_kernel_us_per_step": per_step,
+        "decode_kernel_ms_per_step": round(total / 8, 3),
+    }
+    m.close()
+    if with_cpu:
+        from oracle import bbo
+
+        om = bbo.Model(mw, 64)
+        om.absorb(list(prompt[:16]), 64)
+        t0 = time.perf_counter()
+        reps = 3
+        for t in toks[:reps]:
+            om.forward_step(int(t))
+        cpu = (time.perf_counter() - t0) / reps
+        out["cpu_baseline"] = {"value": round(1.0 / cpu, 2), "unit": "tok/s", "cores": bbo.get_threads(),
+                               "kind": "port", "sample": f"{reps} forward_steps of the C++ restatement (Python "
+                               "composition of its operators) at a 16-token context"}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -431,6 +501,8 @@ def main():
             "kernel_us": p["kernel_us"], "roofline": p["roofline"], "cpu_baseline": p["cpu_baseline"],
             "mean_hit_experts": p["mean_hit_experts"],
         }
+    if args.config == 2 and not args.no_decoder:
+        result["decoder"] = decoder_bench(args, ctx, not args.no_cpu)
     ctx.close()
     print(json.dumps(result), flush=True)
 
