@@ -159,7 +159,12 @@ def stats(args):
     sys.path.insert(0, ROOT)
     from bebelm_amd import synth
 
-    cfg = synth.CONFIGS[args.config]
+    if args.decoder:
+        wname, title = "decoder_full", ("the whole decoder at LFM2.5-8B-A1B's shape (24 layers, 128000-row "
+                                       "logits head): a 512-token prompt absorbed, then one-token forward_steps")
+    else:
+        cfg = synth.CONFIGS[args.config]
+        wname, title = cfg.name, f"config {args.config} ({cfg.name}): {cfg.description}"
     rows = []
     with open(args.csv) as f:
         for row in csv.DictReader(f):
@@ -167,17 +172,17 @@ def stats(args):
             rows.append((name, int(row["Calls"]), float(row["AverageNs"]) / 1e3, float(row["MinNs"]) / 1e3,
                          float(row["MaxNs"]) / 1e3, float(row["Percentage"])))
     bench = None
-    with open(args.bench) as f:
-        for line in f:
-            line = line.strip()
-            if line.startswith("{"):
-                bench = json.loads(line)
+    if args.bench:
+        with open(args.bench) as f:
+            for line in f:
+                line = line.strip()
+                if line.startswith("{"):
+                    bench = json.loads(line)
     keep = ("value", "unit", "ms_per_step", "kernel_us", "roofline")
-    out = [f"# Kernel statistics — config {args.config} ({cfg.name}): {cfg.description}", "",
+    out = [f"# Kernel statistics — {title}", "",
            "Command (from the repository root on one MI355X; `cd /tmp && export TMPDIR=/tmp` first for "
            "rocprofv3's scratch files):", "", "```", args.command, "```", "",
-           "Per-kernel durations over every launch of that run (bench.py's timed pass and its event-timed "
-           "pass):", "",
+           "Per-kernel durations over every launch of that run:", "",
            "| kernel | calls | mean µs | min µs | max µs | share |", "|---|---|---|---|---|---|"]
     for name, calls, avg, mn, mx, pct in rows:
         out.append(f"| `{name}` | {calls} | {avg:.2f} | {mn:.2f} | {mx:.2f} | {pct:.1f}% |")
@@ -185,7 +190,9 @@ def stats(args):
         out += ["", "The bench line (HIP events stamped by each kernel's dispatch, mean µs per launch) of the "
                 "same workload without the profiler:", "", "```", args.bench_command, "```", "", "```",
                 json.dumps({k: bench[k] for k in keep if k in bench}), "```"]
-    path = os.path.join(ROOT, "profiles", f"kernel_stats_{cfg.name}.md")
+    if args.note:
+        out += ["", args.note]
+    path = os.path.join(ROOT, "profiles", f"kernel_stats_{wname}.md")
     with open(path, "w") as f:
         f.write("\n".join(out) + "\n")
     print(path)
@@ -259,10 +266,12 @@ def main():
     t.add_argument("--command-write", default=None)
     st = sub.add_parser("stats")
     st.add_argument("--csv", required=True)
-    st.add_argument("--bench", required=True)
+    st.add_argument("--bench", default=None)
     st.add_argument("--config", type=int, default=2)
+    st.add_argument("--decoder", action="store_true")
     st.add_argument("--command", required=True)
-    st.add_argument("--bench-command", required=True)
+    st.add_argument("--bench-command", default=None)
+    st.add_argument("--note", default=None)
     pm = sub.add_parser("pmc")
     pm.add_argument("--csv", nargs="+", required=True)
     pm.add_argument("--commands", nargs="+", required=True)
