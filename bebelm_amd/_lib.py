@@ -11,7 +11,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libbebelm_moe.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "bebelm_moe.h")
 
-BB_OK, BB_ERR_ARG, BB_ERR_DTYPE, BB_ERR_SHAPE, BB_ERR_HIP, BB_ERR_OOM, BB_ERR_RANGE = range(7)
+(BB_OK, BB_ERR_ARG, BB_ERR_DTYPE, BB_ERR_SHAPE, BB_ERR_HIP, BB_ERR_OOM, BB_ERR_RANGE, BB_ERR_FORMAT, BB_ERR_IO,
+ BB_ERR_MISSING) = range(10)
 LOC_HOST, LOC_DEVICE = 0, 1
 
 c_void_p = ctypes.c_void_p
@@ -45,6 +46,12 @@ class LayerDesc(ctypes.Structure):
 class DecoderLayer(ctypes.Structure):
     _fields_ = [("attn_norm", c_void_p), ("ffn_norm", c_void_p), ("conv", c_void_p), ("attn", c_void_p),
                 ("moe", c_void_p), ("dense", c_void_p)]
+
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", c_uint32), ("dims", P(ctypes.c_uint64)),
+                ("ggml_type", c_uint32), ("offset", ctypes.c_uint64), ("data_start", ctypes.c_uint64),
+                ("data_len", ctypes.c_uint64)]
 
 
 _SIGS = {
@@ -114,6 +121,25 @@ _SIGS = {
     "bb_model_forward_step": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_int]),
     "bb_model_absorb": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
     "bb_model_evict_front": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "bb_gguf_open": (c_int, [ctypes.c_char_p, P(c_void_p)]),
+    "bb_gguf_open_bytes": (c_int, [c_void_p, c_size_t, P(c_void_p)]),
+    "bb_gguf_close": (c_int, [c_void_p]),
+    "bb_gguf_header": (c_int, [c_void_p, P(c_uint32), P(ctypes.c_uint64), P(ctypes.c_uint64), P(c_size_t),
+                               P(c_size_t)]),
+    "bb_gguf_tensor": (c_int, [c_void_p, c_size_t, P(GgufTensorInfo)]),
+    "bb_gguf_find_tensor": (c_int, [c_void_p, ctypes.c_char_p, P(c_size_t)]),
+    "bb_gguf_tensor_data": (c_int, [c_void_p, c_size_t, P(c_void_p), P(c_size_t)]),
+    "bb_gguf_meta_key": (c_int, [c_void_p, c_size_t, P(ctypes.c_char_p)]),
+    "bb_gguf_meta_type": (c_int, [c_void_p, ctypes.c_char_p, P(c_uint32), P(c_uint32), P(c_size_t)]),
+    "bb_gguf_get_u32": (c_int, [c_void_p, ctypes.c_char_p, P(c_uint32)]),
+    "bb_gguf_get_f32": (c_int, [c_void_p, ctypes.c_char_p, P(c_float)]),
+    "bb_gguf_get_str": (c_int, [c_void_p, ctypes.c_char_p, P(c_void_p), P(c_size_t)]),
+    "bb_gguf_get_u32_array": (c_int, [c_void_p, ctypes.c_char_p, P(c_uint32), c_size_t, P(c_size_t)]),
+    "bb_gguf_get_str_item": (c_int, [c_void_p, ctypes.c_char_p, c_size_t, P(c_void_p), P(c_size_t)]),
+    "bb_gguf_validate": (c_int, [c_void_p]),
+    "bb_gguf_check_tensors": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_gguf_upload": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
+    "bb_model_load": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
 }
 
 _lib = None

@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbebelm_moe.so")
-SOURCES = ["bb_kernels.hip", "bb_decode.hip", "bb_prefill.hip", "bb_ops.hip", "bb_api.hip"]
+SOURCES = ["bb_kernels.hip", "bb_decode.hip", "bb_prefill.hip", "bb_ops.hip", "bb_api.hip", "bb_gguf.hip"]
 ARCH = os.environ.get("BB_OFFLOAD_ARCH", "gfx950")
 
 

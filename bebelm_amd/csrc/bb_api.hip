@@ -80,6 +80,8 @@ void* dev_alloc(size_t bytes) {
 
 }  // namespace
 
+void bb::set_last_error(const std::string& msg) { g_err = msg; }
+
 // Workspace of bb_moe_forward_noalloc: a fixed area in the code object's static device memory,
 // one copy per GPU, held until the process ends. Host code never uses the name `scratch` as an
 // address (on the host it only names the symbol): each device's address comes from
@@ -713,7 +715,19 @@ struct bb_model {
   float *h = nullptr, *normed = nullptr, *tmp = nullptr;
   uint32_t* tok = nullptr;  // token ids of the current call
   size_t cap_T = 0, tok_cap = 0;
+  bb::ModelOwned owned;  // set by bb_model_load
 };
+
+void bb::free_owned(bb::ModelOwned& o) {
+  for (bb_conv_op* p : o.conv) (void)bb_conv_op_destroy(p);
+  for (bb_attn_op* p : o.attn) (void)bb_attn_op_destroy(p);
+  for (bb_moe* p : o.moe) (void)bb_moe_destroy(p);
+  for (bb_dense* p : o.dense) (void)bb_dense_destroy(p);
+  for (bb_tensor* p : o.tensors) (void)bb_tensor_free(p);
+  o = bb::ModelOwned();
+}
+
+void bb::model_adopt(bb_model* m, bb::ModelOwned&& o) { m->owned = std::move(o); }
 
 namespace {
 
@@ -1855,6 +1869,7 @@ int bb_model_destroy(bb_model* m) {
     }
     for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok})
       if (p) (void)hipFree(p);
+    bb::free_owned(m->owned);
     delete m;
   });
 }

@@ -6,7 +6,27 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+#include <vector>
+
+#include "../../include/bebelm_moe.h"
+
 namespace bb {
+
+// Sets the calling thread's bb_last_error message (for entry points outside bb_api.hip).
+void set_last_error(const std::string& msg);
+
+// What bb_model_load created for a model: bb_model_destroy frees these after the model itself,
+// operators and FFNs before the tensors they read.
+struct ModelOwned {
+  std::vector<bb_conv_op*> conv;
+  std::vector<bb_attn_op*> attn;
+  std::vector<bb_moe*> moe;
+  std::vector<bb_dense*> dense;
+  std::vector<bb_tensor*> tensors;
+};
+void free_owned(ModelOwned& o);
+void model_adopt(bb_model* m, ModelOwned&& o);
 
 // Profiling: when set, kernels are launched with hipExtLaunchKernelGGL, which has the kernel's
 // own dispatch stamp the two events (exact start and end, no queue gaps in between).

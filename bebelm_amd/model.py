@@ -362,6 +362,9 @@ class Model:
         self.ctx, self.hidden, self.vocab = ctx, mw.hidden, mw.vocab
         self.token_embd = Tensor(ctx, mw.embd_dtype, mw.token_embd, (mw.hidden, mw.vocab))
         self.ops, self.ffns, self._keep = [], [], []
+        # per layer: ("conv", conv state floats) or ("attn", kv_dim)
+        self.layer_kinds = [("conv", (L.op.l_cache - 1) * mw.hidden) if hasattr(L.op, "conv_w")
+                            else ("attn", L.op.n_kv_heads * L.op.head_dim) for L in mw.layers]
         descs = (_lib.DecoderLayer * len(mw.layers))()
         try:
             for i, L in enumerate(mw.layers):
@@ -387,6 +390,34 @@ class Model:
             self.close()
             raise
 
+    @classmethod
+    def load(cls, ctx, gguf, kv_capacity, validate=True):
+        """Model::load (model.rs:36-50) from a GGUF (a path or an open gguf.GgufFile): with
+        `validate`, config::validate first (the LFM2.5-8B-A1B constants); then the tensor-table
+        check and the upload of every tensor into HBM (bb_model_load). The model owns its weights."""
+        from .gguf import GgufFile
+        own = not isinstance(gguf, GgufFile)
+        g = GgufFile.open(gguf) if own else gguf
+        try:
+            if validate:
+                g.validate()
+            g.check_tensors()
+            h = ctypes.c_void_p()
+            check(lib().bb_model_load(ctx.handle, g.handle, kv_capacity, ctypes.byref(h)))
+            self = cls.__new__(cls)
+            self.ctx, self.handle = ctx, h
+            arch = g.architecture() + "."
+            self.hidden, self.vocab = g.get_u32(arch + "embedding_length"), g.get_u32(arch + "vocab_size")
+            head_dim = self.hidden // g.get_u32(arch + "attention.head_count")
+            l_cache = g.get_u32(arch + "shortconv.l_cache")
+            self.layer_kinds = [("attn", kv * head_dim) if kv else ("conv", (l_cache - 1) * self.hidden)
+                                for kv in g.get_u32_array(arch + "attention.head_count_kv")]
+            self.ops, self.ffns, self._keep, self.token_embd = [], [], [], None
+            return self
+        finally:
+            if own:
+                g.close()
+
     def close(self):
         if getattr(self, "handle", None):
             check(lib().bb_model_destroy(self.handle))
@@ -394,7 +425,8 @@ class Model:
         for o in self.ops + self.ffns:
             o.close()
         self.ops, self.ffns = [], []
-        self.token_embd.close()
+        if self.token_embd is not None:
+            self.token_embd.close()
 
     @property
     def pos(self):
@@ -432,14 +464,14 @@ class Model:
 
     def layer_state(self, layer):
         """(conv state, k, v) of one layer; the absent ones are None."""
-        op = self.ops[layer]
-        if isinstance(op, ConvOp):
-            st = np.empty((op.l_cache - 1) * self.hidden, np.float32)
+        kind, size = self.layer_kinds[layer]
+        if kind == "conv":
+            st = np.empty(size, np.float32)
             check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, st.ctypes.data, None, None, LOC_HOST))
             return st, None, None
         n = self.kv_len()
-        k = np.empty(n * op.kv_dim, np.float32)
-        v = np.empty(n * op.kv_dim, np.float32)
+        k = np.empty(n * size, np.float32)
+        v = np.empty(n * size, np.float32)
         check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, None, k.ctypes.data, v.ctypes.data,
                                          LOC_HOST))
         return None, k, v

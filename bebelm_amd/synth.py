@@ -321,3 +321,64 @@ def model_weights(seed=0, hidden=HIDDEN, vocab=VOCAB, n_layers=N_LAYERS, n_dense
     te = quant_tensor(rng(seed, 9101), embd_dtype, hidden, vocab)
     final = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
     return ModelWeights(hidden, vocab, embd_dtype, te, final, layers)
+
+
+def model_gguf(mw, arch="lfm2moe", head_count_kv_type=None):
+    """A GgufWriter holding `mw` as LFM2.5-8B-A1B's GGUF names it (model.rs:619-660: tensor names
+    and [in, out] dims) with the lfm2moe.* metadata config::validate reads (config.rs:51-89).
+    head_count_kv_type: the array's element type (default U32)."""
+    from . import gguf as G
+    w = G.GgufWriter()
+    ops = [L.op for L in mw.layers]
+    att = [op for op in ops if hasattr(op, "n_heads")]
+    conv = [op for op in ops if hasattr(op, "conv_w")]
+    moe = [L.ffn for L in mw.layers if hasattr(L.ffn, "router")]
+    dense = [L.ffn for L in mw.layers if not hasattr(L.ffn, "router")]
+    n_dense = sum(1 for _ in dense)
+    p = arch + "."
+    w.add("general.architecture", G.STRING, arch)
+    for key, v in (("block_count", len(mw.layers)), ("embedding_length", mw.hidden), ("vocab_size", mw.vocab),
+                   ("attention.head_count", att[0].n_heads if att else N_HEADS),
+                   ("expert_count", moe[0].n_experts if moe else 0), ("expert_used_count", moe[0].n_used if moe else 0),
+                   ("feed_forward_length", dense[0].ff if dense else 0),
+                   ("expert_feed_forward_length", moe[0].moe_ff if moe else 0),
+                   ("leading_dense_block_count", n_dense),
+                   ("shortconv.l_cache", conv[0].l_cache if conv else CONV_L_CACHE)):
+        w.add(p + key, G.U32, int(v))
+    w.add(p + "rope.freq_base", G.F32, float(att[0].freq_base if att else ROPE_THETA))
+    w.add(p + "attention.layer_norm_rms_epsilon", G.F32, float(mw.eps))
+    kv = [op.n_kv_heads if hasattr(op, "n_heads") else 0 for op in ops]
+    w.add(p + "attention.head_count_kv", G.ARRAY, (head_count_kv_type or G.U32, kv))
+
+    h = mw.hidden
+    w.add_tensor("token_embd.weight", (h, mw.vocab), mw.embd_dtype, mw.token_embd)
+    w.add_tensor("token_embd_norm.weight", (h,), F32, mw.final_norm.astype(np.float32))
+    for i, L in enumerate(mw.layers):
+        b = f"blk.{i}."
+        w.add_tensor(b + "attn_norm.weight", (h,), F32, L.attn_norm.astype(np.float32))
+        w.add_tensor(b + "ffn_norm.weight", (h,), F32, L.ffn_norm.astype(np.float32))
+        op = L.op
+        if hasattr(op, "n_heads"):
+            qd, kvd = op.n_heads * op.head_dim, op.n_kv_heads * op.head_dim
+            w.add_tensor(b + "attn_q.weight", (h, qd), op.q_dtype, op.q)
+            w.add_tensor(b + "attn_k.weight", (h, kvd), op.k_dtype, op.k)
+            w.add_tensor(b + "attn_v.weight", (h, kvd), op.v_dtype, op.v)
+            w.add_tensor(b + "attn_output.weight", (qd, h), op.o_dtype, op.o)
+            w.add_tensor(b + "attn_q_norm.weight", (op.head_dim,), F32, op.q_norm.astype(np.float32))
+            w.add_tensor(b + "attn_k_norm.weight", (op.head_dim,), F32, op.k_norm.astype(np.float32))
+        else:
+            w.add_tensor(b + "shortconv.in_proj.weight", (h, 3 * h), op.in_dtype, op.in_proj)
+            w.add_tensor(b + "shortconv.conv.weight", (op.l_cache, h), F32, op.conv_w.astype(np.float32))
+            w.add_tensor(b + "shortconv.out_proj.weight", (h, h), op.out_dtype, op.out_proj)
+        f = L.ffn
+        if hasattr(f, "router"):
+            w.add_tensor(b + "ffn_gate_inp.weight", (h, f.n_experts), F32, f.router.astype(np.float32))
+            w.add_tensor(b + "exp_probs_b.bias", (f.n_experts,), F32, f.exp_probs_b.astype(np.float32))
+            w.add_tensor(b + "ffn_gate_exps.weight", (h, f.moe_ff, f.n_experts), f.gate_dtype, f.gate_exps)
+            w.add_tensor(b + "ffn_up_exps.weight", (h, f.moe_ff, f.n_experts), f.up_dtype, f.up_exps)
+            w.add_tensor(b + "ffn_down_exps.weight", (f.moe_ff, h, f.n_experts), f.down_dtype, f.down_exps)
+        else:
+            w.add_tensor(b + "ffn_gate.weight", (h, f.ff), f.gate_dtype, f.gate)
+            w.add_tensor(b + "ffn_up.weight", (h, f.ff), f.up_dtype, f.up)
+            w.add_tensor(b + "ffn_down.weight", (f.ff, h), f.down_dtype, f.down)
+    return w

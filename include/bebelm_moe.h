@@ -41,7 +41,10 @@ enum bb_status {
   BB_ERR_SHAPE = 3,  /* sizes inconsistent (byte_size mismatch, n_in % block != 0)   */
   BB_ERR_HIP = 4,    /* a HIP runtime call failed                                     */
   BB_ERR_OOM = 5,    /* device allocation failed                                      */
-  BB_ERR_RANGE = 6   /* size beyond what this build supports                          */
+  BB_ERR_RANGE = 6,  /* size beyond what this build supports                          */
+  BB_ERR_FORMAT = 7, /* malformed GGUF, or metadata / tensor table not what is expected */
+  BB_ERR_IO = 8,     /* a file could not be opened or mapped                           */
+  BB_ERR_MISSING = 9 /* metadata key or tensor absent, or of another value type        */
 };
 
 enum bb_dtype { BB_F32 = 0, BB_F16 = 1, BB_Q4_K = 12, BB_Q6_K = 14 };
@@ -56,6 +59,7 @@ typedef struct bb_conv_op bb_conv_op;
 typedef struct bb_attn_op bb_attn_op;
 typedef struct bb_kv_cache bb_kv_cache;
 typedef struct bb_model bb_model;
+typedef struct bb_gguf bb_gguf;
 
 /* Message for the last failed call on this thread ("" if none). */
 const char* bb_last_error(void);
@@ -291,6 +295,75 @@ int bb_model_forward_step(bb_ctx* ctx, bb_model* m, uint32_t token, float* logit
 int bb_model_absorb(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t n, size_t max_context);
 /* Cache::evict_front (cache.rs:40-50) on every attention layer. */
 int bb_model_evict_front(bb_ctx* ctx, bb_model* m, size_t n);
+
+/* ---- GGUF files (gguf.rs, config.rs:51-89, model.rs:36-50, :572-584, :619-660) ---------------- */
+/* GgufFile::open (gguf.rs:171-177): maps the file read-only and parses the header, the metadata
+ * and the tensor table. Errors as gguf.rs:22-55 (bad magic, version other than 2 or 3, a read
+ * past the end, an unknown value type, a string that is not UTF-8, a tensor of an unmodelled
+ * ggml type or whose data falls outside the file): BB_ERR_FORMAT with the reference's message;
+ * an open or map failure: BB_ERR_IO. */
+int bb_gguf_open(const char* path, bb_gguf** out);
+/* GgufFile::from_bytes (gguf.rs:181-184): the same parse over a copy of n in-memory bytes. */
+int bb_gguf_open_bytes(const void* bytes, size_t n, bb_gguf** out);
+int bb_gguf_close(bb_gguf* g);
+/* version, alignment, data_offset (gguf.rs:152-160) and the table sizes. Any pointer may be NULL. */
+int bb_gguf_header(const bb_gguf* g, uint32_t* version, uint64_t* alignment, uint64_t* data_offset,
+                   size_t* n_tensors, size_t* n_metadata);
+
+/* TensorInfo (gguf.rs:123-140); name and dims point into the bb_gguf and live as long as it. */
+typedef struct {
+  const char* name;
+  uint32_t n_dims;
+  const uint64_t* dims;       /* GGUF order, fastest-varying first */
+  uint32_t ggml_type;
+  uint64_t offset;            /* relative to the tensor-data section */
+  uint64_t data_start;        /* absolute file offset */
+  uint64_t data_len;          /* GgmlType::byte_size of the element count (tensor.rs:99-105) */
+} bb_gguf_tensor_info;
+int bb_gguf_tensor(const bb_gguf* g, size_t index, bb_gguf_tensor_info* info);
+/* Model::tensor's name lookup (model.rs:80-82): BB_ERR_MISSING when absent. */
+int bb_gguf_find_tensor(const bb_gguf* g, const char* name, size_t* index);
+/* tensor_data (gguf.rs:191-193): zero-copy view of the tensor's bytes in the mapping. */
+int bb_gguf_tensor_data(const bb_gguf* g, size_t index, const void** data, size_t* nbytes);
+
+/* Metadata (gguf.rs:195-266). Every accessor returns BB_ERR_MISSING when the key is absent or
+ * its value has another type, as the reference's Option-returning getters give None.
+ * bb_gguf_meta_key enumerates the keys in file order (a key repeated in the file keeps the
+ * last value, as the reference's HashMap insert does). bb_gguf_meta_type gives the value type
+ * (gguf.rs:61-75 codes), and for arrays the element type and length (else 0 and 0). */
+int bb_gguf_meta_key(const bb_gguf* g, size_t index, const char** key);
+int bb_gguf_meta_type(const bb_gguf* g, const char* key, uint32_t* value_type, uint32_t* elem_type, size_t* n_items);
+/* get_u32 (gguf.rs:200-212): any integer type, converted as Rust's `as u32`. */
+int bb_gguf_get_u32(const bb_gguf* g, const char* key, uint32_t* value);
+/* get_f32 (gguf.rs:250-256): F32, or F64 rounded to f32. */
+int bb_gguf_get_f32(const bb_gguf* g, const char* key, float* value);
+/* get_str (gguf.rs:258-263): a pointer into the bb_gguf (not NUL-terminated) and its length. */
+int bb_gguf_get_str(const bb_gguf* g, const char* key, const char** str, size_t* len);
+/* get_u32_array (gguf.rs:215-233): *n_items = the array length; up to `cap` values written.
+ * BB_ERR_MISSING when an item is not an integer. */
+int bb_gguf_get_u32_array(const bb_gguf* g, const char* key, uint32_t* out, size_t cap, size_t* n_items);
+/* get_str_array (gguf.rs:236-248), one item at a time: item `index` of a string array. */
+int bb_gguf_get_str_item(const bb_gguf* g, const char* key, size_t index, const char** str, size_t* len);
+
+/* config::validate (config.rs:51-89): the file is LFM2.5-8B-A1B (architecture "lfm2moe", its
+ * sizes, RoPE base, rmsnorm eps and conv/attention schedule). BB_ERR_FORMAT with the
+ * reference's message on the first mismatch, BB_ERR_MISSING for an absent key. */
+int bb_gguf_validate(const bb_gguf* g);
+/* Model::check_tensors (model.rs:572-584) against expected_tensors (model.rs:619-660), the list
+ * derived from the file's own lfm2moe.* sizes and schedule (equal to the reference's hardcoded
+ * list for a file that passes bb_gguf_validate). *n_expected (may be NULL) = the list's length. */
+int bb_gguf_check_tensors(const bb_gguf* g, size_t* n_expected);
+/* One tensor into HBM (what bb_tensor_upload does with tensor_data's bytes and the table's
+ * dims and dtype). */
+int bb_gguf_upload(bb_ctx* ctx, const bb_gguf* g, size_t index, bb_tensor** out);
+/* Model::load (model.rs:36-50) after the open: check_tensors, then every tensor the forward
+ * pass reads uploaded to HBM, the operators, FFNs and the decoder built from them with the
+ * file's sizes (hidden, heads and kv heads per layer, expert counts, conv length, RoPE base,
+ * eps; the small F32 tensors read as precompute_f32 reads them, :54-67) and caches of
+ * kv_capacity positions. The returned model owns all of it: bb_model_destroy frees it. The
+ * bb_gguf may be closed once this returns. Call bb_gguf_validate first to also pin the
+ * LFM2.5-8B-A1B constants, as Model::load does. */
+int bb_model_load(bb_ctx* ctx, const bb_gguf* g, size_t kv_capacity, bb_model** out);
 
 #ifdef __cplusplus
 }
