@@ -145,6 +145,7 @@ struct bb_dense {
   bb_ctx* ctx;
   const bb_tensor *gate, *up, *down;
   int H, F;
+  bb::PackedW gu, dn;  // gate/up interleaved and down in the grouped GEMM's layout (batches)
 };
 
 struct bb_stack {
@@ -210,6 +211,26 @@ void launch(bb_ctx* c, int id, F&& f) {
   bb::launch_events() = {};
   check_hip(rc, bb::kernel_name(id));
   c->pending.push_back({id, a, b});
+}
+
+// The one-group route of T tokens for the grouped GEMM (counts, offsets, identity permutation),
+// written into a carved buffer of T + 8 ints.
+bb::RouteBufs one_group(bb_ctx* c, int32_t* grp, size_t T) {
+  bb::RouteBufs rb{};
+  rb.counts = grp;
+  rb.offsets = grp + 2;
+  rb.perm = grp + 8;
+  launch(c, bb::K_DISPATCH, [&] { return bb::launch_one_group(c->stream, (int)T, rb); });
+  return rb;
+}
+
+// y = W·x on the grouped GEMM for a packed W (p: plain 64-row tiles), x's Q8 rows in q.
+void packed_project(bb_ctx* c, const bb::PackedW& p, size_t n_in, size_t n_out, size_t T, bb::Q8Bufs q,
+                    const bb::RouteBufs& rb, float* y) {
+  launch(c, bb::K_GEMM_DOWN, [&] {
+    return bb::launch_gemm_down(c->stream, p.dt, p.w, p.stride, (int)T, (int)n_out, (int)n_in, 1, 1, rb,
+                                bb::GemmX{q.q, q.scales}, y);
+  });
 }
 
 void collect(bb_ctx* c) {
@@ -461,12 +482,25 @@ void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* 
     float* gate = cv.take<float>(T * F);
     float* up = cv.take<float>(T * F);
     bb::Q8Bufs aq{cv.take<int8_t>(T * F), cv.take<float>(T * F / 256), cv.take<int32_t>(T * F / 32)};
+    int32_t* grp = cv.take<int32_t>(T + 8);
     if (pass == 0) {
       base = ensure_ws(c, cv.off);
       continue;
     }
     const int nz = T == 1;  // n_tokens == 1 takes matvec (-0.0-started sum), else matmul
     launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
+    if (T >= bb::PROJ_GEMM_MIN_T && d->gu.w && d->dn.w) {
+      // a batch: gate, up and swiglu, then down, as grouped GEMMs of one group (matmul's sums
+      // from +0.0, the same per-(row, token) values as the row kernels)
+      const bb::RouteBufs rb = one_group(c, grp, T);
+      launch(c, bb::K_GEMM_GATEUP, [&] {
+        return bb::launch_gemm_gateup(c->stream, d->gu.dt, d->gu.w, d->gu.stride, (int)T, (int)H, (int)F, 1, 1, rb,
+                                      bb::GemmX{xq.q, xq.scales}, gate);
+      });
+      launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, gate, T, (int)F, aq.q, aq.scales); });
+      packed_project(c, d->dn, F, H, T, aq, rb, out);
+      continue;
+    }
     const size_t gate_rb = (H / 256) * (d->gate->dtype == BB_Q4_K ? 144 : 210);
     if (d->gate->dtype == d->up->dtype && H / 256 <= 64) {
       // gate, up and swiglu in one pass over both matrices
@@ -581,10 +615,17 @@ bb::Q8Bufs carve_q8(Carve& cv, size_t T, size_t n_in) {
 // y = W·x for T token-major rows as the reference's operators call it: matvec1 for one token
 // (model.rs:557-560), matmul1 for a batch (:372-375); both are the row kernels (the one-token
 // form sums from -0.0 as matvec does). q: Q8 buffers for x when W is Q4_K / Q6_K.
-void project_dev(bb_ctx* c, const bb_tensor* w, size_t n_in, size_t n_out, const float* x, size_t T, float* y,
-                 bb::Q8Bufs q) {
+// With a packed form and a one-group route (rb non-null: batches of PROJ_GEMM_MIN_T tokens and
+// more) the batch runs on the grouped GEMM instead.
+void project_dev(bb_ctx* c, const bb_tensor* w, const bb::PackedW& pk, const bb::RouteBufs* rb, size_t n_in,
+                 size_t n_out, const float* x, size_t T, float* y, bb::Q8Bufs q) {
   size_t row_bytes;
   check_weight_range(w, w->dtype, 0, n_in, n_out, row_bytes);
+  if (pk.w && rb) {
+    launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, x, T, (int)n_in, q.q, q.scales); });
+    packed_project(c, pk, n_in, n_out, T, q, *rb, y);
+    return;
+  }
   if (w->dtype == BB_Q4_K || w->dtype == BB_Q6_K) {
     launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, n_in, q); });
     launch(c, bb::K_ROWS_Q8, [&] {
@@ -614,6 +655,33 @@ float* upload_f32(bb_ctx* c, const float* host, size_t n) {
     throw;
   }
   return d;
+}
+
+// The grouped GEMM's packed form of a projection (one expert): plain 64-row tiles of w, or gate
+// and up interleaved (up != null). Empty (w null) when the dtype or shape has no packed form.
+bb::PackedW pack_weights(bb_ctx* c, const bb_tensor* w, const bb_tensor* up, size_t n_in, size_t n_out) {
+  bb::PackedW p;
+  const uint32_t dt = w->dtype;
+  if (dt != BB_Q4_K && dt != BB_Q6_K) return p;
+  if (up && up->dtype != dt) return p;
+  if (n_in % 256 != 0 || n_out % (up ? 64 : 128) != 0) return p;
+  const size_t nb = n_in / 256, row_bytes = nb * (dt == BB_Q4_K ? 144 : 210);
+  p.dt = (int)dt;
+  p.stride = (up ? n_out / 32 : n_out / 64) * nb * bb::pack_tile_block_bytes((int)dt);
+  p.w = static_cast<uint8_t*>(dev_alloc(p.stride));
+  const hipError_t e = bb::launch_pack_rows(c->stream, (int)dt, w->dev, up ? up->dev : nullptr, n_out * row_bytes,
+                                            up ? n_out * row_bytes : 0, (int)n_out, (int)nb, 1, p.w);
+  const hipError_t e2 = e == hipSuccess ? hipStreamSynchronize(c->stream) : e;
+  if (e2 != hipSuccess) {
+    (void)hipFree(p.w);
+    check_hip(e2, "weight packing");
+  }
+  return p;
+}
+
+void free_packed(bb::PackedW& p) {
+  if (p.w) (void)hipFree(p.w);
+  p = bb::PackedW();
 }
 
 // (cos, sin) of RoPE pair i at `pos` as rope.rs:17-30 computes them: theta from (float)pos,
@@ -672,6 +740,7 @@ struct bb_conv_op {
   const bb_tensor* out_proj;
   float* conv_w;  // device, [hidden][l_cache]
   int H, L;
+  bb::PackedW in_p, out_p;  // the projections in the grouped GEMM's layout (batches)
 };
 
 struct bb_kv_cache {
@@ -684,6 +753,7 @@ struct bb_kv_cache {
 struct bb_attn_op {
   bb_ctx* ctx;
   const bb_tensor *q, *k, *v, *o;
+  bb::PackedW q_p, k_p, v_p, o_p;  // the projections in the grouped GEMM's layout (batches)
   float *q_norm, *k_norm;  // device, [head_dim]
   int H, NH, NKV, HD;
   float eps, freq_base, scale;
@@ -741,14 +811,18 @@ void conv_forward_dev(bb_ctx* c, bb_conv_op* op, float* state, const float* x, s
     float* bcx = cv.take<float>(T * 3 * H);
     float* y = cv.take<float>(T * H);
     bb::Q8Bufs yq = carve_q8(cv, T, H);
+    int32_t* grp = cv.take<int32_t>(T + 8);
     if (pass == 0) {
       base = ensure_ws(c, cv.off);
       continue;
     }
-    project_dev(c, op->in_proj, H, 3 * H, x, T, bcx, xq);
+    bb::RouteBufs rb{};
+    const bool gemm = T >= bb::PROJ_GEMM_MIN_T && (op->in_p.w || op->out_p.w);
+    if (gemm) rb = one_group(c, grp, T);
+    project_dev(c, op->in_proj, op->in_p, gemm ? &rb : nullptr, H, 3 * H, x, T, bcx, xq);
     launch(c, bb::K_CONV, [&] { return bb::launch_conv(c->stream, true, bcx, state, op->conv_w, (int)H, op->L, (int)T, y); });
     launch(c, bb::K_CONV_STATE, [&] { return bb::launch_conv_state(c->stream, true, bcx, state, (int)H, op->L, (int)T); });
-    project_dev(c, op->out_proj, H, H, y, T, out, yq);
+    project_dev(c, op->out_proj, op->out_p, gemm ? &rb : nullptr, H, H, y, T, out, yq);
   }
 }
 
@@ -784,15 +858,20 @@ void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, c
     float* scores = cv.take<float>(T * NH * (n0 + T));
     float* attn = cv.take<float>(T * QD);
     bb::Q8Bufs aq = carve_q8(cv, T, QD);
+    int32_t* grp = cv.take<int32_t>(T + 8);
     if (pass == 0) {
       base = ensure_ws(c, cv.off);
       continue;
     }
     float* kn = kv->k + n0 * KV;
     float* vn = kv->v + n0 * KV;
-    project_dev(c, op->q, H, QD, x, T, q, xq);
-    project_dev(c, op->k, H, KV, x, T, kn, xq);
-    project_dev(c, op->v, H, KV, x, T, vn, xq);
+    bb::RouteBufs rb{};
+    const bool gemm = T >= bb::PROJ_GEMM_MIN_T && (op->q_p.w || op->k_p.w || op->v_p.w || op->o_p.w);
+    if (gemm) rb = one_group(c, grp, T);
+    const bb::RouteBufs* rbp = gemm ? &rb : nullptr;
+    project_dev(c, op->q, op->q_p, rbp, H, QD, x, T, q, xq);
+    project_dev(c, op->k, op->k_p, rbp, H, KV, x, T, kn, xq);
+    project_dev(c, op->v, op->v_p, rbp, H, KV, x, T, vn, xq);
     const float2* rope = op->rope + pos0 * (HD / 2);
     launch(c, bb::K_NORM_ROPE, [&] {
       return bb::launch_norm_rope(c->stream, q, (int)T, (int)NH, (int)HD, op->q_norm, op->eps, rope);
@@ -806,7 +885,7 @@ void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, c
     launch(c, bb::K_ATTN_PV, [&] {
       return bb::launch_attn_pv(c->stream, scores, kv->v, (int)n0, (int)T, (int)NH, (int)NKV, (int)HD, attn);
     });
-    project_dev(c, op->o, QD, H, attn, T, out, aq);
+    project_dev(c, op->o, op->o_p, rbp, QD, H, attn, T, out, aq);
   }
   kv->n = n0 + T;
 }
@@ -1241,6 +1320,7 @@ int bb_dense_create(bb_ctx* c, const bb_tensor* gate, const bb_tensor* up, const
     for (const bb_tensor* t : {gate, up, down})
       need(t->dtype == BB_Q4_K || t->dtype == BB_Q6_K, BB_ERR_DTYPE, "dense weights must be Q4_K or Q6_K");
     need(H % 256 == 0 && F % 256 == 0, BB_ERR_SHAPE, "hidden and ff must be multiples of 256");
+    set_device(c);
     auto* d = new bb_dense();
     d->ctx = c;
     d->gate = gate;
@@ -1248,12 +1328,27 @@ int bb_dense_create(bb_ctx* c, const bb_tensor* gate, const bb_tensor* up, const
     d->down = down;
     d->H = (int)H;
     d->F = (int)F;
+    try {
+      d->gu = pack_weights(c, gate, up, H, F);
+      d->dn = pack_weights(c, down, nullptr, F, H);
+    } catch (...) {
+      free_packed(d->gu);
+      delete d;
+      throw;
+    }
     *out = d;
   });
 }
 
 int bb_dense_destroy(bb_dense* d) {
-  return guard([&] { delete d; });
+  return guard([&] {
+    if (!d) return;
+    set_device(d->ctx);
+    (void)hipStreamSynchronize(d->ctx->stream);
+    free_packed(d->gu);
+    free_packed(d->dn);
+    delete d;
+  });
 }
 
 int bb_dense_forward(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* out, int loc) {
@@ -1533,7 +1628,11 @@ int bb_conv_op_create(bb_ctx* c, const bb_tensor* in_proj, const float* conv_w, 
     op->L = (int)l_cache;
     try {
       op->conv_w = upload_f32(c, conv_w, H * l_cache);
+      op->in_p = pack_weights(c, in_proj, nullptr, H, 3 * H);
+      op->out_p = pack_weights(c, out_proj, nullptr, H, H);
     } catch (...) {
+      if (op->conv_w) (void)hipFree(op->conv_w);
+      free_packed(op->in_p);
       delete op;
       throw;
     }
@@ -1545,7 +1644,10 @@ int bb_conv_op_destroy(bb_conv_op* op) {
   return guard([&] {
     if (!op) return;
     set_device(op->ctx);
+    (void)hipStreamSynchronize(op->ctx->stream);
     (void)hipFree(op->conv_w);
+    free_packed(op->in_p);
+    free_packed(op->out_p);
     delete op;
   });
 }
@@ -1679,9 +1781,15 @@ int bb_attn_op_create(bb_ctx* c, const bb_tensor* q, const bb_tensor* k, const b
       op->q_norm = upload_f32(c, q_norm, HD);
       op->k_norm = upload_f32(c, k_norm, HD);
       ensure_rope(c, op, 4096);
+      op->q_p = pack_weights(c, q, nullptr, H, QD);
+      op->k_p = pack_weights(c, k, nullptr, H, KV);
+      op->v_p = pack_weights(c, v, nullptr, H, KV);
+      op->o_p = pack_weights(c, o, nullptr, QD, H);
     } catch (...) {
       if (op->q_norm) (void)hipFree(op->q_norm);
       if (op->k_norm) (void)hipFree(op->k_norm);
+      if (op->rope) (void)hipFree(op->rope);
+      for (bb::PackedW* p : {&op->q_p, &op->k_p, &op->v_p, &op->o_p}) free_packed(*p);
       delete op;
       throw;
     }
@@ -1693,9 +1801,11 @@ int bb_attn_op_destroy(bb_attn_op* op) {
   return guard([&] {
     if (!op) return;
     set_device(op->ctx);
+    (void)hipStreamSynchronize(op->ctx->stream);
     (void)hipFree(op->q_norm);
     (void)hipFree(op->k_norm);
     if (op->rope) (void)hipFree(op->rope);
+    for (bb::PackedW* p : {&op->q_p, &op->k_p, &op->v_p, &op->o_p}) free_packed(*p);
     delete op;
   });
 }

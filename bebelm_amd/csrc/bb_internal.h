@@ -187,6 +187,20 @@ hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
                             int K, const RouteBufs& rb, GemmX x, float* slots);
 
+// A Q4_K / Q6_K weight matrix in the grouped GEMM's packed tile layout as a single expert: plain
+// 64-row tiles (GEMM_DOWN form, n_out % 128 == 0) or gate and up interleaved (GEMM_GATEUP form,
+// n_out % 64 == 0). w null: the matrix has no packed form and stays on the row kernels.
+struct PackedW {
+  uint8_t* w = nullptr;
+  size_t stride = 0;  // bytes of the packed matrix
+  int dt = 0;
+};
+// Batches of at least this many tokens run a packed projection on the grouped GEMM (every token
+// a member of the one group); smaller ones take the row kernels.
+constexpr size_t PROJ_GEMM_MIN_T = 32;
+// The route of "every one of T tokens in group 0": counts[0] = T, offsets = {0, T}, perm = 0..T-1.
+hipError_t launch_one_group(hipStream_t s, int T, RouteBufs rb);
+
 // Q8 rows (quants and per-256 scales only) of n_rows vectors of n floats.
 hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx);
 

@@ -9,8 +9,8 @@
 //   conv      sum = w[L-1]·bx, then += w[k]·col_k for k = 0..L-2 (columns oldest first; the
 //             columns before the batch come from the state). One thread per (token, channel):
 //             every output depends only on its own L columns, so the batch is the rolled loop.
-//   scores    matmul.rs's dot (32 fmaf chains, the `wide` lane reduce) on a half-wave, times
-//             1/sqrt(head_dim).
+//   scores    matmul.rs's dot (32 fmaf chains, the `wide` lane reduce) in one lane per position,
+//             times 1/sqrt(head_dim).
 //   softmax   max, f32 exps (bb_expf: glibc's expf restated), their f64 sum left to right in one
 //             lane, each value times (float)(1.0 / sum).
 //   P·V       out[d] = Σ_j w_j·v[j][d] in position order from 0.0, one lane per d.
@@ -23,6 +23,9 @@
 #include "bb_internal.h"
 
 namespace bb {
+
+constexpr int PV_CHUNK = 32;    // value-column loads in flight per lane in P·V of one row
+constexpr int AT_PV_MIN_T = 8;  // batches of this many tokens take the tiled softmax + P·V
 
 // ---- gated short conv ------------------------------------------------------------------------
 // Column j of [state; bx] for channel c (j < L-1: the state; else token j-(L-1) of the batch).
@@ -114,40 +117,66 @@ hipError_t launch_norm_rope(hipStream_t s, float* buf, int T, int n_heads, int h
 }
 
 // ---- attention -------------------------------------------------------------------------------
-// matmul.rs:36-66's dot of q (LDS) and a key row on a 32-lane half-wave: lane c runs chain c,
-// then the lane combine and the `wide` reduce tree through shuffles; valid on lane c == 0.
-__device__ __forceinline__ float dot_half(const float* q, const float* __restrict__ k, int n, int c) {
-  float acc = 0.0f;
-  const int n32 = n & ~31;
+// matmul.rs:36-66's dot of q (LDS) and a key row in one lane: 32 fmaf chains (chain c over the
+// elements i = c mod 32, then for a tail of whole groups of 8 the chains c < 8 over it), the lane
+// combine v_c = (a_c + a_{c+8}) + (a_{c+16} + a_{c+24}), the `wide` reduce tree
+// ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7)), then the last n % 8 products added left to right.
+// V4: n % 4 == 0 and 16-byte aligned rows (float4 loads).
+template <bool V4>
+__device__ __forceinline__ float dot_lane(const float* q, const float* __restrict__ k, int n) {
+  float a[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) a[c] = 0.0f;
   int i = 0;
-  for (; i < n32; i += 32) acc = fmaf(q[i + c], k[i + c], acc);
-  for (; i + 8 <= n; i += 8)
-    if (c < 8) acc = fmaf(q[i + c], k[i + c], acc);
-  const float A = acc + __shfl_down(acc, 8, 32);
-  const float v = A + __shfl_down(A, 16, 32);
-  const float u = v + __shfl_down(v, 4, 32);
-  const float y = u + __shfl_down(u, 2, 32);
-  float r = y + __shfl_down(y, 1, 32);
+  for (; i + 32 <= n; i += 32) {
+    if constexpr (V4) {
+#pragma unroll
+      for (int c4 = 0; c4 < 8; ++c4) {
+        const float4 kv = *reinterpret_cast<const float4*>(k + i + 4 * c4);
+        const float4 qv = *reinterpret_cast<const float4*>(q + i + 4 * c4);
+        a[4 * c4] = fmaf(qv.x, kv.x, a[4 * c4]);
+        a[4 * c4 + 1] = fmaf(qv.y, kv.y, a[4 * c4 + 1]);
+        a[4 * c4 + 2] = fmaf(qv.z, kv.z, a[4 * c4 + 2]);
+        a[4 * c4 + 3] = fmaf(qv.w, kv.w, a[4 * c4 + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 32; ++c) a[c] = fmaf(q[i + c], k[i + c], a[c]);
+    }
+  }
+  for (; i + 8 <= n; i += 8) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) a[c] = fmaf(q[i + c], k[i + c], a[c]);
+  }
+  float v[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) v[c] = (a[c] + a[c + 8]) + (a[c + 16] + a[c + 24]);
+  float r = ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
   for (; i < n; ++i) r = r + q[i] * k[i];
   return r;
 }
 
 // scores[t][h][j] = dot(q[t][h], k[j][h / group]) · scale for j < n0 + t + 1 (the positions
-// token t sees once its own key is in the cache). Block = 8 half-waves = 8 positions.
-__global__ void __launch_bounds__(256) k_attn_scores(const float* __restrict__ q, const float* __restrict__ kc, int n0,
-                                                     int n_heads, int n_kv, int hd, float scale, float* __restrict__ sc,
-                                                     int ld) {
-  __shared__ float sq[OPS_HD_MAX];
-  const int h = blockIdx.y, t = blockIdx.z;
-  for (int d = threadIdx.x; d < hd; d += 256) sq[d] = q[((size_t)t * n_heads + h) * hd + d];
+// token t sees once its own key is in the cache). Block = one wave = 64 positions of one token
+// and one kv head: lane j's key row is read once for the G heads that share it, q of those
+// heads from LDS (dynamic, G·hd floats; the same address in every lane).
+template <bool V4>
+__global__ void __launch_bounds__(64) k_attn_scores_gqa(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        int n0, int n_heads, int n_kv, int hd, float scale,
+                                                        float* __restrict__ sc, int ld) {
+  extern __shared__ __align__(16) float sq[];
+  const int g = blockIdx.y, t = blockIdx.z, G = n_heads / n_kv;
+  const int n = n0 + t + 1, j0 = blockIdx.x * 64;
+  if (j0 >= n) return;  // the whole block
+  const float* qt = q + ((size_t)t * n_heads + (size_t)g * G) * hd;  // heads gG .. gG+G-1, contiguous
+  for (int i = threadIdx.x; i < G * hd; i += 64) sq[i] = qt[i];
   __syncthreads();
-  const int j = blockIdx.x * 8 + (threadIdx.x >> 5), c = threadIdx.x & 31;
-  if (j >= n0 + t + 1) return;  // whole half-waves leave together
-  const int kv = h / (n_heads / n_kv);
-  const float r = dot_half(sq, kc + ((size_t)j * n_kv + kv) * hd, hd, c);
-  if (c == 0) sc[((size_t)t * n_heads + h) * ld + j] = r * scale;
+  const int j = j0 + threadIdx.x;
+  if (j >= n) return;  // (no barrier follows)
+  const float* kr = kc + ((size_t)j * n_kv + g) * hd;
+  for (int hh = 0; hh < G; ++hh)
+    sc[((size_t)t * n_heads + (size_t)g * G + hh) * ld + j] = dot_lane<V4>(sq + hh * hd, kr, hd) * scale;
 }
-
 // A score row as one wave reads and rewrites it: in LDS (rows up to OPS_ROW_LDS values), else in
 // global memory through agent-scope accesses. The row is re-read after other lanes of the wave
 // rewrote it, so it must not be read through the non-coherent vector L1 cache.
@@ -174,8 +203,17 @@ __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, fl
   for (int j = lane; j < n; j += 64) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
   __syncthreads();
   if (lane == 0) {
+    // left to right; eight values read ahead of their adds
     double sum = 0.0;
-    for (int j = 0; j < n; ++j) sum += (double)r.ld(j);
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      float e[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) e[u] = r.ld(j + u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += (double)e[u];
+    }
+    for (; j < n; ++j) sum += (double)r.ld(j);
     *s_inv = (float)(1.0 / sum);
   }
   __syncthreads();
@@ -202,24 +240,224 @@ __global__ void __launch_bounds__(64) k_attn_softmax_pv(float* sc, const float* 
   const Row<LDS> r{LDS ? lrow : s};
   wave_softmax<LDS>(r, n, exptab, &s_inv);
   const int kv = h / (n_heads / n_kv);
+  const size_t vs = (size_t)n_kv * hd;  // between consecutive positions of one value column
   for (int d = lane; d < hd; d += 64) {
+    // position order from 0.0; the values of the next 32 positions are loaded while the adds of
+    // the current 32 run (the adds are a dependent chain, the loads are not)
+    const float* vp = vc + (size_t)kv * hd + d;
     float o = 0.0f;
-    for (int j = 0; j < n; ++j) o += r.ld(j) * vc[((size_t)j * n_kv + kv) * hd + d];
+    float xa[PV_CHUNK], xb[PV_CHUNK];
+    const int nfull = n / PV_CHUNK;
+    auto load = [&](float(&x)[PV_CHUNK], int c) {
+#pragma unroll
+      for (int u = 0; u < PV_CHUNK; ++u) x[u] = vp[(size_t)(c * PV_CHUNK + u) * vs];
+    };
+    auto accum = [&](const float(&x)[PV_CHUNK], int c) {
+#pragma unroll
+      for (int u = 0; u < PV_CHUNK; ++u) o += r.ld(c * PV_CHUNK + u) * x[u];
+    };
+    if (nfull > 0) load(xa, 0);
+    int c = 0;
+    for (; c + 2 <= nfull; c += 2) {
+      load(xb, c + 1);
+      accum(xa, c);
+      if (c + 2 < nfull) load(xa, c + 2);
+      accum(xb, c + 1);
+    }
+    if (c < nfull) accum(xa, c);
+    for (int j = nfull * PV_CHUNK; j < n; ++j) o += r.ld(j) * vp[(size_t)j * vs];
     out[((size_t)t * n_heads + h) * hd + d] = o;
+  }
+}
+
+// ---- attention tiles (head_dim 64) ------------------------------------------------------------
+// Items are (token, head) pairs of one kv head g: a block takes AT_ITEMS / G tokens, so that its
+// items (token-major, then the G heads) number at most AT_ITEMS, and 4 waves take items w, w+4, ...
+constexpr int AT_HD = 64;
+constexpr int AT_KS = AT_HD + 4;  // padded LDS row of a key (conflict-free float4 reads)
+constexpr int AT_ITEMS = 64;     // items of a scores block
+constexpr int AT_PV_ITEMS = 16;  // items of a P·V block (more blocks: its waves run long chains)
+constexpr int AT_IPW = AT_PV_ITEMS / 4;  // P·V items per wave
+
+__host__ __device__ constexpr int at_tokens(int G, int items = AT_ITEMS) { return G >= items ? 1 : items / G; }
+
+// matmul.rs:36-66's dot (dot_lane's order) of a key row held in registers and q in LDS.
+__device__ __forceinline__ float dot64_reg(const float (&k)[AT_HD], const float* q) {
+  float a[32];
+#pragma unroll
+  for (int c4 = 0; c4 < 8; ++c4) {
+    const float4 qv = *reinterpret_cast<const float4*>(q + 4 * c4);
+    a[4 * c4] = fmaf(qv.x, k[4 * c4], 0.0f);
+    a[4 * c4 + 1] = fmaf(qv.y, k[4 * c4 + 1], 0.0f);
+    a[4 * c4 + 2] = fmaf(qv.z, k[4 * c4 + 2], 0.0f);
+    a[4 * c4 + 3] = fmaf(qv.w, k[4 * c4 + 3], 0.0f);
+  }
+#pragma unroll
+  for (int c4 = 0; c4 < 8; ++c4) {
+    const float4 qv = *reinterpret_cast<const float4*>(q + 32 + 4 * c4);
+    a[4 * c4] = fmaf(qv.x, k[32 + 4 * c4], a[4 * c4]);
+    a[4 * c4 + 1] = fmaf(qv.y, k[32 + 4 * c4 + 1], a[4 * c4 + 1]);
+    a[4 * c4 + 2] = fmaf(qv.z, k[32 + 4 * c4 + 2], a[4 * c4 + 2]);
+    a[4 * c4 + 3] = fmaf(qv.w, k[32 + 4 * c4 + 3], a[4 * c4 + 3]);
+  }
+  float v[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) v[c] = (a[c] + a[c + 8]) + (a[c + 16] + a[c + 24]);
+  return ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+}
+
+// Scores of the block's tokens x the G heads of kv head g against positions j0..j0+63: the 64
+// key rows are copied into LDS (coalesced) and lane j keeps row j in registers; q of every item
+// is read from LDS (the same address in every lane). Causal: item (t, .) covers j <= n0 + t.
+__global__ void __launch_bounds__(256) k_attn_scores_tile(const float* __restrict__ q, const float* __restrict__ kc,
+                                                          int n0, int T, int n_heads, int n_kv, float scale,
+                                                          float* __restrict__ sc, int ld) {
+  __shared__ __align__(16) float sq[AT_ITEMS * AT_HD];
+  __shared__ __align__(16) float sk[64 * AT_KS];
+  const int G = n_heads / n_kv, TT = at_tokens(G);
+  const int g = blockIdx.y, t0 = blockIdx.z * TT, j0 = blockIdx.x * 64;
+  const int nt = min(TT, T - t0), n_items = nt * G;
+  if (j0 > n0 + t0 + nt - 1) return;  // no token of the block sees these positions
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n_items * (AT_HD / 4); i += 256) {
+    const int it = i / (AT_HD / 4), c4 = i % (AT_HD / 4), tt = it / G, hh = it % G;
+    reinterpret_cast<float4*>(sq)[i] =
+        reinterpret_cast<const float4*>(q + ((size_t)(t0 + tt) * n_heads + (size_t)g * G + hh) * AT_HD)[c4];
+  }
+  const int jlast = n0 + T - 1;  // last cached position (rows past it are clamped, never used)
+  for (int i = tid; i < 64 * (AT_HD / 4); i += 256) {
+    const int r = i / (AT_HD / 4), c4 = i % (AT_HD / 4);
+    const int jj = min(j0 + r, jlast);
+    *reinterpret_cast<float4*>(sk + r * AT_KS + 4 * c4) =
+        reinterpret_cast<const float4*>(kc + ((size_t)jj * n_kv + g) * AT_HD)[c4];
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6, j = j0 + lane;
+  float kr[AT_HD];
+#pragma unroll
+  for (int c4 = 0; c4 < AT_HD / 4; ++c4) {
+    const float4 v = *reinterpret_cast<const float4*>(sk + lane * AT_KS + 4 * c4);
+    kr[4 * c4] = v.x;
+    kr[4 * c4 + 1] = v.y;
+    kr[4 * c4 + 2] = v.z;
+    kr[4 * c4 + 3] = v.w;
+  }
+  for (int it = w; it < n_items; it += 4) {
+    const int tt = it / G, hh = it % G, t = t0 + tt;
+    if (j > n0 + t) continue;  // (no barrier follows)
+    sc[((size_t)t * n_heads + (size_t)g * G + hh) * ld + j] = dot64_reg(kr, sq + it * AT_HD) * scale;
+  }
+}
+
+// softmax.rs:9-22 of every score row (t, h), each of its own length n0 + t + 1, in place.
+template <bool LDS>
+__global__ void __launch_bounds__(64) k_attn_softmax(float* sc, int n0, int n_heads, int ld) {
+  extern __shared__ float lrow[];
+  __shared__ uint64_t exptab[32];
+  __shared__ float s_inv;
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  if (lane < 32) exptab[lane] = exp_table_entry();
+  const int n = n0 + t + 1;
+  float* s = sc + ((size_t)t * n_heads + h) * ld;
+  if constexpr (LDS)
+    for (int j = lane; j < n; j += 64) lrow[j] = s[j];
+  __syncthreads();
+  wave_softmax<LDS>(Row<LDS>{LDS ? lrow : s}, n, exptab, &s_inv);
+  if constexpr (LDS)
+    for (int j = lane; j < n; j += 64) s[j] = lrow[j];
+}
+
+// out[t][h][d] = Σ_j p[t][h][j]·v[j][g][d] for the block's items, position order from 0.0. Per
+// chunk of 64 positions the value rows and the items' probabilities are copied into LDS; lane d
+// of wave w keeps the running sums of items w, w+4, ... (independent chains side by side).
+__global__ void __launch_bounds__(256) k_attn_pv_tile(const float* __restrict__ p, const float* __restrict__ vc,
+                                                      int n0, int T, int n_heads, int n_kv, int ld,
+                                                      float* __restrict__ out) {
+  __shared__ __align__(16) float sv[64 * AT_HD];
+  __shared__ __align__(16) float sp[AT_PV_ITEMS * 64];
+  const int G = n_heads / n_kv, TT = at_tokens(G, AT_PV_ITEMS);
+  const int g = blockIdx.x, t0 = blockIdx.y * TT;
+  const int nt = min(TT, T - t0), n_items = nt * G;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int jlast = n0 + t0 + nt - 1;  // the last position any item uses
+  float o[AT_IPW];
+  int lim[AT_IPW];  // item w + 4k uses positions j <= lim[k] (-1: no such item)
+#pragma unroll
+  for (int k = 0; k < AT_IPW; ++k) {
+    const int it = w + 4 * k;
+    o[k] = 0.0f;
+    lim[k] = it < n_items ? n0 + t0 + it / G : -1;
+  }
+  for (int c0 = 0; c0 <= jlast; c0 += 64) {
+    __syncthreads();  // the previous chunk has been used
+    for (int i = tid; i < 64 * (AT_HD / 4); i += 256) {
+      const int r = i / (AT_HD / 4), c4 = i % (AT_HD / 4);
+      const int jj = min(c0 + r, jlast);
+      reinterpret_cast<float4*>(sv)[i] = reinterpret_cast<const float4*>(vc + ((size_t)jj * n_kv + g) * AT_HD)[c4];
+    }
+    for (int i = tid; i < n_items * 64; i += 256) {
+      const int it = i >> 6, jj = c0 + (i & 63), t = t0 + it / G, hh = it % G;
+      sp[i] = jj <= n0 + t ? p[((size_t)t * n_heads + (size_t)g * G + hh) * ld + jj] : 0.0f;
+    }
+    __syncthreads();
+    const int jn = min(64, jlast - c0 + 1);
+    for (int jj = 0; jj < jn; ++jj) {
+      const float v = sv[jj * AT_HD + lane];
+      const int j = c0 + jj;
+      // branch-free: every item adds its product, with the bits cleared (+0.0) where the item
+      // does not see position j. Adding +0.0 leaves a sum unchanged: the sums start at +0.0 and
+      // never become -0.0 (x + y rounds an exact zero to +0.0), so they are the ones of adding
+      // only the positions seen.
+#pragma unroll
+      for (int k = 0; k < AT_IPW; ++k) {
+        const uint32_t keep = j <= lim[k] ? 0xffffffffu : 0u;
+        const float pv = sp[(w + 4 * k) * 64 + jj] * v;
+        o[k] += __uint_as_float(__float_as_uint(pv) & keep);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < AT_IPW; ++k) {
+    const int it = w + 4 * k;
+    if (it < n_items)
+      out[((size_t)(t0 + it / G) * n_heads + (size_t)g * G + it % G) * AT_HD + lane] = o[k];
   }
 }
 
 hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
                               int hd, float scale, float* scores) {
   const int ld = n0 + T;
-  BB_LAUNCH(k_attn_scores, dim3((unsigned)((ld + 7) / 8), n_heads, T), dim3(256), 0, s, q, kc, n0, n_heads, n_kv, hd,
-            scale, scores, ld);
+  if (hd == AT_HD && n_heads / n_kv <= AT_ITEMS) {
+    const int TT = at_tokens(n_heads / n_kv);
+    BB_LAUNCH(k_attn_scores_tile, dim3((unsigned)((ld + 63) / 64), n_kv, (unsigned)((T + TT - 1) / TT)), dim3(256), 0,
+              s, q, kc, n0, T, n_heads, n_kv, scale, scores, ld);
+    return hipGetLastError();
+  }
+  const size_t lds = (size_t)(n_heads / n_kv) * hd * sizeof(float);
+  const dim3 grid((unsigned)((ld + 63) / 64), n_kv, T);
+  if (hd % 4 == 0)
+    BB_LAUNCH(k_attn_scores_gqa<true>, grid, dim3(64), lds, s, q, kc, n0, n_heads, n_kv, hd, scale, scores, ld);
+  else
+    BB_LAUNCH(k_attn_scores_gqa<false>, grid, dim3(64), lds, s, q, kc, n0, n_heads, n_kv, hd, scale, scores, ld);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0, int T, int n_heads, int n_kv, int hd,
                           float* out) {
   const int ld = n0 + T;
+  if (T >= AT_PV_MIN_T && hd == AT_HD && n_heads / n_kv <= AT_PV_ITEMS) {
+    // a batch: every row's softmax, then P·V in tiles of (tokens x heads of one kv head)
+    if (ld <= OPS_ROW_LDS)
+      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, n0, n_heads, ld);
+    else
+      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64), 0, s, scores, n0, n_heads, ld);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int TT = at_tokens(n_heads / n_kv, AT_PV_ITEMS);
+    BB_LAUNCH(k_attn_pv_tile, dim3(n_kv, (unsigned)((T + TT - 1) / TT)), dim3(256), 0, s, scores, vc, n0, T, n_heads,
+              n_kv, ld, out);
+    return hipGetLastError();
+  }
   if (ld <= OPS_ROW_LDS)
     BB_LAUNCH(k_attn_softmax_pv<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, vc, n0, n_heads, n_kv, hd,
               ld, out);

@@ -1003,6 +1003,23 @@ hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t 
   return launch_gemm<DT_Q6_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots);
 }
 
+// ---- one group of T tokens (dense projections on the grouped GEMM) ----------------------------------
+__global__ void __launch_bounds__(256) k_one_group(int T, RouteBufs rb) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < T) rb.perm[i] = i;
+  if (i == 0) {
+    rb.counts[0] = T;
+    rb.offsets[0] = 0;
+    rb.offsets[1] = T;
+  }
+}
+
+hipError_t launch_one_group(hipStream_t s, int T, RouteBufs rb) {
+  if (T < 1) return hipErrorInvalidValue;
+  BB_LAUNCH(k_one_group, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, T, rb);
+  return hipGetLastError();
+}
+
 // ---- Q8 rows ---------------------------------------------------------------------------------------
 // One wave per 256-block: amax, scale amax/127, quants round(v·127/amax) (kernels/matmul.rs:141-160).
 __global__ void __launch_bounds__(256) k_quant_rows(const float* __restrict__ x, size_t n_rows, int n,

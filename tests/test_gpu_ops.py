@@ -111,7 +111,10 @@ def test_rope_matches_oracle(gpu_ctx, oracle, pos):
 
 @pytest.mark.parametrize("hidden,dtypes,steps", [(512, (synth.Q4_K, synth.Q6_K), (1, 1, 5, 1, 9)),
                                                  (2048, (synth.Q4_K, synth.Q4_K), (1, 1, 3, 1)),
-                                                 (2048, (synth.Q6_K, synth.Q4_K), (12, 1))])
+                                                 (2048, (synth.Q6_K, synth.Q4_K), (12, 1)),
+                                                 # batches of 32+ tokens: projections on the grouped GEMM
+                                                 (2048, (synth.Q4_K, synth.Q6_K), (32, 1, 300)),
+                                                 (512, (synth.Q6_K, synth.Q6_K), (200, 2, 33))])
 def test_conv_op_matches_oracle(gpu_ctx, oracle, hidden, dtypes, steps):
     w = synth.conv_weights(21, hidden=hidden, in_dtype=dtypes[0], out_dtype=dtypes[1])
     op = ConvOp(gpu_ctx, w)
@@ -131,7 +134,9 @@ def test_conv_op_matches_oracle(gpu_ctx, oracle, hidden, dtypes, steps):
 
 @pytest.mark.parametrize("hidden,nh,nkv,steps", [(512, 8, 2, (7, 1, 1, 3, 1)),
                                                  (2048, 32, 8, (1, 1, 1, 1)),
-                                                 (2048, 32, 8, (40, 1, 2))])
+                                                 (2048, 32, 8, (40, 1, 2)),
+                                                 (2048, 32, 8, (300, 1, 64)),
+                                                 (512, 8, 2, (33, 100))])
 def test_attn_op_matches_oracle(gpu_ctx, oracle, hidden, nh, nkv, steps):
     w = synth.attn_weights(23, hidden=hidden, n_heads=nh, n_kv_heads=nkv)
     op = AttnOp(gpu_ctx, w)

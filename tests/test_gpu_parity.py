@@ -352,6 +352,27 @@ def test_dense_ffn(gpu_ctx, oracle):
         layer.close()
 
 
+@pytest.mark.parametrize("hidden,ff,dts,ts", [(2048, 7168, (Q4_K, Q4_K, Q4_K), (32, 77, 512)),
+                                               (512, 1024, (Q6_K, Q6_K, Q6_K), (40, 130, 200)),
+                                               (512, 1024, (Q4_K, Q6_K, Q6_K), (64,))])
+def test_dense_ffn_batches(gpu_ctx, oracle, hidden, ff, dts, ts):
+    # batches of 32 tokens and more: gate/up + swiglu and down on the grouped GEMM with every token
+    # in one group (Q6_K down of 128+ tokens: member tiles of 128; 192+: k_gemm_wide); gate and up
+    # of two dtypes stay on the row kernels
+    g = synth.rng(7, hidden)
+    d = synth.DenseWeights(hidden, ff, dts[0], dts[1], dts[2], synth.quant_tensor(g, dts[0], hidden, ff),
+                           synth.quant_tensor(g, dts[1], hidden, ff), synth.quant_tensor(g, dts[2], ff, hidden))
+    layer = DenseLayer(gpu_ctx, d)
+    try:
+        for t in ts:
+            log(f"dense batch hidden={hidden} ff={ff} dtypes={dts} t={t}")
+            x = synth.hidden_states(8 + t, t, hidden=hidden).reshape(-1)
+            got = layer.forward(np.ascontiguousarray(x), t, np.empty(t * hidden, np.float32))
+            assert_bits(got, oracle.dense_ffn(d, x, t), f"dense batch {dts} t={t}")
+    finally:
+        layer.close()
+
+
 @pytest.mark.parametrize("dts", [(Q6_K, Q6_K, Q6_K), (Q4_K, Q6_K, Q4_K)])
 def test_dense_ffn_other_dtypes(gpu_ctx, oracle, dts):
     # gate and up of one dtype take the fused gate/up/swiglu pass; of two dtypes, separate passes
