@@ -31,7 +31,8 @@ class BBError(RuntimeError):
 
 class FusedJob(ctypes.Structure):
     _fields_ = [("dtype", c_uint32), ("w", c_void_p), ("byte_off", c_size_t), ("n_in", c_size_t),
-                ("n_out", c_size_t), ("qx_q", c_void_p), ("qx_scales", c_void_p), ("qx_sums", c_void_p)]
+                ("n_out", c_size_t), ("qx_q", c_void_p), ("qx_scales", c_void_p), ("qx_sums", c_void_p),
+                ("x", c_void_p)]
 
 
 class RouteTrace(ctypes.Structure):

@@ -1106,29 +1106,46 @@ int bb_matvec_fused_batch(bb_ctx* c, const bb_fused_job* jobs, size_t n_jobs, fl
     size_t total = 0;
     std::vector<size_t> rbytes(n_jobs);
     for (size_t j = 0; j < n_jobs; ++j) {
+      // (F32 / F16 jobs have no fused path: fused_row_dot panics on them, matmul.rs:783)
       need(jobs[j].dtype == BB_Q4_K || jobs[j].dtype == BB_Q6_K, BB_ERR_DTYPE,
-           "matvec_fused_batch: only pre-quantised Q4_K/Q6_K jobs are supported");
+           "matvec_fused_batch: jobs must be Q4_K or Q6_K");
+      need(jobs[j].qx_q != nullptr || jobs[j].x != nullptr, BB_ERR_ARG, "matvec_fused_batch: a job has neither qx nor x");
       check_weight_range(jobs[j].w, jobs[j].dtype, jobs[j].byte_off, jobs[j].n_in, jobs[j].n_out, rbytes[j]);
       total += jobs[j].n_out;
     }
     set_device(c);
     std::vector<Io> ios;
+    std::vector<size_t> first(n_jobs);  // the job's first entry in ios
     for (size_t j = 0; j < n_jobs; ++j) {
-      ios.push_back({jobs[j].qx_q, jobs[j].n_in, true, false});
-      ios.push_back({jobs[j].qx_scales, jobs[j].n_in / 256 * 4, true, false});
-      ios.push_back({jobs[j].qx_sums, jobs[j].n_in / 32 * 4, true, false});
+      first[j] = ios.size();
+      if (jobs[j].qx_q) {
+        ios.push_back({jobs[j].qx_q, jobs[j].n_in, true, false});
+        ios.push_back({jobs[j].qx_scales, jobs[j].n_in / 256 * 4, true, false});
+        ios.push_back({jobs[j].qx_sums, jobs[j].n_in / 32 * 4, true, false});
+      } else {
+        ios.push_back({jobs[j].x, jobs[j].n_in * 4, true, false});
+      }
     }
     ios.push_back({out, total * 4, false, true});
     with_io(c, loc, ios, [&](std::vector<void*>& d) {
       float* o = static_cast<float*>(d.back());
       size_t start = 0;
       for (size_t j = 0; j < n_jobs; ++j) {
-        bb::Q8Bufs q{static_cast<int8_t*>(d[3 * j]), static_cast<float*>(d[3 * j + 1]), static_cast<int32_t*>(d[3 * j + 2])};
         const bb_fused_job& jb = jobs[j];
-        launch(c, bb::K_ROWS_Q8, [&] {
-          return bb::launch_rows_q8(c->stream, (int)jb.dtype, jb.w->dev + jb.byte_off, rbytes[j], (int)(jb.n_in / 256),
-                                    jb.n_out, q, jb.n_in, 1, o + start, jb.n_out, 1);
-        });
+        const size_t f = first[j];
+        if (jb.qx_q) {
+          bb::Q8Bufs q{static_cast<int8_t*>(d[f]), static_cast<float*>(d[f + 1]), static_cast<int32_t*>(d[f + 2])};
+          launch(c, bb::K_ROWS_Q8, [&] {
+            return bb::launch_rows_q8(c->stream, (int)jb.dtype, jb.w->dev + jb.byte_off, rbytes[j],
+                                      (int)(jb.n_in / 256), jb.n_out, q, jb.n_in, 1, o + start, jb.n_out, 1);
+          });
+        } else {
+          launch(c, bb::K_ROWS_F32, [&] {
+            return bb::launch_fused_rows_f32(c->stream, (int)jb.dtype, jb.w->dev + jb.byte_off, rbytes[j],
+                                             (int)(jb.n_in / 256), jb.n_out, static_cast<const float*>(d[f]),
+                                             o + start);
+          });
+        }
         start += jb.n_out;
       }
     });

@@ -218,6 +218,9 @@ hipError_t launch_rows_q8_swiglu(hipStream_t s, int dtype, const uint8_t* gate, 
 
 hipError_t launch_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t n_in, size_t n_rows, const float* x,
                            size_t n_tok, float* y);
+// The f32 fused dot (fused_row_dot) of n_rows Q4_K / Q6_K rows with one f32 vector x.
+hipError_t launch_fused_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows,
+                                 const float* x, float* y);
 
 enum ElemOp : int { EW_SWIGLU = 0, EW_SIGMOID, EW_ADD_SCALED, EW_ADD_ASSIGN };
 hipError_t launch_elementwise(hipStream_t s, int op, float* out, const float* a, const float* b, float scalar,

@@ -255,6 +255,105 @@ hipError_t launch_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t n_
   return hipGetLastError();
 }
 
+// ---- the f32 arm of matvec_fused_batch (FusedJob with qx: None) ------------------------------
+// fused_row_dot (matmul.rs:777-785): per 256-block the f32 fused dot of the row with x, summed
+// over blocks from -0.0. One lane per row; x (shared by every row) is read through the cache.
+__device__ __forceinline__ float reduce8(const float (&v)[8]) {
+  return ((v[0] + v[4]) + (v[2] + v[6])) + ((v[1] + v[5]) + (v[3] + v[7]));
+}
+
+// dot_q4k_block (matmul.rs:104-122): per 64-element chunk, nibble_dot32 (:73-94) of the low
+// then the high nibbles (8 lanes of fmaf chains for Σq·x and of adds for Σx, each reduced by the
+// reduce tree), then sum += (d·sc)·Σqx − (dmin·m)·Σx per sub-block.
+__device__ float q4k_block_f32(const uint8_t* __restrict__ blk, const float* __restrict__ x) {
+  const float d = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+  const float dmin = f16_bits_to_f32((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+  uint32_t sw[3];
+  for (int i = 0; i < 3; ++i)
+    sw[i] = (uint32_t)blk[4 + 4 * i] | ((uint32_t)blk[5 + 4 * i] << 8) | ((uint32_t)blk[6 + 4 * i] << 16) |
+            ((uint32_t)blk[7 + 4 * i] << 24);
+  float sum = 0.0f;
+  for (int chunk = 0; chunk < 4; ++chunk) {
+    const uint8_t* q = blk + 16 + 32 * chunk;
+    float part[2];
+    for (int hi = 0; hi < 2; ++hi) {
+      const float* xs = x + 64 * chunk + 32 * hi;
+      float qx[8], xa[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) qx[l] = xa[l] = 0.0f;
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const uint8_t b = q[8 * k + l];
+          const float xv = xs[8 * k + l];
+          qx[l] = fmaf((float)(hi ? (b >> 4) : (b & 0xF)), xv, qx[l]);
+          xa[l] = xa[l] + xv;
+        }
+      int sc, m;
+      q4k_scale_min(sw[0], sw[1], sw[2], 2 * chunk + hi, sc, m);
+      part[hi] = (d * (float)sc) * reduce8(qx) - (dmin * (float)m) * reduce8(xa);
+    }
+    sum += part[0];
+    sum += part[1];
+  }
+  return sum;
+}
+
+// dot_q6k_block (matmul.rs:455-479): acc += sc·q6_dot16 over the 16 sub-blocks (q6_dot16,
+// :430-444: 8 lanes of fmaf chains over two 8-element steps, reduced), then d·acc.
+__device__ float q6k_block_f32(const uint8_t* __restrict__ blk, const float* __restrict__ x) {
+  const float d = f16_bits_to_f32((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+  float acc = 0.0f;
+  for (int n = 0; n < 2; ++n) {
+    const uint8_t* ql = blk + 64 * n;
+    const uint8_t* qh = blk + 128 + 32 * n;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192 + 8 * n);
+    for (int g = 0; g < 4; ++g) {
+      const int ql_off = (g & 1) ? 32 : 0, high = g >> 1, shift = 2 * g;
+      for (int sub = 0; sub < 2; ++sub) {
+        const float* xg = x + 128 * n + 32 * g + 16 * sub;
+        float qx[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qx[j] = 0.0f;
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int li = 16 * sub + 8 * c + j;
+            const int lo = high ? (ql[ql_off + li] >> 4) : (ql[ql_off + li] & 0x0F);
+            const int h2 = (qh[li] >> shift) & 3;
+            qx[j] = fmaf((float)((lo | (h2 << 4)) - 32), xg[8 * c + j], qx[j]);
+          }
+        acc += (float)sc[2 * g + sub] * reduce8(qx);
+      }
+    }
+  }
+  return d * acc;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) k_fused_rows_f32(const uint8_t* __restrict__ w, size_t row_bytes, int nb,
+                                                        size_t n_rows, const float* __restrict__ x,
+                                                        float* __restrict__ y) {
+  const size_t o = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n_rows) return;
+  const uint8_t* row = w + o * row_bytes;
+  float sum = -0.0f;
+  for (int b = 0; b < nb; ++b) {
+    if constexpr (DT == DT_Q4_K) sum += q4k_block_f32(row + (size_t)b * 144, x + (size_t)b * QK);
+    else sum += q6k_block_f32(row + (size_t)b * 210, x + (size_t)b * QK);
+  }
+  y[o] = sum;
+}
+
+hipError_t launch_fused_rows_f32(hipStream_t s, int dtype, const uint8_t* w, size_t row_bytes, int nb, size_t n_rows,
+                                 const float* x, float* y) {
+  if (n_rows == 0) return hipSuccess;
+  const dim3 grid((unsigned)((n_rows + 255) / 256));
+  if (dtype == DT_Q4_K) BB_LAUNCH(k_fused_rows_f32<DT_Q4_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, x, y);
+  else BB_LAUNCH(k_fused_rows_f32<DT_Q6_K>, grid, dim3(256), 0, s, w, row_bytes, nb, n_rows, x, y);
+  return hipGetLastError();
+}
+
 // activation.rs:16-29, elementwise.rs:4-17.
 __global__ void __launch_bounds__(256) k_elementwise(int op, float* __restrict__ out, const float* __restrict__ a,
                                                      const float* __restrict__ b, float scalar, size_t n) {

@@ -55,21 +55,28 @@ def matmul(ctx, dtype, w, n_in, n_out, x, n_tokens, y, byte_off=0):
 
 @dataclass
 class FusedJob:
+    """FusedJob (matmul.rs:995-1005): qx (Q8Vec) for the integer dot, or qx None and x (f32) for
+    the f32 fused dot."""
     dtype: int
     w: object
     n_in: int
     n_out: int
-    qx: Q8Vec
+    qx: object = None
     byte_off: int = 0
+    x: object = None
 
 
 def matvec_fused_batch(ctx, jobs, out):
     arr = (_lib.FusedJob * len(jobs))()
     arrays = [out]
     for i, j in enumerate(jobs):
-        arr[i] = _lib.FusedJob(j.dtype, j.w.handle, j.byte_off, j.n_in, j.n_out, _ptr(j.qx.q)[0],
-                               _ptr(j.qx.scales)[0], _ptr(j.qx.sums)[0])
-        arrays += [j.qx.q, j.qx.scales, j.qx.sums]
+        if j.qx is not None:
+            arr[i] = _lib.FusedJob(j.dtype, j.w.handle, j.byte_off, j.n_in, j.n_out, _ptr(j.qx.q)[0],
+                                   _ptr(j.qx.scales)[0], _ptr(j.qx.sums)[0], None)
+            arrays += [j.qx.q, j.qx.scales, j.qx.sums]
+        else:
+            arr[i] = _lib.FusedJob(j.dtype, j.w.handle, j.byte_off, j.n_in, j.n_out, None, None, None, _ptr(j.x)[0])
+            arrays += [j.x]
     loc = _same_loc(*arrays)
     check(lib().bb_matvec_fused_batch(ctx.handle, arr, len(jobs), _ptr(out)[0], loc))
     return out

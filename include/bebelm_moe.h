@@ -109,16 +109,18 @@ int bb_matvec(bb_ctx* ctx, uint32_t dtype, const bb_tensor* w, size_t byte_off, 
 int bb_matmul(bb_ctx* ctx, uint32_t dtype, const bb_tensor* w, size_t byte_off, size_t n_in, size_t n_out,
               const float* x, size_t n_tokens, float* y, int loc);
 
-/* FusedJob (kernels/matmul.rs:995-1005). Only the pre-quantised arm (`qx: Some`) is provided:
- * it is the one every MoE job takes (model.rs:507, :512, :544). */
+/* FusedJob (kernels/matmul.rs:995-1005). With qx_q set (`qx: Some`, the arm every MoE job
+ * takes, model.rs:507, :512, :544) the rows take the Q8-activation integer dot; with qx_q NULL
+ * (`qx: None`) they take the f32 fused dot over x (fused_row_dot, matmul.rs:777-785, :1045). */
 typedef struct {
   uint32_t dtype;           /* Q4_K or Q6_K                         */
   const bb_tensor* w;
   size_t byte_off;          /* first row of this job inside w       */
   size_t n_in, n_out;
-  const int8_t* qx_q;       /* Q8 of this job's x (bb_quantize_q8)  */
+  const int8_t* qx_q;       /* Q8 of this job's x (bb_quantize_q8), or NULL */
   const float* qx_scales;
   const int32_t* qx_sums;
+  const float* x;           /* f32[n_in], read when qx_q is NULL    */
 } bb_fused_job;
 /* matvec_fused_batch(jobs, out) (kernels/matmul.rs:1015): out = Σ n_out values, jobs in order. */
 int bb_matvec_fused_batch(bb_ctx* ctx, const bb_fused_job* jobs, size_t n_jobs, float* out, int loc);

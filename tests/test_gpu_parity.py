@@ -191,6 +191,30 @@ def test_fused_batch(gpu_ctx, oracle):
     assert_bits(out, want, "fused batch")
 
 
+def test_fused_batch_f32_arm(gpu_ctx, oracle):
+    # FusedJob with qx: None takes fused_row_dot (matmul.rs:777-785, :1045): jobs of both dtypes
+    # without qx, mixed with a pre-quantised one, as one call (matmul.rs:1519-1528 checks the
+    # Q4_K f32 fallback against standalone fused_row_dot rows)
+    H, F = 2048, 1792
+    wg = synth.quant_tensor(synth.rng(9, 1), Q4_K, H, F, 2)
+    wd = synth.quant_tensor(synth.rng(9, 2), Q6_K, F, H, 1)
+    tg = Tensor(gpu_ctx, Q4_K, wg, (H, F, 2))
+    td = Tensor(gpu_ctx, Q6_K, wd, (F, H, 1))
+    x = (synth.hidden_states(10, 1)[0] * 3).astype(np.float32)
+    a = synth.hidden_states(11, 1, hidden=F)[0]
+    qx = K.quantize_q8(gpu_ctx, x)
+    gs = synth.byte_size(Q4_K, H * F)
+    jobs = [K.FusedJob(Q4_K, tg, H, F, x=x, byte_off=gs), K.FusedJob(Q6_K, td, F, H, x=a),
+            K.FusedJob(Q4_K, tg, H, F, qx, byte_off=0)]
+    out = np.empty(F + H + F, np.float32)
+    K.matvec_fused_batch(gpu_ctx, jobs, out)
+    want = oracle.matvec_fused_batch([(Q4_K, wg[gs:], H, F, x, None), (Q6_K, wd, F, H, a, None),
+                                      (Q4_K, wg[:gs], H, F, x, oracle.quantize_q8(x))])
+    assert_bits(out, want, "fused batch, f32 arm")
+    rows = [oracle.fused_row_dot(Q4_K, wg[gs + o * 8 * 144:gs + (o + 1) * 8 * 144], x) for o in range(0, F, 97)]
+    assert_bits(out[0:F:97], np.array(rows, np.float32), "f32 arm == fused_row_dot")
+
+
 def test_elementwise_and_rmsnorm(gpu_ctx, oracle):
     g = np.random.default_rng(2)
     a = (g.standard_normal(5000) * 8).astype(np.float32)
