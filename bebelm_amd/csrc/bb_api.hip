@@ -473,7 +473,8 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
 }
 
 // ---- dense FFN on device pointers (model.rs:459-469 / :262-278) --------------------------------
-void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* out) {
+// xq_in (may be null): x's Q8, already computed (the decoder's fused residual + rmsnorm).
+void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* out, const bb::Q8Bufs* xq_in = nullptr) {
   const size_t H = d->H, F = d->F;
   uint8_t* base = nullptr;
   for (int pass = 0; pass < 2; ++pass) {
@@ -488,7 +489,8 @@ void dense_forward_dev(bb_ctx* c, bb_dense* d, const float* x, size_t T, float* 
       continue;
     }
     const int nz = T == 1;  // n_tokens == 1 takes matvec (-0.0-started sum), else matmul
-    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
+    if (xq_in) xq = *xq_in;
+    else launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
     if (T >= bb::PROJ_GEMM_MIN_T && d->gu.w && d->dn.w) {
       // a batch: gate, up and swiglu, then down, as grouped GEMMs of one group (matmul's sums
       // from +0.0, the same per-(row, token) values as the row kernels)
@@ -617,17 +619,19 @@ bb::Q8Bufs carve_q8(Carve& cv, size_t T, size_t n_in) {
 // form sums from -0.0 as matvec does). q: Q8 buffers for x when W is Q4_K / Q6_K.
 // With a packed form and a one-group route (rb non-null: batches of PROJ_GEMM_MIN_T tokens and
 // more) the batch runs on the grouped GEMM instead.
+// q_ready: q already holds x's Q8 (quants, scales and sums), so no quantisation is launched.
 void project_dev(bb_ctx* c, const bb_tensor* w, const bb::PackedW& pk, const bb::RouteBufs* rb, size_t n_in,
-                 size_t n_out, const float* x, size_t T, float* y, bb::Q8Bufs q) {
+                 size_t n_out, const float* x, size_t T, float* y, bb::Q8Bufs q, bool q_ready = false) {
   size_t row_bytes;
   check_weight_range(w, w->dtype, 0, n_in, n_out, row_bytes);
   if (pk.w && rb) {
-    launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, x, T, (int)n_in, q.q, q.scales); });
+    if (!q_ready)
+      launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, x, T, (int)n_in, q.q, q.scales); });
     packed_project(c, pk, n_in, n_out, T, q, *rb, y);
     return;
   }
   if (w->dtype == BB_Q4_K || w->dtype == BB_Q6_K) {
-    launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, n_in, q); });
+    if (!q_ready) launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, n_in, q); });
     launch(c, bb::K_ROWS_Q8, [&] {
       return bb::launch_rows_q8(c->stream, (int)w->dtype, w->dev, row_bytes, (int)(n_in / 256), n_out, q, n_in, T, y,
                                 n_out, T == 1);
@@ -783,6 +787,7 @@ struct bb_model {
   std::vector<Layer> layers;
   size_t pos = 0;
   float *h = nullptr, *normed = nullptr, *tmp = nullptr;
+  bb::Q8Bufs nq{};          // Q8 of normed, written with it for the conv / attention / dense layers
   uint32_t* tok = nullptr;  // token ids of the current call
   size_t cap_T = 0, tok_cap = 0;
   bb::ModelOwned owned;  // set by bb_model_load
@@ -802,7 +807,8 @@ void bb::model_adopt(bb_model* m, bb::ModelOwned&& o) { m->owned = std::move(o);
 namespace {
 
 // model.rs:399-427 (T == 1) and :190-216 (T > 1) on device pointers; state [(L-1)][H] is updated.
-void conv_forward_dev(bb_ctx* c, bb_conv_op* op, float* state, const float* x, size_t T, float* out) {
+void conv_forward_dev(bb_ctx* c, bb_conv_op* op, float* state, const float* x, size_t T, float* out,
+                      const bb::Q8Bufs* xq_in = nullptr) {
   const size_t H = op->H;
   uint8_t* base = nullptr;
   for (int pass = 0; pass < 2; ++pass) {
@@ -819,7 +825,14 @@ void conv_forward_dev(bb_ctx* c, bb_conv_op* op, float* state, const float* x, s
     bb::RouteBufs rb{};
     const bool gemm = T >= bb::PROJ_GEMM_MIN_T && (op->in_p.w || op->out_p.w);
     if (gemm) rb = one_group(c, grp, T);
-    project_dev(c, op->in_proj, op->in_p, gemm ? &rb : nullptr, H, 3 * H, x, T, bcx, xq);
+    project_dev(c, op->in_proj, op->in_p, gemm ? &rb : nullptr, H, 3 * H, x, T, bcx, xq_in ? *xq_in : xq,
+                xq_in != nullptr);
+    if (T == 1 && H % 256 == 0 && (op->out_proj->dtype == BB_Q4_K || op->out_proj->dtype == BB_Q6_K)) {
+      // one token: conv, state update and y's Q8 in one launch
+      launch(c, bb::K_CONV, [&] { return bb::launch_conv1_q8(c->stream, bcx, state, op->conv_w, (int)H, op->L, y, yq); });
+      project_dev(c, op->out_proj, op->out_p, nullptr, H, H, y, T, out, yq, true);
+      continue;
+    }
     launch(c, bb::K_CONV, [&] { return bb::launch_conv(c->stream, true, bcx, state, op->conv_w, (int)H, op->L, (int)T, y); });
     launch(c, bb::K_CONV_STATE, [&] { return bb::launch_conv_state(c->stream, true, bcx, state, (int)H, op->L, (int)T); });
     project_dev(c, op->out_proj, op->out_p, gemm ? &rb : nullptr, H, H, y, T, out, yq);
@@ -846,7 +859,8 @@ void ensure_rope(bb_ctx* c, bb_attn_op* op, size_t rows) {
 
 // model.rs:430-456 (T == 1) and :222-259 (T > 1) on device pointers: the T new keys / values
 // are projected straight into the cache rows n .. n+T-1.
-void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out) {
+void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, const float* x, size_t T, float* out,
+                      const bb::Q8Bufs* xq_in = nullptr) {
   const size_t H = op->H, NH = op->NH, NKV = op->NKV, HD = op->HD, KV = NKV * HD, QD = NH * HD;
   const size_t n0 = kv->n;
   ensure_rope(c, op, pos0 + T);
@@ -869,15 +883,19 @@ void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, c
     const bool gemm = T >= bb::PROJ_GEMM_MIN_T && (op->q_p.w || op->k_p.w || op->v_p.w || op->o_p.w);
     if (gemm) rb = one_group(c, grp, T);
     const bb::RouteBufs* rbp = gemm ? &rb : nullptr;
-    project_dev(c, op->q, op->q_p, rbp, H, QD, x, T, q, xq);
-    project_dev(c, op->k, op->k_p, rbp, H, KV, x, T, kn, xq);
-    project_dev(c, op->v, op->v_p, rbp, H, KV, x, T, vn, xq);
+    // x's Q8 (quants, scales and sums: both the row kernels and the GEMMs can read it) once for
+    // the three projections, or as given
+    const bb::Q8Bufs xqv = xq_in ? *xq_in : xq;
+    if (!xq_in && (op->q->dtype == BB_Q4_K || op->q->dtype == BB_Q6_K || op->k->dtype == BB_Q4_K ||
+                   op->k->dtype == BB_Q6_K || op->v->dtype == BB_Q4_K || op->v->dtype == BB_Q6_K))
+      launch(c, bb::K_QUANT, [&] { return bb::launch_quantize(c->stream, x, T, H, xq); });
+    project_dev(c, op->q, op->q_p, rbp, H, QD, x, T, q, xqv, true);
+    project_dev(c, op->k, op->k_p, rbp, H, KV, x, T, kn, xqv, true);
+    project_dev(c, op->v, op->v_p, rbp, H, KV, x, T, vn, xqv, true);
     const float2* rope = op->rope + pos0 * (HD / 2);
     launch(c, bb::K_NORM_ROPE, [&] {
-      return bb::launch_norm_rope(c->stream, q, (int)T, (int)NH, (int)HD, op->q_norm, op->eps, rope);
-    });
-    launch(c, bb::K_NORM_ROPE, [&] {
-      return bb::launch_norm_rope(c->stream, kn, (int)T, (int)NKV, (int)HD, op->k_norm, op->eps, rope);
+      return bb::launch_norm_rope(c->stream, q, (int)T, (int)NH, (int)HD, op->q_norm, op->eps, rope, kn, (int)NKV,
+                                  op->k_norm);
     });
     launch(c, bb::K_ATTN_SCORES, [&] {
       return bb::launch_attn_scores(c->stream, q, kv->k, (int)n0, (int)T, (int)NH, (int)NKV, (int)HD, op->scale, scores);
@@ -1859,7 +1877,8 @@ size_t model_kv_len(const bb_model* m) {
 void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
   if (T <= m->cap_T) return;
   check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-  for (void** p : {(void**)&m->h, (void**)&m->normed, (void**)&m->tmp}) {
+  for (void** p : {(void**)&m->h, (void**)&m->normed, (void**)&m->tmp, (void**)&m->nq.q, (void**)&m->nq.scales,
+                   (void**)&m->nq.sums}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
@@ -1868,6 +1887,11 @@ void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
   m->h = static_cast<float*>(dev_alloc(T * H * 4));
   m->normed = static_cast<float*>(dev_alloc(T * H * 4));
   m->tmp = static_cast<float*>(dev_alloc(T * H * 4));
+  if (H % 256 == 0) {
+    m->nq.q = static_cast<int8_t*>(dev_alloc(T * H));
+    m->nq.scales = static_cast<float*>(dev_alloc(T * H / 256 * 4));
+    m->nq.sums = static_cast<int32_t*>(dev_alloc(T * H / 32 * 4));
+  }
   m->cap_T = T;
 }
 
@@ -1900,19 +1924,41 @@ void model_run_dev(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T) {
     return bb::launch_embed(c->stream, m->tok_embd->dev, (int)m->tok_embd->dtype, m->row_bytes, tokens, (int)T, (int)H,
                             m->h);
   });
-  for (auto& L : m->layers) {
-    launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, m->h, L.attn_norm, m->eps, H, T, m->normed); });
-    if (L.conv) conv_forward_dev(c, L.conv, L.conv_state, m->normed, T, m->tmp);
-    else attn_forward_dev(c, L.attn, L.kv, m->pos, m->normed, T, m->tmp);
+  // Each layer boundary (h += sub-layer output, then the next rmsnorm) is one launch of
+  // k_residual_norm, which also writes the normed rows' Q8 when the next sub-layer projects
+  // them (conv, attention, dense FFN; the MoE route quantises its input itself).
+  const bool fused = H <= (size_t)bb::GU_H_MAX && m->nq.q;
+  auto boundary = [&](const float* gain, bool q8) {
+    if (fused) {
+      launch(c, bb::K_RESIDUAL_NORM, [&] {
+        return bb::launch_residual_norm(c->stream, m->h, nullptr, nullptr, 0, m->tmp, gain, m->eps, H, T, m->normed,
+                                        q8 && gain ? m->nq : bb::Q8Bufs{});
+      });
+      return;
+    }
     launch(c, bb::K_ELEMWISE, [&] {
       return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, m->h, m->tmp, nullptr, 0.0f, T * H);
     });
-    launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, m->h, L.ffn_norm, m->eps, H, T, m->normed); });
+    if (gain) launch(c, bb::K_RMSNORM, [&] { return bb::launch_rmsnorm(c->stream, m->h, gain, m->eps, H, T, m->normed); });
+  };
+  const bb::Q8Bufs* nq = fused ? &m->nq : nullptr;
+  const size_t n_layers = m->layers.size();
+  if (fused)
+    launch(c, bb::K_RMSNORM, [&] {
+      return bb::launch_rmsnorm_q8(c->stream, m->h, m->layers[0].attn_norm, m->eps, H, T, m->normed, m->nq);
+    });
+  else
+    launch(c, bb::K_RMSNORM, [&] {
+      return bb::launch_rmsnorm(c->stream, m->h, m->layers[0].attn_norm, m->eps, H, T, m->normed);
+    });
+  for (size_t i = 0; i < n_layers; ++i) {
+    auto& L = m->layers[i];
+    if (L.conv) conv_forward_dev(c, L.conv, L.conv_state, m->normed, T, m->tmp, nq);
+    else attn_forward_dev(c, L.attn, L.kv, m->pos, m->normed, T, m->tmp, nq);
+    boundary(L.ffn_norm, L.dense != nullptr);
     if (L.moe) moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr);
-    else dense_forward_dev(c, L.dense, m->normed, T, m->tmp);
-    launch(c, bb::K_ELEMWISE, [&] {
-      return bb::launch_elementwise(c->stream, bb::EW_ADD_ASSIGN, m->h, m->tmp, nullptr, 0.0f, T * H);
-    });
+    else dense_forward_dev(c, L.dense, m->normed, T, m->tmp, nq);
+    boundary(i + 1 < n_layers ? m->layers[i + 1].attn_norm : nullptr, true);
   }
   m->pos += T;
 }
@@ -1994,7 +2040,8 @@ int bb_model_destroy(bb_model* m) {
       if (L.conv_state) (void)hipFree(L.conv_state);
       if (L.kv) (void)bb_kv_cache_destroy(L.kv);
     }
-    for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok})
+    for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok,
+                    (void*)m->nq.q, (void*)m->nq.scales, (void*)m->nq.sums})
       if (p) (void)hipFree(p);
     bb::free_owned(m->owned);
     delete m;

@@ -233,7 +233,7 @@ hipError_t launch_rmsnorm_q8(hipStream_t s, const float* x, const float* gain, f
                              float* out, Q8Bufs q);
 // h += (slots, wts, K) combine or ffn row; then normed = rmsnorm(h, gain) unless gain is null.
 hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
-                                const float* gain, float eps, size_t n, size_t n_vec, float* normed);
+                                const float* gain, float eps, size_t n, size_t n_vec, float* normed, Q8Bufs q = Q8Bufs{});
 
 // ---- decoder-layer operators (bb_ops.hip) ----
 constexpr int OPS_HD_MAX = 256;     // head_dim bound of the attention kernels
@@ -244,9 +244,13 @@ hipError_t launch_conv(hipStream_t s, bool op, const float* src, const float* st
                        int T, float* out);
 // state <- the last L-1 columns of [state; bx] (run after launch_conv on the same batch).
 hipError_t launch_conv_state(hipStream_t s, bool op, const float* src, float* state, int C, int L, int T);
+// One token: conv, state update and the Q8 of y in one launch (C % 256 == 0; y f32[C] too).
+hipError_t launch_conv1_q8(hipStream_t s, const float* src, float* state, const float* w, int C, int L, float* y,
+                           Q8Bufs q);
 // per-head rmsnorm (gain null: none) and RoPE from (cos, sin) rows [T][hd/2], in place on buf [T][n_heads][hd].
 hipError_t launch_norm_rope(hipStream_t s, float* buf, int T, int n_heads, int hd, const float* gain, float eps,
-                            const float2* rope);
+                            const float2* rope, float* buf2 = nullptr, int n2 = 0,
+                            const float* gain2 = nullptr);
 // scores [T][n_heads][n0+T]: token t's query against cached positions j < n0 + t + 1.
 hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
                               int hd, float scale, float* scores);

@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm(const float* __restrict__ x, co
 __global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, const float* __restrict__ slots,
                                                        const float* __restrict__ wts, int K,
                                                        const float* __restrict__ ffn, const float* __restrict__ gain,
-                                                       float eps, size_t n, float* __restrict__ normed) {
+                                                       float eps, size_t n, float* __restrict__ normed, Q8Bufs q) {
   const size_t t = blockIdx.x;
   float* hv = h + t * n;
   // thread j takes elements j, j+256, ... (k_rmsnorm's order); every load is issued before the
@@ -523,6 +523,26 @@ __global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, co
   lds_barrier();
   const float scale = s_scale;
   float* ov = normed + t * n;
+  if (q.q) {
+    // the normed row's Q8 as well (k_rmsnorm's q form: a copy in LDS, one wave per 256-block)
+    __shared__ __align__(16) float s_norm[GU_H_MAX];
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const size_t i = threadIdx.x + 256 * it;
+      if (i >= n) break;
+      const float v = hr[it] * scale * gr[it];
+      s_norm[i] = v;
+      ov[i] = v;
+    }
+    lds_barrier();
+    const size_t nbk = n / QK;
+    const int lane = threadIdx.x & 63;
+    for (size_t b = threadIdx.x >> 6; b < nbk; b += 4) {
+      const float4 val = *reinterpret_cast<const float4*>(s_norm + b * QK + 4 * lane);
+      wave_quantize_block(val, q.q + t * n + b * QK, q.scales + t * nbk + b, q.sums + t * (n / 32) + b * 8);
+    }
+    return;
+  }
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     const size_t i = threadIdx.x + 256 * it;
@@ -532,10 +552,11 @@ __global__ void __launch_bounds__(256) k_residual_norm(float* __restrict__ h, co
 }
 
 hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, const float* wts, int K, const float* ffn,
-                                const float* gain, float eps, size_t n, size_t n_vec, float* normed) {
+                                const float* gain, float eps, size_t n, size_t n_vec, float* normed, Q8Bufs q) {
   if (n_vec == 0) return hipSuccess;
   if (n > (size_t)GU_H_MAX || K > 8) return hipErrorInvalidValue;  // the kernel's register tiles
-  BB_LAUNCH(k_residual_norm, dim3((unsigned)n_vec), dim3(256), 0, s, h, slots, wts, K, ffn, gain, eps, n, normed);
+  if (q.q && (!gain || n % QK != 0)) return hipErrorInvalidValue;
+  BB_LAUNCH(k_residual_norm, dim3((unsigned)n_vec), dim3(256), 0, s, h, slots, wts, K, ffn, gain, eps, n, normed, q);
   return hipGetLastError();
 }
 

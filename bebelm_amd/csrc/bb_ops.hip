@@ -78,15 +78,51 @@ hipError_t launch_conv_state(hipStream_t s, bool op, const float* src, float* st
   return hipGetLastError();
 }
 
+// One token, the whole conv step in one launch: wave w takes channels 256w..256w+255 (four per
+// lane, lane l holding 4l..4l+3): y = C·conv over [state; bx] as k_conv computes it, the state
+// shifted by one column as k_conv_state does (each channel's reads before its writes, in the
+// same thread), and the 256-block of y quantised to Q8 (quantize_q8's arithmetic) for out_proj.
+__global__ void __launch_bounds__(64) k_conv1_q8(const float* __restrict__ src, float* state,
+                                                 const float* __restrict__ w, int C, int L, float* __restrict__ y,
+                                                 Q8Bufs q) {
+  const int c0 = blockIdx.x * QK + 4 * threadIdx.x;
+  float out[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = c0 + u;
+    const float* wc = w + (size_t)c * L;
+    float sum = wc[L - 1] * conv_col<true>(src, state, C, L, L - 1, c);
+    for (int k = 0; k + 1 < L; ++k) sum += wc[k] * conv_col<true>(src, state, C, L, k, c);
+    out[u] = src[C + c] * sum;
+    for (int k = 0; k + 1 < L; ++k) state[(size_t)k * C + c] = conv_col<true>(src, state, C, L, 1 + k, c);
+  }
+  *reinterpret_cast<float4*>(y + c0) = make_float4(out[0], out[1], out[2], out[3]);
+  wave_quantize_block(make_float4(out[0], out[1], out[2], out[3]), q.q + blockIdx.x * QK, q.scales + blockIdx.x,
+                      q.sums + blockIdx.x * 8);
+}
+
+hipError_t launch_conv1_q8(hipStream_t s, const float* src, float* state, const float* w, int C, int L, float* y,
+                           Q8Bufs q) {
+  if (C % QK != 0 || L < 2 || !q.q) return hipErrorInvalidValue;
+  BB_LAUNCH(k_conv1_q8, dim3((unsigned)(C / QK)), dim3(64), 0, s, src, state, w, C, L, y, q);
+  return hipGetLastError();
+}
+
 // ---- per-head rmsnorm + RoPE -----------------------------------------------------------------
 // One 64-thread block per (token, head) of buf [T][n_heads][hd] (hd <= OPS_HD_MAX, even).
 // rope: (cos, sin) pairs [position][hd/2]; token t uses position row t of the table slice.
+// Blocks past n_heads take the heads of a second buffer (buf2: n2 heads per token, gain2), so q
+// and k are normed and rotated in one launch.
 __global__ void __launch_bounds__(64) k_norm_rope(float* buf, int n_heads, int hd, const float* __restrict__ gain,
-                                                  float eps, const float2* __restrict__ rope, int norm) {
+                                                  float eps, const float2* __restrict__ rope, int norm, float* buf2,
+                                                  int n2, const float* __restrict__ gain2) {
   __shared__ float sx[OPS_HD_MAX];
   __shared__ float s_scale;
-  const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  float* x = buf + ((size_t)t * n_heads + head) * hd;
+  const int t = blockIdx.y, lane = threadIdx.x;
+  const bool second = (int)blockIdx.x >= n_heads;
+  const int head = second ? (int)blockIdx.x - n_heads : (int)blockIdx.x;
+  if (second) gain = gain2;
+  float* x = second ? buf2 + ((size_t)t * n2 + head) * hd : buf + ((size_t)t * n_heads + head) * hd;
   for (int d = lane; d < hd; d += 64) sx[d] = x[d];
   __syncthreads();
   if (norm) {
@@ -111,8 +147,10 @@ __global__ void __launch_bounds__(64) k_norm_rope(float* buf, int n_heads, int h
 }
 
 hipError_t launch_norm_rope(hipStream_t s, float* buf, int T, int n_heads, int hd, const float* gain, float eps,
-                            const float2* rope) {
-  BB_LAUNCH(k_norm_rope, dim3(n_heads, T), dim3(64), 0, s, buf, n_heads, hd, gain, eps, rope, gain != nullptr);
+                            const float2* rope, float* buf2, int n2, const float* gain2) {
+  if (buf2 && (gain == nullptr) != (gain2 == nullptr)) return hipErrorInvalidValue;
+  BB_LAUNCH(k_norm_rope, dim3(n_heads + (buf2 ? n2 : 0), T), dim3(64), 0, s, buf, n_heads, hd, gain, eps, rope,
+            gain != nullptr, buf2, n2, gain2);
   return hipGetLastError();
 }
 
