@@ -21,6 +21,8 @@
 // The MFMA runs with the activations as the A operand and the weight rows as the B operand, so
 // every output a lane holds belongs to one weight row and the row's scales stay in the lane.
 #include "bb_device.h"
+#include <type_traits>
+
 #include "bb_internal.h"
 #include "bb_members.h"
 #include "bb_mfma.h"
@@ -241,6 +243,25 @@ __device__ void member_rows_list(const int32_t* list, const TileInfo& ti, int K,
   }
 }
 
+// Buffer resources (gfx9 raw buffers: base, byte size, word 3 = 0x00020000): loads through them
+// take a 32-bit per-lane offset and a wave-uniform one, so a lane keeps one register per stream
+// instead of a 64-bit address per load. An access at or past the size reads zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+// global_load_lds through a buffer: 16 (or 4) bytes a lane into dst + 16·lane (4·lane)
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, (int)voff, (int)soff, 0,
+                                           0);
+}
+__device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, (int)voff, (int)soff, 0,
+                                           0);
+}
+
 // ---- grouped GEMM ------------------------------------------------------------------------------
 // Block (member tile of 16*MT members, row tile = two 64-row packed tiles), 8 waves; wave w owns
 // the 16-row tile (w&3) of packed tile (w>>2) against all members of the tile. For gate/up,
@@ -374,7 +395,63 @@ __device__ __forceinline__ void plan_build(IssuePlan<DT, MT>& p, const uint8_t* 
   }
 }
 
-template <int DT, int KIND, int MT>
+// IssuePlan's copies through buffer resources: a lane's 32-bit source offset of each copy is fixed
+// and super-block b adds a wave-uniform offset (b times the stream's stride), so a copy costs no
+// vector address arithmetic. For inputs whose offsets fit 31 bits.
+template <int DT, int MT>
+struct BufPlan {
+  __amdgpu_buffer_rsrc_t rw, rx, rs;
+  uint32_t off[8];  // GemmCfg<DT, MT>::OPS <= 8 used
+
+  __device__ __forceinline__ void issue(int b, uint8_t* wb, uint8_t* xb, float* sb) {
+    using C = GemmCfg<DT, MT>;
+    constexpr int TB = C::TB;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int t = 0; t < C::OPS; ++t) {
+      const int j = w + 8 * t;
+      if (j < C::WCH) {
+        if (j * 64 + lane < C::W_UNITS) buf_dma16(rw, off[t], (uint32_t)(b * TB), wb + j * 1024);
+      } else if (j < C::WCH + C::XCH) {
+        buf_dma16(rx, off[t], (uint32_t)(b * QK), xb + (j - C::WCH) * 1024);
+      } else {
+        buf_dma4(rs, off[t], (uint32_t)(4 * b), reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH, C::SCH) * 64));
+      }
+    }
+  }
+};
+
+// w0: the block's two packed tiles (wave-uniform); x_rows: rows of x.q / x.sx.
+template <int DT, int MT>
+__device__ __forceinline__ void bufplan_build(BufPlan<DT, MT>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
+                                              int n_in, int x_rows, const int32_t* rowidx) {
+  using C = GemmCfg<DT, MT>;
+  static_assert(C::OPS <= 8, "copy plan size");
+  constexpr int TB = C::TB;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = n_in / QK;
+  p.rw = buf_rsrc(w0, (uint32_t)(2 * tile_bytes));
+  p.rx = buf_rsrc(x.q, (uint32_t)x_rows * (uint32_t)n_in);
+  p.rs = buf_rsrc(x.sx, (uint32_t)x_rows * (uint32_t)nb * 4u);
+#pragma unroll
+  for (int t = 0; t < C::OPS; ++t) {
+    const int j = w + 8 * t;
+    if (j < C::WCH) {
+      const int u = min(j * 64 + lane, C::W_UNITS - 1);
+      const int k = u / (TB / 16), o = u % (TB / 16);
+      p.off[t] = (uint32_t)(k * tile_bytes) + 16u * (uint32_t)o;
+    } else if (j < C::WCH + C::XCH) {
+      const int u = (j - C::WCH) * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
+      p.off[t] = (uint32_t)rowidx[m] * (uint32_t)n_in + 16u * (uint32_t)c;
+    } else {
+      const int i = min(j - C::WCH - C::XCH, C::SCH);
+      const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
+      p.off[t] = (uint32_t)rowidx[m] * (uint32_t)nb * 4u;
+    }
+  }
+}
+
+template <int DT, int KIND, int MT, bool BUF = false>
 __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
                                               int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
                                               float* __restrict__ out) {
@@ -466,7 +543,7 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
     }
   } else {
     if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
-    w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
+    w0 = wpk + (size_t)__builtin_amdgcn_readfirstlane(ti.e) * stride_e + (size_t)(2 * rtile) * tile_bytes;
     gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
   }
@@ -483,8 +560,13 @@ __global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, s
   lds_barrier();  // rowidx, outrow; the first block's copies stay in flight
   if (MT > 1 || !(KIND == GEMM_GATEUP && n_ent / K <= 16))
     gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
-  IssuePlan<DT, MT> plan;
-  if constexpr (MT > 1) plan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, rowidx);
+  using Plan = std::conditional_t<BUF, BufPlan<DT, MT>, IssuePlan<DT, MT>>;
+  Plan plan;
+  if constexpr (MT > 1) {
+    if constexpr (BUF) bufplan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, KIND == GEMM_GATEUP ? n_ent / K : n_ent,
+                                             rowidx);
+    else plan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, rowidx);
+  }
   for (int b = 0; b < nb; b += 2) {
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
     if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
@@ -575,25 +657,6 @@ struct WideW<DT_Q6_K> {
   uint4 sc, ql[2], qh[2];
   uint32_t d;
 };
-
-// Buffer resources (gfx9 raw buffers: base, byte size, word 3 = 0x00020000): loads through them
-// take a 32-bit per-lane offset and a wave-uniform one, so a lane keeps one register per stream
-// instead of a 64-bit address per load. An access at or past the size reads zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
-// global_load_lds through a buffer: 16 (or 4) bytes a lane into dst + 16·lane (4·lane)
-__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, (int)voff, (int)soff, 0,
-                                           0);
-}
-__device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, (int)voff, (int)soff, 0,
-                                           0);
-}
 
 // A lane's offsets in its packed tile (row = its weight row, g = its K group): the row's 16
 // bytes of a 1 KB chunk, shifted by chunk g or g & 1; Q6_K's d field of the row.
@@ -982,8 +1045,17 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   // members); else every hit expert adds at most one partial tile
   const int n_mt = mt == 1 ? E * ((T + bn - 1) / bn) : ((n_ent + bn - 1) / bn + E + 7) / 8 * 8;
   dim3 grid(n_mt, n_t64 / 2);
-  if (DT == DT_Q6_K && mt == 8)
+  // copies through buffer resources when every source offset fits 31 bits
+  const uint64_t x_rows = KIND == GEMM_GATEUP ? (uint64_t)T : (uint64_t)n_ent;
+  const uint64_t tile2 = 2ull * (uint64_t)(n_in / QK) * (uint64_t)GemmTraits<DT>::TB;
+  const bool buf = x_rows * (uint64_t)n_in < (1ull << 31) && tile2 < (1ull << 31);
+  if (DT == DT_Q6_K && mt == 8 && buf)
+    BB_LAUNCH((k_gemm<DT_Q6_K, KIND, 8, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x,
+              out);
+  else if (DT == DT_Q6_K && mt == 8)
     BB_LAUNCH((k_gemm<DT_Q6_K, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
+  else if (mt == 4 && buf)
+    BB_LAUNCH((k_gemm<DT, KIND, 4, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4)
     BB_LAUNCH((k_gemm<DT, KIND, 4>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else
