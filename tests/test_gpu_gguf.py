@@ -72,3 +72,37 @@ def test_full_size_model_from_gguf(gpu_ctx, tmp_path):
         check_caches(gm, om, "full size from GGUF")
     finally:
         gm.close()
+
+
+def test_load_rejects_bad_files(gpu_ctx):
+    # Model::load's failures (model.rs:36-67, :572-584) come back as error codes with the
+    # reference's messages, before or during the upload, and leave nothing behind
+    from bebelm_amd import _lib
+
+    mw = small_weights()
+    w = synth.model_gguf(mw)
+    w.tensors = [t for t in w.tensors if t[0] != "blk.4.attn_k.weight"]
+    with pytest.raises(gguf.BBError, match="missing tensor blk.4.attn_k.weight") as e:
+        Model.load(gpu_ctx, gguf.GgufFile.from_bytes(w.to_bytes()), 16, validate=False)
+    assert e.value.code == _lib.BB_ERR_MISSING
+
+    w = synth.model_gguf(mw)
+    i = [t[0] for t in w.tensors].index("blk.0.attn_norm.weight")
+    name, dims, ty, data = w.tensors[i]
+    w.tensors[i] = (name, dims, synth.F16, np.zeros(dims[0], np.float16))
+    with pytest.raises(gguf.BBError, match="f32 tensor not precomputed: blk.0.attn_norm.weight") as e:
+        Model.load(gpu_ctx, gguf.GgufFile.from_bytes(w.to_bytes()), 16, validate=False)
+    assert e.value.code == _lib.BB_ERR_DTYPE
+
+    w = synth.model_gguf(mw)
+    i = [t[0] for t in w.tensors].index("blk.5.ffn_up_exps.weight")
+    name, dims, ty, data = w.tensors[i]
+    w.tensors[i] = (name, [dims[0], dims[1] // 2, dims[2] * 2], ty, data)
+    with pytest.raises(gguf.BBError, match=r"tensor blk.5.ffn_up_exps.weight: shape \[512, 256, 16\] != expected"):
+        Model.load(gpu_ctx, gguf.GgufFile.from_bytes(w.to_bytes()), 16, validate=False)
+    # the context still works
+    gm = Model.load(gpu_ctx, gguf.GgufFile.from_bytes(synth.model_gguf(mw).to_bytes()), 16, validate=False)
+    try:
+        assert gm.run_layers([1, 2]).shape == (2 * mw.hidden,)
+    finally:
+        gm.close()
