@@ -3,9 +3,10 @@
 //
 // MFMA v_mfma_i32_16x16x64_i8 with the activations as A (16 members x 64 elements; lane l:
 // member l%16) and the weights as B (64 elements x 16 rows; lane l: row l%16); lane group
-// g = l/16 supplies elements 16g..16g+15 of each 64-element step for both, so a lane's weights
-// lie in one sub-block (Q4_K: 32 elements, Q6_K: 16) and its activations are one 16-byte chunk
-// of the member's row. D lane l = members 4(l/16)..+3 of row l%16.
+// g = l/16 supplies 16 consecutive elements of each 64-element step for both (Q6_K: elements
+// 64c + 16g.. of step c; Q4_K: 64g + 16s.. of step s, see q4_block), so a lane's weights of a
+// step lie in one sub-block and its activations are one 16-byte chunk of the member's row.
+// D lane l = members 4(l/16)..+3 of row l%16.
 //
 // Operands in LDS, per 256-element super-block b:
 //   weights      the packed tile-block of the 64-row tile verbatim (chunk k of lane/row j at
@@ -60,92 +61,111 @@ __device__ __forceinline__ uint32_t splat_byte(uint32_t v) { return __builtin_am
 // Q4_K: sd = Σ_j sc_j·Σ q·x with sc = 8·(sc>>3) + (sc&7): both weight products stay <= 105, so
 // the high- and low-scale passes give sd = 8·Dh + Dl; a third pass with weight m_j for every
 // element of sub-block j gives sm = Σ_j m_j·S_j. Epilogue matmul.rs:242 in the reference's order.
+//
+// The elements of a super-block are dealt to steps and lane groups g-major: step s, lane group
+// g takes elements 64g + 16s .. +15 (activation chunk 4g + s). A lane group then covers the
+// two sub-blocks of qs bytes 32g..32g+31 (dequant.rs:87-104): their low nibbles in steps 0-1
+// (sub-block 2g) and their high nibbles in steps 2-3 (sub-block 2g+1), so a lane loads two
+// 16-byte qs words per super-block instead of four and each sub-block's scale and min serve
+// two steps. The sums over the 256 elements are the same integers in any order.
+struct Q4Lane {
+  float dd, dm;
+  uint32_t hs[2], ls[2];  // sub-block 2g + h: sc >> 3, sc & 7
+  int ms[2];              // its min in every byte
+};
+
+__device__ __forceinline__ Q4Lane q4_lane(uint4 hd, int g) {
+  Q4Lane o;
+  o.dd = f16_bits_to_f32(hd.x & 0xffff);
+  o.dm = f16_bits_to_f32(hd.x >> 16);
+  // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time; sub-blocks 2g, 2g+1 lie in the
+  // dword of sub-blocks 0-3 (g < 2) or 4-7, bytes 2(g&1) and 2(g&1) + 1
+  const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
+  const uint32_t sw = g >= 2 ? (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u) : s0 & 0x3F3F3F3Fu;
+  const uint32_t mw = g >= 2 ? ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u) : s1 & 0x3F3F3F3Fu;
+  const uint32_t sh = 16 * (g & 1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t scv = (sw >> (sh + 8 * h)) & 0xffu;
+    o.hs[h] = scv >> 3;
+    o.ls[h] = scv & 7u;
+    o.ms[h] = (int)splat_byte(mw >> (sh + 8 * h));
+  }
+  return o;
+}
+
+// the weight operands of step s (h = s >> 1, a compile-time constant) from the lane's qs half
+// s & 1: its low (h = 0) or high (h = 1) nibbles times the scale of sub-block 2g + h
+__device__ __forceinline__ void q4_step_ops(const uint4 qv, int h, const Q4Lane& L, v4i& Bh, v4i& Bl) {
+  const uint32_t nsh = 4 * h;
+  const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
+                         (qv.w >> nsh) & 0x0F0F0F0Fu};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    Bh[k] = (int)mul_bytes(q[k], L.hs[h]);
+    Bl[k] = (int)mul_bytes(q[k], L.ls[h]);
+  }
+}
+
 template <int MT>
 __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
                                          float (&acc)[MT][4]) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const uint4 hd = *reinterpret_cast<const uint4*>(wt + 16 * row);
-  const float dd = f16_bits_to_f32(hd.x & 0xffff);
-  const float dm = f16_bits_to_f32(hd.x >> 16);
-  // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time
-  const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
-  const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
-  const uint32_t mw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+  const Q4Lane L = q4_lane(*reinterpret_cast<const uint4*>(wt + 16 * row), g);
+  uint4 qv[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) qv[k] = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * g + k) + 16 * row);
+  v4i Bm[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) Bm[h] = (v4i){L.ms[h], L.ms[h], L.ms[h], L.ms[h]};
   if constexpr (MT == 1) {
-    // one member tile: the operands of step c feed its three MFMAs right away (fewer live
+    // one member tile: the operands of step s feed its three MFMAs right away (fewer live
     // registers, so more blocks fit on a CU)
     v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0}, Dm = {0, 0, 0, 0};
-    const int hi = g >> 1;
-    const uint32_t nsh = 4 * hi;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int sh = 8 * (2 * (c & 1) + hi);
-      const uint4 qv = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * c + (g & 1)) + 16 * row);
-      const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
-                             (qv.w >> nsh) & 0x0F0F0F0Fu};
-      const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
-      const uint32_t hs = scv >> 3, ls = scv & 7u;
-      const int ms = (int)splat_byte(mw[c >> 1] >> sh);
-      v4i Bh, Bl, Bm;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        Bh[k] = (int)mul_bytes(q[k], hs);
-        Bl[k] = (int)mul_bytes(q[k], ls);
-        Bm[k] = ms;
-      }
-      const v4i ax = read_x16(xb, r, 4 * c + g);
+    for (int s = 0; s < 4; ++s) {
+      v4i Bh, Bl;
+      q4_step_ops(qv[s & 1], s >> 1, L, Bh, Bl);
+      const v4i ax = read_x16(xb, r, 4 * g + s);
       Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh, 0, 0, 0);
       Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl, 0, 0, 0);
-      Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm, 0, 0, 0);
+      Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm[s >> 1], Dm, 0, 0, 0);
     }
     const float4 sx4 = *reinterpret_cast<const float4*>(sb + 4 * g);
     const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int sd = 8 * Dh[i] + Dl[i];
-      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[i]));
+      const float v = sxv[i] * ((L.dd * (float)sd) - (L.dm * (float)Dm[i]));
       acc[0][i] += v;
     }
     return;
   }
   // the lane's weight operands for the whole block first, then member tile by member tile:
-  // twelve MFMAs and the tile's f32 epilogue, which is independent of the next tile's MFMAs
-  // and can issue while they run
-  v4i Bh[4], Bl[4], Bm[4];
-  const int hi = g >> 1;  // high nibbles: sub-block 2c+1
-  const uint32_t nsh = 4 * hi;
+  // twelve MFMAs, during which the next tile's activation chunks are read (each chunk once its
+  // three MFMAs are issued), and the tile's f32 epilogue
+  v4i Bh[4], Bl[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int sh = 8 * (2 * (c & 1) + hi);  // byte of sub-block 2c+hi in the scale dwords
-    const uint4 qv = *reinterpret_cast<const uint4*>(wt + 1024 * (1 + 2 * c + (g & 1)) + 16 * row);
-    const uint32_t q[4] = {(qv.x >> nsh) & 0x0F0F0F0Fu, (qv.y >> nsh) & 0x0F0F0F0Fu, (qv.z >> nsh) & 0x0F0F0F0Fu,
-                           (qv.w >> nsh) & 0x0F0F0F0Fu};
-    const uint32_t scv = (scw[c >> 1] >> sh) & 0xffu;
-    const uint32_t hs = scv >> 3, ls = scv & 7u;
-    const int ms = (int)splat_byte(mw[c >> 1] >> sh);
+  for (int s = 0; s < 4; ++s) q4_step_ops(qv[s & 1], s >> 1, L, Bh[s], Bl[s]);
+  v4i ax[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      Bh[c][k] = (int)mul_bytes(q[k], hs);
-      Bl[c][k] = (int)mul_bytes(q[k], ls);
-      Bm[c][k] = ms;
-    }
-  }
+  for (int s = 0; s < 4; ++s) ax[s] = read_x16(xb, r, 4 * g + s);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0}, Dm = {0, 0, 0, 0};
+    v4i D[3] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const v4i ax = read_x16(xb, mt * 16 + r, 4 * c + g);
-      Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh[c], Dh, 0, 0, 0);
-      Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl[c], Dl, 0, 0, 0);
-      Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm[c], Dm, 0, 0, 0);
+    for (int s = 0; s < 4; ++s) {
+      D[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bh[s], D[0], 0, 0, 0);
+      D[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bl[s], D[1], 0, 0, 0);
+      D[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bm[s >> 1], D[2], 0, 0, 0);
+      if (mt + 1 < MT) ax[s] = read_x16(xb, (mt + 1) * 16 + r, 4 * g + s);
     }
     const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
     const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int sd = 8 * Dh[i] + Dl[i];
-      const float v = sxv[i] * ((dd * (float)sd) - (dm * (float)Dm[i]));
+      const int sd = 8 * D[0][i] + D[1][i];
+      const float v = sxv[i] * ((L.dd * (float)sd) - (L.dm * (float)D[2][i]));
       acc[mt][i] += v;
     }
   }

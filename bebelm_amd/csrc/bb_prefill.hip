@@ -270,9 +270,10 @@ __device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff
 //
 // MFMA v_mfma_i32_16x16x64_i8 with the activations as A (16 members x 64 elements; lane l:
 // member l%16) and the weights as B (64 elements x 16 rows; lane l: row l%16); lane group
-// g = l/16 supplies elements 16g..16g+15 of each 64-element step for both, so a lane's weights
-// lie in one sub-block (Q4_K: 32 elements, Q6_K: 16) and its activations are one 16-byte chunk
-// of the member's row. D lane l = members 4(l/16)..+3 of row l%16.
+// g = l/16 supplies 16 consecutive elements of each 64-element step for both (the order of
+// steps and groups is bb_mfma.h's), so a lane's weights of a step lie in one sub-block and its
+// activations are one 16-byte chunk of the member's row. D lane l = members 4(l/16)..+3 of
+// row l%16.
 //
 // Super-block b's operands are copied from HBM straight into LDS (global_load_lds_dwordx4: lane
 // l's 16 bytes land at base + 16l), double-buffered, so block b+1 streams in while block b is
@@ -298,6 +299,10 @@ struct GemmCfg {
   static constexpr int OPS = (WCH + XCH + SCH + 7) / 8;
   static constexpr int SB_FLOATS = (SCH + 1) * 64;  // scales, then the spare copies' bytes
 };
+
+// Waves per SIMD the registers of k_gemm are budgeted for: two blocks of 8 waves share a CU
+// where the LDS stages leave room (Q4_K tiles of 16 and 64 members), else one.
+constexpr int gemm_waves_per_simd(int dt) { return dt == DT_Q4_K ? 4 : 2; }
 
 enum : int { ISSUE_W = 1, ISSUE_X = 2, ISSUE_ALL = 3 };
 
@@ -452,7 +457,7 @@ __device__ __forceinline__ void bufplan_build(BufPlan<DT, MT>& p, const uint8_t*
 }
 
 template <int DT, int KIND, int MT, bool BUF = false>
-__global__ void __launch_bounds__(512) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
+__global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
                                               int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
                                               float* __restrict__ out) {
   using C = GemmCfg<DT, MT>;
