@@ -80,9 +80,11 @@ __device__ __forceinline__ Q4Lane q4_lane(uint4 hd, int g) {
   o.dm = f16_bits_to_f32(hd.x >> 16);
   // get_scale_min_k4 (dequant.rs:64-72) four bytes at a time; sub-blocks 2g, 2g+1 lie in the
   // dword of sub-blocks 0-3 (g < 2) or 4-7, bytes 2(g&1) and 2(g&1) + 1
+  // (bitwise selects: the lane groups differ, and a branch would run both arms one after the other)
   const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
-  const uint32_t sw = g >= 2 ? (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u) : s0 & 0x3F3F3F3Fu;
-  const uint32_t mw = g >= 2 ? ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u) : s1 & 0x3F3F3F3Fu;
+  const uint32_t upper = 0u - (uint32_t)(g >> 1);  // all ones for g >= 2
+  const uint32_t sw = (((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)) & upper) | (s0 & 0x3F3F3F3Fu & ~upper);
+  const uint32_t mw = ((((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)) & upper) | (s1 & 0x3F3F3F3Fu & ~upper);
   const uint32_t sh = 16 * (g & 1);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {

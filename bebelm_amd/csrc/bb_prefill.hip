@@ -1022,6 +1022,178 @@ __global__ void __launch_bounds__(64 * WIDE_WAVES, 2) k_gemm_wide(const uint8_t*
 // still fills a CU's LDS alone.)
 int gemm_member_tiles(int n_ent, int E) { return n_ent >= 16 * E ? 4 : 1; }
 
+// ---- Q4_K gate/up of decode batches (at most 16 tokens): weight rows straight into registers -------
+// Work unit = one expert x 16 outputs: the gate rows 16t.. and the up rows 32 + 16t.. of a 64-row
+// packed tile (t = 0, 1), so one wave holds both values of its outputs and applies SwiGLU itself.
+// Block = GU16_WAVES waves, each on its own unit (unit = block·GU16_WAVES + wave, expert-major):
+// E = 32 experts x 112 units of F = 1792 = 512 blocks of 7 waves, two on every CU, so each CU
+// runs the same number of units (blocks of one expert's 8 units left 448 blocks, and the CUs that
+// got two did twice the work of those that got one). The member tile is every token of the batch
+// (outputs of tokens that did not choose the expert are computed and dropped), so its
+// activations do not depend on the selections: all NB super-blocks of the tokens' Q8 rows
+// (XOR-swizzled 16-byte chunks, as k_gemm stages them) and their scales are copied into LDS
+// once, at the block's start, and shared by its waves. No wave reads another wave's weight rows,
+// so a lane loads its 48 bytes per row and super-block (header and two qs words, the g-major
+// order of q4_block) straight into registers, two super-blocks ahead, through a buffer resource
+// on its packed tile (fixed per-lane offsets, the super-block's offset wave-uniform).
+// The unit's expert is known from the ids, so its first weights are requested before the
+// selections are read (a unit of an expert nobody chose wastes them and leaves). The integer
+// sums and the f32 epilogue are q4_block's, in the same order; the sum over super-blocks starts
+// at +0.0 (-0.0 for an expert with one member).
+constexpr int GU16_SLOTS = 5;  // register slots of one row tile and super-block per lane
+constexpr int GU16_WAVES = 7;
+
+// A lane's bytes of one row tile and super-block (header and its two qs words). The wave streams
+// its 2·NB (super-block, tile) halves through GU16_SLOTS register slots: half h is computed while
+// halves h+1 .. h+GU16_SLOTS-1 (two super-blocks) are in flight.
+struct Gu16H {
+  uint4 h, q0, q1;
+};
+
+__device__ __forceinline__ void gu16_load(Gu16H& v, __amdgpu_buffer_rsrc_t r, uint32_t orow, uint32_t oq, uint32_t sb) {
+  v.h = buf_load16(r, orow, sb);
+  v.q0 = buf_load16(r, orow + oq, sb);
+  v.q1 = buf_load16(r, orow + oq + 1024u, sb);
+}
+
+// One super-block of one of the wave's row tiles (header h, qs words q0 and q1) against the 16
+// tokens: q4_block's three passes and epilogue.
+__device__ __forceinline__ void gu16_tile(uint4 h, uint4 q0, uint4 q1, const uint8_t* xb, const float* sb,
+                                          float (&acc)[4]) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const Q4Lane L = q4_lane(h, g);
+  v4i Dh = {0, 0, 0, 0}, Dl = {0, 0, 0, 0}, Dm = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int hh = s >> 1;
+    const v4i ax = read_x16(xb, r, 4 * g + s);
+    v4i Bh, Bl;
+    q4_step_ops((s & 1) ? q1 : q0, hh, L, Bh, Bl);
+    const v4i Bm = {L.ms[hh], L.ms[hh], L.ms[hh], L.ms[hh]};
+    Dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bh, Dh, 0, 0, 0);
+    Dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bl, Dl, 0, 0, 0);
+    Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax, Bm, Dm, 0, 0, 0);
+  }
+  const float4 sx4 = *reinterpret_cast<const float4*>(sb + 4 * g);
+  const float sxv[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sd = 8 * Dh[i] + Dl[i];
+    acc[i] += sxv[i] * ((L.dd * (float)sd) - (L.dm * (float)Dm[i]));
+  }
+}
+
+template <int NB>
+__global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* __restrict__ wpk, size_t stride_e,
+                                                                int E, int K, int n_out, int n_tok,
+                                                                const int32_t* __restrict__ sel, GemmX x,
+                                                                float* __restrict__ out) {
+  constexpr int TB = (int)TB4;
+  constexpr int XB = 16 * QK;  // one super-block of the 16 tokens' quants
+  constexpr int NW = GU16_WAVES;
+  constexpr int NC = (4 * NB + NW - 1) / NW;  // activation copies per wave
+  __shared__ __align__(16) uint8_t xs[NB * XB];
+  __shared__ __align__(16) float sxs[NW * 64];  // scales [b][16] (waves 0-1); the rest absorbs copies
+  __shared__ uint64_t exptab[NW * 32];
+  __shared__ int32_t selw[NW * 64];
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_ot = n_out / 16;                 // units per expert
+  const int unit = blockIdx.x * NW + w;
+  const bool real = unit < E * n_ot;
+  const int e = real ? unit / n_ot : 0, o = real ? unit % n_ot : 0;
+  const int n_ent = n_tok * K;
+  {
+    // the exp table of the SwiGLU (32 x 8 bytes) and the selections (T*K <= 64 entries; their
+    // workspace slot holds 64) into the wave's own LDS slots
+    lds_dma4(reinterpret_cast<const uint8_t*>(bb_exp2f_tab_dev) + 4 * lane,
+             reinterpret_cast<uint8_t*>(exptab + 32 * w));
+    lds_dma4(reinterpret_cast<const uint8_t*>(sel + lane), reinterpret_cast<uint8_t*>(selw + 64 * w));
+    // activation copies: NB super-blocks x 4 KB as 4·NB wave copies of 1 KB, copy j = super-block
+    // j/4, tokens 4(j%4)..+3; wave w issues copies w, w+NW, ... (NC per wave; repeats of the last
+    // copy rewrite the same bytes)
+    const int m = lane >> 4, p = lane & 15;
+#pragma unroll
+    for (int t = 0; t < NC; ++t) {
+      const int j = min(w + NW * t, 4 * NB - 1);
+      const int b = j >> 2, mm = 4 * (j & 3) + m;
+      const int row = min(mm, n_tok - 1);
+      lds_dma16(reinterpret_cast<const uint8_t*>(x.q) + (size_t)row * (NB * QK) + b * QK + 16 * (p ^ mm),
+                xs + j * 1024);
+    }
+    // scales: wave w < 2 copies entries 64w.. of [b][16]; the others copy into spare space
+    const int u = min(64 * w + lane, 16 * NB - 1);
+    const int row = min(u & 15, n_tok - 1);
+    lds_dma4(reinterpret_cast<const uint8_t*>(x.sx + (size_t)row * NB + (u >> 4)),
+             reinterpret_cast<uint8_t*>(sxs + 64 * w));
+  }
+  __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads (vmcnt below)
+  const int t64 = o >> 1, t16 = o & 1;
+  const size_t tile_bytes = (size_t)NB * TB;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      buf_rsrc(wpk + (size_t)e * stride_e + (size_t)t64 * tile_bytes, real ? (uint32_t)tile_bytes : 0u);
+  // half h = (super-block h/2, row tile h%2: gate rows 16·t16.., up rows 32 + 16·t16..)
+  const uint32_t og = 16u * (uint32_t)(16 * t16 + r), oq = 1024u * (uint32_t)(1 + 2 * g);
+  constexpr int NH = 2 * NB, AHEAD = GU16_SLOTS - 1;
+  auto half_load = [&](Gu16H& v, int h) { gu16_load(v, rsrc, og + 512u * (uint32_t)(h & 1), oq, (uint32_t)((h >> 1) * TB)); };
+  Gu16H wr[GU16_SLOTS];
+#pragma unroll
+  for (int h = 0; h < AHEAD; ++h)
+    if (h < NH) half_load(wr[h], h);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wave's copies landed (the weight loads issued after them may still be in flight)
+  constexpr int WL = 3 * (AHEAD < NH ? AHEAD : NH);
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
+  lds_barrier();
+  // the expert's entries (entry i = token·K + slot on lane i), the entries of smaller expert ids
+  // (the first group position of its members) and each token's group position
+  const int sv = lane < n_ent ? selw[64 * w + lane] : -1;
+  const unsigned long long me = __ballot(sv == e);
+  const int cnt = __popcll(me);
+  if (!real || cnt == 0) {
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+    return;
+  }
+  const int base = __popcll(__ballot(sv >= 0 && sv < e));
+  const unsigned long long kmask = K >= 64 ? ~0ull : (1ull << K) - 1ull;
+  int orow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = 4 * g + i;
+    orow[i] = -1;
+    if (n < n_tok) {
+      const unsigned long long bits = (me >> (n * K)) & kmask;
+      if (bits) {
+        const int ii = n * K + __builtin_ctzll(bits);
+        orow[i] = base + __popcll(me & ((1ull << ii) - 1ull));
+      }
+    }
+  }
+  const float start = cnt > 1 ? 0.0f : -0.0f;
+  float acc[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[t][i] = start;
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    // the slot half h-1 used takes half h+AHEAD
+    if (h + AHEAD < NH) half_load(wr[(h + AHEAD) % GU16_SLOTS], h + AHEAD);
+    __builtin_amdgcn_sched_barrier(0);
+    const Gu16H& cur = wr[h % GU16_SLOTS];
+    gu16_tile(cur.h, cur.q0, cur.q1, xs + (h >> 1) * XB, sxs + 16 * (h >> 1), acc[h & 1]);
+    // the sums are formed here (the compiler would otherwise sink every super-block's epilogue
+    // into the conditional stores below and keep all their integer sums live)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[h & 1][i]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (orow[i] >= 0)
+      out[(size_t)orow[i] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[0][i], exptab + 32 * w) * acc[1][i];
+}
+
 // Q6_K down GEMMs whose groups hold this many members on average take k_gemm_wide (blocks of up
 // to 256 members). For config 4 (4096 tokens, Zipf-skewed groups) it runs the Q6_K down GEMM in
 // 228 µs against k_gemm's 274; the Q4_K gate/up GEMM, whose 3-pass epilogue and operand build
@@ -1045,6 +1217,17 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
     }
   }
   const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
+  if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
+    // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048)
+    if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && E <= 32 && n_out % 32 == 0 && (n_in == 2048 || n_in == 512)) {
+      const dim3 grid((E * (n_out / 16) + GU16_WAVES - 1) / GU16_WAVES), block(64 * GU16_WAVES);
+      if (n_in == 2048)
+        BB_LAUNCH(k_gateup16<8>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out);
+      else
+        BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out);
+      return hipGetLastError();
+    }
+  }
   const int bn = 16 * mt;
   // enough member tiles: with tiles of 16, ceil(T/16) per expert (an expert has at most T
   // members); else every hit expert adds at most one partial tile
