@@ -591,25 +591,46 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
     block(wb1, xb1, sb1);
   }
   if constexpr (KIND == GEMM_GATEUP) {
-    // the up waves hand their values to the gate waves of the same outputs
+    // SwiGLU of the wave pair (gate rows t16, up rows t16 + 2 of the same outputs): the gate wave
+    // takes member tiles mt < MG, the up wave the rest; each hands the other its values of the
+    // other's tiles through LDS
+    constexpr int MG = MT - MT / 2;
     __syncthreads();
-    float* upv = reinterpret_cast<float*>(xb0);  // 4 up waves x MT*4 values x 64 lanes = sizeof xb0
+    float* upv = reinterpret_cast<float*>(xb0);  // 4 up waves x MG*4 values x 64 lanes <= sizeof xb0
+    float* gtv = reinterpret_cast<float*>(xb1);  // 4 gate waves x (MT-MG)*4 values x 64 lanes
+    const int pair = k64 * 2 + (t16 & 1);
     if (t16 >= 2) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MG; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) upv[((k64 * 2 + (t16 - 2)) * (4 * MT) + mt * 4 + i) * 64 + lane] = acc[mt][i];
+        for (int i = 0; i < 4; ++i) upv[(pair * (4 * MG) + mt * 4 + i) * 64 + lane] = acc[mt][i];
+    } else {
+#pragma unroll
+      for (int mt = MG; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gtv[(pair * (4 * (MT - MG)) + (mt - MG) * 4 + i) * 64 + lane] = acc[mt][i];
     }
     __syncthreads();
+    const int col = 32 * t64 + 16 * (t16 & 1) + r;
     if (t16 < 2) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MG; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int n = mt * 16 + 4 * g + i;
           if (outrow[n] < 0) continue;
-          const float up = upv[((k64 * 2 + t16) * (4 * MT) + mt * 4 + i) * 64 + lane];
-          out[(size_t)outrow[n] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[mt][i], exptab) * up;
+          const float up = upv[(pair * (4 * MG) + mt * 4 + i) * 64 + lane];
+          out[(size_t)outrow[n] * n_out + col] = silu_tab(acc[mt][i], exptab) * up;
+        }
+    } else {
+#pragma unroll
+      for (int mt = MG; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = mt * 16 + 4 * g + i;
+          if (outrow[n] < 0) continue;
+          const float gate = gtv[(pair * (4 * (MT - MG)) + (mt - MG) * 4 + i) * 64 + lane];
+          out[(size_t)outrow[n] * n_out + col] = silu_tab(gate, exptab) * acc[mt][i];
         }
     }
   } else {
