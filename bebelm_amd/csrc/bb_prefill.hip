@@ -1237,7 +1237,10 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
       return hipGetLastError();
     }
   }
-  const int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
+  int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
+  // Q4_K groups of 48+ members on average: member tiles of 80 (groups of 64 +- 8 then take one
+  // tile where tiles of 64 often took a second one nearly empty)
+  if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E) mt = 5;
   if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
     // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048)
     if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && E <= 32 && n_out % 32 == 0 && (n_in == 2048 || n_in == 512)) {
@@ -1263,6 +1266,11 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
               out);
   else if (DT == DT_Q6_K && mt == 8)
     BB_LAUNCH((k_gemm<DT_Q6_K, KIND, 8>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
+  else if (DT == DT_Q4_K && mt == 5 && buf)
+    BB_LAUNCH((k_gemm<DT_Q4_K, KIND, 5, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x,
+              out);
+  else if (DT == DT_Q4_K && mt == 5)
+    BB_LAUNCH((k_gemm<DT_Q4_K, KIND, 5>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4 && buf)
     BB_LAUNCH((k_gemm<DT, KIND, 4, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4)
