@@ -558,10 +558,6 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[mt][i] = start;
-  auto block = [&](const uint8_t* wb, const uint8_t* xb, const float* sb) {
-    if constexpr (DT == DT_Q4_K) q4_block<MT>(wb + wo, xb, sb, row, acc);
-    else q6_block<MT>(wb + wo, xb, sb, row, acc);
-  };
   lds_barrier();  // rowidx, outrow; the first block's copies stay in flight
   if (MT > 1 || !(KIND == GEMM_GATEUP && n_ent / K <= 16))
     gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
@@ -572,23 +568,40 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
                                              rowidx);
     else plan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, rowidx);
   }
-  for (int b = 0; b < nb; b += 2) {
-    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
-    if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
-    __syncthreads();
-    if (b + 1 < nb) {
-      if constexpr (MT > 1) plan.issue(b + 1, wb1, xb1, sb1);
-      else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+  // The super-block loop over the first M member tiles (the copies still bring all MT).
+  auto sweep = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    float(&am)[M][4] = reinterpret_cast<float(&)[M][4]>(acc);
+    auto block = [&](const uint8_t* wb, const uint8_t* xb, const float* sb) {
+      if constexpr (DT == DT_Q4_K) q4_block<M>(wb + wo, xb, sb, row, am);
+      else q6_block<M>(wb + wo, xb, sb, row, am);
+    };
+    for (int b = 0; b < nb; b += 2) {
+      __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): this wave's copies into buffer 0 landed
+      if (KIND == GEMM_GATEUP && b == 0 && tid < 32) exptab[tid] = exp_e;
+      __syncthreads();
+      if (b + 1 < nb) {
+        if constexpr (MT > 1) plan.issue(b + 1, wb1, xb1, sb1);
+        else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+      }
+      block(wb0, xb0, sb0);
+      if (b + 1 >= nb) break;
+      __builtin_amdgcn_s_waitcnt(0x3f70);
+      __syncthreads();
+      if (b + 2 < nb) {
+        if constexpr (MT > 1) plan.issue(b + 2, wb0, xb0, sb0);
+        else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+      }
+      block(wb1, xb1, sb1);
     }
-    block(wb0, xb0, sb0);
-    if (b + 1 >= nb) break;
-    __builtin_amdgcn_s_waitcnt(0x3f70);
-    __syncthreads();
-    if (b + 2 < nb) {
-      if constexpr (MT > 1) plan.issue(b + 2, wb0, xb0, sb0);
-      else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
-    }
-    block(wb1, xb1, sb1);
+  };
+  // A tile of MT = 5 that holds at most 64 members computes only its first 4 member tiles (the
+  // others' outputs are not stored), so it costs what a tile of 64 does.
+  if constexpr (MT == 5) {
+    if (__builtin_amdgcn_readfirstlane(ti.cnt) <= 64) sweep(std::integral_constant<int, 4>{});
+    else sweep(std::integral_constant<int, 5>{});
+  } else {
+    sweep(std::integral_constant<int, MT>{});
   }
   if constexpr (KIND == GEMM_GATEUP) {
     // SwiGLU of the wave pair (gate rows t16, up rows t16 + 2 of the same outputs): the gate wave
@@ -1239,8 +1252,10 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   }
   int mt = DT == DT_Q6_K && n_ent >= 128 * E ? 8 : gemm_member_tiles(n_ent, E);
   // Q4_K groups of 48+ members on average: member tiles of 80 (groups of 64 +- 8 then take one
-  // tile where tiles of 64 often took a second one nearly empty)
-  if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E) mt = 5;
+  // tile where tiles of 64 often took a second one nearly empty); one group of known size takes
+  // the tile that pads it less
+  if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E)
+    mt = E > 1 || (n_ent + 79) / 80 * 5 < (n_ent + 63) / 64 * 4 ? 5 : 4;
   if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
     // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048)
     if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && E <= 32 && n_out % 32 == 0 && (n_in == 2048 || n_in == 512)) {
