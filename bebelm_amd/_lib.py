@@ -111,17 +111,19 @@ _SIGS = {
                                   c_size_t, c_float, c_float, P(c_void_p)]),
     "bb_attn_op_destroy": (c_int, [c_void_p]),
     "bb_attn_op_forward": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_int]),
-    "bb_model_create": (c_int, [c_void_p, c_void_p, c_void_p, P(DecoderLayer), c_size_t, c_float, c_size_t,
-                                P(c_void_p)]),
+    "bb_model_create": (c_int, [c_void_p, c_void_p, c_void_p, P(DecoderLayer), c_size_t, c_float, P(c_void_p)]),
     "bb_model_destroy": (c_int, [c_void_p]),
-    "bb_model_reset": (c_int, [c_void_p, c_void_p]),
-    "bb_model_position": (c_int, [c_void_p, P(c_size_t)]),
-    "bb_model_kv_length": (c_int, [c_void_p, P(c_size_t)]),
-    "bb_model_layer_state": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_int]),
-    "bb_model_run_layers": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_int]),
-    "bb_model_forward_step": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_int]),
-    "bb_model_absorb": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
-    "bb_model_evict_front": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "bb_cache_create": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
+    "bb_cache_clone": (c_int, [c_void_p, c_void_p, P(c_void_p)]),
+    "bb_cache_destroy": (c_int, [c_void_p]),
+    "bb_cache_reset": (c_int, [c_void_p, c_void_p]),
+    "bb_cache_position": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_cache_kv_length": (c_int, [c_void_p, P(c_size_t)]),
+    "bb_cache_evict_front": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "bb_cache_layer_state": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_int]),
+    "bb_model_run_layers": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p, c_int]),
+    "bb_model_forward_step": (c_int, [c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_int]),
+    "bb_model_absorb": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
     "bb_gguf_open": (c_int, [ctypes.c_char_p, P(c_void_p)]),
     "bb_gguf_open_bytes": (c_int, [c_void_p, c_size_t, P(c_void_p)]),
     "bb_gguf_close": (c_int, [c_void_p]),
@@ -140,7 +142,7 @@ _SIGS = {
     "bb_gguf_validate": (c_int, [c_void_p]),
     "bb_gguf_check_tensors": (c_int, [c_void_p, P(c_size_t)]),
     "bb_gguf_upload": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
-    "bb_model_load": (c_int, [c_void_p, c_void_p, c_size_t, P(c_void_p)]),
+    "bb_model_load": (c_int, [c_void_p, c_void_p, P(c_void_p)]),
 }
 
 _lib = None

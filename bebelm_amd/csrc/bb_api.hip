@@ -355,8 +355,9 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegi
       w.aq_sx = cv.take<float>(T * K * F / 256);
     }
     if (pass == 0) {
+      // the scratch area keeps the PAD bytes of tail slack every dev_alloc'd workspace has
       if (fixed)
-        need(cv.off <= fixed->cap, BB_ERR_RANGE,
+        need(cv.off + PAD <= fixed->cap, BB_ERR_RANGE,
              "the call's workspace exceeds the allocation-free scratch area (BB_NOALLOC_SCRATCH_BYTES)");
       else
         ensure_ws(c, cv.off);
@@ -765,8 +766,10 @@ struct bb_attn_op {
   size_t rope_rows = 0;
 };
 
-// The decoder (Model, model.rs:25-31, with the Cache of cache.rs:10-19): embedding, layers of
-// (attn_norm, conv or attention operator, ffn_norm, dense or MoE FFN), final norm and logits.
+// The decoder's weights (Model, model.rs:25-31): embedding, layers of (attn_norm, conv or
+// attention operator, ffn_norm, dense or MoE FFN), final norm and logits. Immutable once built;
+// the decode-time state lives in bb_cache. The buffers below are per-call scratch of the
+// model's context (its calls are ordered on that context's stream).
 struct bb_model {
   bb_ctx* ctx;
   const bb_tensor* tok_embd;
@@ -781,16 +784,24 @@ struct bb_model {
     bb_attn_op* attn;
     bb_moe* moe;
     bb_dense* dense;
-    float* conv_state;  // conv layers: [(L-1)][H]
-    bb_kv_cache* kv;    // attention layers
   };
   std::vector<Layer> layers;
-  size_t pos = 0;
   float *h = nullptr, *normed = nullptr, *tmp = nullptr;
   bb::Q8Bufs nq{};          // Q8 of normed, written with it for the conv / attention / dense layers
   uint32_t* tok = nullptr;  // token ids of the current call
   size_t cap_T = 0, tok_cap = 0;
   bb::ModelOwned owned;  // set by bb_model_load
+};
+
+// Decode-time state of one conversation (Cache, cache.rs:10-19) for the layers of one model:
+// a conv state per conv layer, a device KV cache per attention layer (grown on demand, as the
+// reference's Vec histories grow), and the next token's position.
+struct bb_cache {
+  bb_ctx* ctx;
+  const bb_model* model;
+  std::vector<float*> conv;       // per layer: [(L-1)][H] for conv layers, else null
+  std::vector<bb_kv_cache*> kv;   // per layer: attention layers, else null
+  size_t pos = 0;
 };
 
 void bb::free_owned(bb::ModelOwned& o) {
@@ -1765,8 +1776,9 @@ int bb_kv_cache_evict_front(bb_ctx* c, bb_kv_cache* kv, size_t n) {
     need_ctx(c);
     need(kv != nullptr && kv->ctx == c, BB_ERR_ARG, "bad cache");
     set_device(c);
-    if (n == 0) return;
-    if (n >= kv->n) {
+    // a history shorter than n positions is left as it is (cache.rs:44: `if k.len() >= drop`)
+    if (n == 0 || n > kv->n) return;
+    if (n == kv->n) {
       kv->n = 0;
       return;
     }
@@ -1867,11 +1879,41 @@ int bb_attn_op_forward(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, 
 // ---- the decoder ---------------------------------------------------------------------------------
 namespace {
 
-size_t model_kv_len(const bb_model* m) {
+// Cache::kv_len (cache.rs:32-35): the longest attention layer's history.
+size_t cache_kv_len(const bb_cache* k) {
   size_t n = 0;
-  for (const auto& L : m->layers)
-    if (L.kv) n = std::max(n, L.kv->n);
+  for (const bb_kv_cache* kv : k->kv)
+    if (kv) n = std::max(n, kv->n);
   return n;
+}
+
+// Room for `want` positions in one layer's KV history: the reference appends to growing Vecs,
+// so a full cache grows (to at least twice its capacity) instead of failing. The n cached
+// positions are copied into the new arrays on the context's stream, which is drained before
+// the old arrays are freed.
+void kv_reserve(bb_ctx* c, bb_kv_cache* kv, size_t want) {
+  if (want <= kv->cap) return;
+  const size_t cap = std::max(want, 2 * kv->cap);
+  need(kv->kv_dim * cap < (1u << 29), BB_ERR_RANGE, "KV cache above 2 GB per array");
+  float* nk = static_cast<float*>(dev_alloc(kv->kv_dim * cap * 4));
+  float* nv = nullptr;
+  try {
+    nv = static_cast<float*>(dev_alloc(kv->kv_dim * cap * 4));
+  } catch (...) {
+    (void)hipFree(nk);
+    throw;
+  }
+  const size_t bytes = kv->n * kv->kv_dim * 4;
+  if (bytes) {
+    check_hip(hipMemcpyAsync(nk, kv->k, bytes, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+    check_hip(hipMemcpyAsync(nv, kv->v, bytes, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+  }
+  check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  (void)hipFree(kv->k);
+  (void)hipFree(kv->v);
+  kv->k = nk;
+  kv->v = nv;
+  kv->cap = cap;
 }
 
 void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
@@ -1913,11 +1955,11 @@ const uint32_t* model_tokens(bb_ctx* c, bb_model* m, const uint32_t* host, size_
 }
 
 // Model::run_layers (T == 1, model.rs:105-130) / run_layers_batch (T > 1, :146-181): embeds
-// the tokens (device ids) at positions pos.., runs every layer (updating the conv states and
-// KV caches) and leaves the final hidden states in m->h.
-void model_run_dev(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T) {
-  for (const auto& L : m->layers)
-    if (L.kv) need(L.kv->n + T <= L.kv->cap, BB_ERR_RANGE, "a KV cache is full (evict positions first)");
+// the tokens (device ids) at positions k->pos.., runs every layer (updating the cache's conv
+// states and KV histories) and leaves the final hidden states in m->h.
+void model_run_dev(bb_ctx* c, bb_model* m, bb_cache* k, const uint32_t* tokens, size_t T) {
+  for (bb_kv_cache* kv : k->kv)
+    if (kv) kv_reserve(c, kv, kv->n + T);
   model_buffers(c, m, T);
   const size_t H = m->H;
   launch(c, bb::K_EMBED, [&] {
@@ -1953,26 +1995,74 @@ void model_run_dev(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T) {
     });
   for (size_t i = 0; i < n_layers; ++i) {
     auto& L = m->layers[i];
-    if (L.conv) conv_forward_dev(c, L.conv, L.conv_state, m->normed, T, m->tmp, nq);
-    else attn_forward_dev(c, L.attn, L.kv, m->pos, m->normed, T, m->tmp, nq);
+    if (L.conv) conv_forward_dev(c, L.conv, k->conv[i], m->normed, T, m->tmp, nq);
+    else attn_forward_dev(c, L.attn, k->kv[i], k->pos, m->normed, T, m->tmp, nq);
     boundary(L.ffn_norm, L.dense != nullptr);
     if (L.moe) moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr);
     else dense_forward_dev(c, L.dense, m->normed, T, m->tmp, nq);
     boundary(i + 1 < n_layers ? m->layers[i + 1].attn_norm : nullptr, true);
   }
-  m->pos += T;
+  k->pos += T;
 }
 
-void model_evict(bb_ctx* c, bb_model* m, size_t n) {
+// Cache::evict_front (cache.rs:40-50) on every attention layer.
+void cache_evict(bb_ctx* c, bb_cache* k, size_t n) {
   if (n == 0) return;
-  for (auto& L : m->layers)
-    if (L.kv) check_code(bb_kv_cache_evict_front(c, L.kv, n));
+  for (bb_kv_cache* kv : k->kv)
+    if (kv) check_code(bb_kv_cache_evict_front(c, kv, n));
+}
+
+// Cache::new (cache.rs:21-28) for the layers of m: conv states zeroed, empty KV histories.
+void cache_clear(bb_ctx* c, bb_cache* k) {
+  const bb_model* m = k->model;
+  for (size_t i = 0; i < m->layers.size(); ++i) {
+    if (k->conv[i]) {
+      float* st = k->conv[i];
+      const size_t n = (size_t)(m->layers[i].conv->L - 1) * m->H;
+      launch(c, bb::K_ELEMWISE, [&] { return bb::launch_zero(c->stream, st, n); });
+    }
+    if (k->kv[i]) k->kv[i]->n = 0;
+  }
+  k->pos = 0;
+}
+
+void cache_free(bb_cache* k) {
+  for (float* p : k->conv)
+    if (p) (void)hipFree(p);
+  for (bb_kv_cache* kv : k->kv)
+    if (kv) (void)bb_kv_cache_destroy(kv);
+  delete k;
+}
+
+// A cache of m's layout: conv states and KV histories allocated, contents not yet set.
+bb_cache* cache_alloc(bb_ctx* c, const bb_model* m, size_t kv_capacity) {
+  auto* k = new bb_cache();
+  k->ctx = c;
+  k->model = m;
+  k->conv.assign(m->layers.size(), nullptr);
+  k->kv.assign(m->layers.size(), nullptr);
+  try {
+    for (size_t i = 0; i < m->layers.size(); ++i) {
+      const auto& L = m->layers[i];
+      if (L.conv) k->conv[i] = static_cast<float*>(dev_alloc((size_t)(L.conv->L - 1) * m->H * 4));
+      else check_code(bb_kv_cache_create(c, (size_t)L.attn->NKV * L.attn->HD, kv_capacity, &k->kv[i]));
+    }
+  } catch (...) {
+    cache_free(k);
+    throw;
+  }
+  return k;
+}
+
+void need_model_cache(bb_ctx* c, const bb_model* m, const bb_cache* k) {
+  need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+  need(k != nullptr && k->model == m && k->ctx == c, BB_ERR_ARG, "the cache belongs to another model or context");
 }
 
 }  // namespace
 
 int bb_model_create(bb_ctx* c, const bb_tensor* token_embd, const float* final_norm, const bb_decoder_layer* layers,
-                    size_t n_layers, float eps, size_t kv_capacity, bb_model** out) {
+                    size_t n_layers, float eps, bb_model** out) {
   return guard([&] {
     need_ctx(c);
     need(token_embd && final_norm && layers && out && n_layers > 0, BB_ERR_ARG, "null argument");
@@ -1980,7 +2070,6 @@ int bb_model_create(bb_ctx* c, const bb_tensor* token_embd, const float* final_n
     const size_t H = token_embd->dims[0], V = token_embd->dims[1];
     size_t be, bb_;
     need(block_of(token_embd->dtype, be, bb_) && H % be == 0, BB_ERR_DTYPE, "unsupported token_embd dtype or shape");
-    need(kv_capacity >= 1, BB_ERR_ARG, "kv_capacity must be >= 1");
     for (size_t i = 0; i < n_layers; ++i) {
       const bb_decoder_layer& D = layers[i];
       need(D.attn_norm && D.ffn_norm, BB_ERR_ARG, "layer norms must be set");
@@ -2013,13 +2102,6 @@ int bb_model_create(bb_ctx* c, const bb_tensor* token_embd, const float* final_n
         bb_model::Layer& B = m->layers.back();
         B.attn_norm = upload_f32(c, D.attn_norm, H);
         B.ffn_norm = upload_f32(c, D.ffn_norm, H);
-        if (D.conv) {
-          const size_t n = (size_t)(D.conv->L - 1) * H;
-          B.conv_state = static_cast<float*>(dev_alloc(n * 4));
-          clear_dev(c, B.conv_state, n * 4);
-        } else {
-          check_code(bb_kv_cache_create(c, (size_t)D.attn->NKV * D.attn->HD, kv_capacity, &B.kv));
-        }
       }
     } catch (...) {
       (void)bb_model_destroy(m);
@@ -2037,8 +2119,6 @@ int bb_model_destroy(bb_model* m) {
     for (auto& L : m->layers) {
       if (L.attn_norm) (void)hipFree(L.attn_norm);
       if (L.ffn_norm) (void)hipFree(L.ffn_norm);
-      if (L.conv_state) (void)hipFree(L.conv_state);
-      if (L.kv) (void)bb_kv_cache_destroy(L.kv);
     }
     for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok,
                     (void*)m->nq.q, (void*)m->nq.scales, (void*)m->nq.sums})
@@ -2048,109 +2128,180 @@ int bb_model_destroy(bb_model* m) {
   });
 }
 
-int bb_model_reset(bb_ctx* c, bb_model* m) {
+int bb_cache_create(bb_ctx* c, const bb_model* m, size_t kv_capacity, bb_cache** out) {
   return guard([&] {
     need_ctx(c);
     need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need(out != nullptr, BB_ERR_ARG, "null argument");
+    need(kv_capacity >= 1, BB_ERR_ARG, "kv_capacity must be >= 1");
     set_device(c);
-    for (auto& L : m->layers) {
-      if (L.conv_state)
-        launch(c, bb::K_ELEMWISE, [&] { return bb::launch_zero(c->stream, L.conv_state, (size_t)(L.conv->L - 1) * m->H); });
-      if (L.kv) L.kv->n = 0;
+    bb_cache* k = cache_alloc(c, m, kv_capacity);
+    try {
+      cache_clear(c, k);
+      check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    } catch (...) {
+      cache_free(k);
+      throw;
     }
-    m->pos = 0;
+    *out = k;
   });
 }
 
-int bb_model_position(const bb_model* m, size_t* pos) {
-  return guard([&] {
-    need(m != nullptr && pos != nullptr, BB_ERR_ARG, "null argument");
-    *pos = m->pos;
-  });
-}
-
-int bb_model_kv_length(const bb_model* m, size_t* n) {
-  return guard([&] {
-    need(m != nullptr && n != nullptr, BB_ERR_ARG, "null argument");
-    *n = model_kv_len(m);
-  });
-}
-
-int bb_model_layer_state(bb_ctx* c, const bb_model* m, size_t layer, float* conv_state, float* k, float* v, int loc) {
+int bb_cache_clone(bb_ctx* c, const bb_cache* src, bb_cache** out) {
   return guard([&] {
     need_ctx(c);
-    need(m != nullptr && m->ctx == c && layer < m->layers.size(), BB_ERR_ARG, "bad model or layer");
+    need(src != nullptr && src->ctx == c, BB_ERR_ARG, "bad cache");
+    need(out != nullptr, BB_ERR_ARG, "null argument");
+    set_device(c);
+    const bb_model* m = src->model;
+    size_t cap = 1;
+    for (const bb_kv_cache* kv : src->kv)
+      if (kv) cap = std::max(cap, kv->cap);
+    bb_cache* k = cache_alloc(c, m, cap);
+    try {
+      for (size_t i = 0; i < m->layers.size(); ++i) {
+        if (src->conv[i])
+          check_hip(hipMemcpyAsync(k->conv[i], src->conv[i], (size_t)(m->layers[i].conv->L - 1) * m->H * 4,
+                                   hipMemcpyDeviceToDevice, c->stream),
+                    "cache copy");
+        if (src->kv[i]) {
+          const bb_kv_cache* a = src->kv[i];
+          bb_kv_cache* b = k->kv[i];
+          const size_t bytes = a->n * a->kv_dim * 4;
+          if (bytes) {
+            check_hip(hipMemcpyAsync(b->k, a->k, bytes, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+            check_hip(hipMemcpyAsync(b->v, a->v, bytes, hipMemcpyDeviceToDevice, c->stream), "cache copy");
+          }
+          b->n = a->n;
+        }
+      }
+      k->pos = src->pos;
+      check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    } catch (...) {
+      cache_free(k);
+      throw;
+    }
+    *out = k;
+  });
+}
+
+int bb_cache_destroy(bb_cache* k) {
+  return guard([&] {
+    if (!k) return;
+    set_device(k->ctx);
+    (void)hipStreamSynchronize(k->ctx->stream);
+    cache_free(k);
+  });
+}
+
+int bb_cache_reset(bb_ctx* c, bb_cache* k) {
+  return guard([&] {
+    need_ctx(c);
+    need(k != nullptr && k->ctx == c, BB_ERR_ARG, "bad cache");
+    set_device(c);
+    cache_clear(c, k);
+  });
+}
+
+int bb_cache_position(const bb_cache* k, size_t* pos) {
+  return guard([&] {
+    need(k != nullptr && pos != nullptr, BB_ERR_ARG, "null argument");
+    *pos = k->pos;
+  });
+}
+
+int bb_cache_kv_length(const bb_cache* k, size_t* n) {
+  return guard([&] {
+    need(k != nullptr && n != nullptr, BB_ERR_ARG, "null argument");
+    *n = cache_kv_len(k);
+  });
+}
+
+int bb_cache_evict_front(bb_ctx* c, bb_cache* k, size_t n) {
+  return guard([&] {
+    need_ctx(c);
+    need(k != nullptr && k->ctx == c, BB_ERR_ARG, "bad cache");
+    set_device(c);
+    cache_evict(c, k, n);
+  });
+}
+
+int bb_cache_layer_state(bb_ctx* c, const bb_cache* k, size_t layer, float* conv_state, float* kk, float* v, int loc) {
+  return guard([&] {
+    need_ctx(c);
+    need(k != nullptr && k->ctx == c && layer < k->conv.size(), BB_ERR_ARG, "bad cache or layer");
     need_loc(loc);
     set_device(c);
-    const auto& L = m->layers[layer];
+    const bb_model* m = k->model;
     const hipMemcpyKind kind = loc == BB_LOC_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
-    if (L.conv_state && conv_state)
-      check_hip(hipMemcpyAsync(conv_state, L.conv_state, (size_t)(L.conv->L - 1) * m->H * 4, kind, c->stream), "copy");
-    if (L.kv && L.kv->n) {
-      const size_t bytes = L.kv->n * L.kv->kv_dim * 4;
-      if (k) check_hip(hipMemcpyAsync(k, L.kv->k, bytes, kind, c->stream), "copy");
-      if (v) check_hip(hipMemcpyAsync(v, L.kv->v, bytes, kind, c->stream), "copy");
+    if (k->conv[layer] && conv_state)
+      check_hip(hipMemcpyAsync(conv_state, k->conv[layer], (size_t)(m->layers[layer].conv->L - 1) * m->H * 4, kind,
+                               c->stream),
+                "copy");
+    const bb_kv_cache* kv = k->kv[layer];
+    if (kv && kv->n) {
+      const size_t bytes = kv->n * kv->kv_dim * 4;
+      if (kk) check_hip(hipMemcpyAsync(kk, kv->k, bytes, kind, c->stream), "copy");
+      if (v) check_hip(hipMemcpyAsync(v, kv->v, bytes, kind, c->stream), "copy");
     }
     check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   });
 }
 
-int bb_model_run_layers(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T, float* h_out, int loc) {
+int bb_model_run_layers(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t T, bb_cache* k, float* h_out,
+                        int loc) {
   return guard([&] {
     need_ctx(c);
-    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need_model_cache(c, m, k);
     need_loc(loc);
     need(tokens != nullptr && T >= 1 && T <= (size_t)bb::PF_MAX_ENTRIES / 8, BB_ERR_RANGE, "T must be in 1..4096");
     set_device(c);
     const size_t H = m->H;
     with_io(c, loc, {{h_out, T * H * 4, false, true}}, [&](std::vector<void*>& d) {
-      model_run_dev(c, m, model_tokens(c, m, tokens, T), T);
+      model_run_dev(c, m, k, model_tokens(c, m, tokens, T), T);
       if (h_out) check_hip(hipMemcpyAsync(d[0], m->h, T * H * 4, hipMemcpyDeviceToDevice, c->stream), "h copy");
     });
   });
 }
 
-int bb_model_forward_step(bb_ctx* c, bb_model* m, uint32_t token, float* logits, int loc) {
+int bb_model_forward_step(bb_ctx* c, bb_model* m, uint32_t token, bb_cache* k, float* logits, int loc) {
   return guard([&] {
     need_ctx(c);
-    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need_model_cache(c, m, k);
     need_loc(loc);
     set_device(c);
     with_io(c, loc, {{logits, m->vocab * 4, false, true}}, [&](std::vector<void*>& d) {
-      model_run_dev(c, m, model_tokens(c, m, &token, 1), 1);
+      model_run_dev(c, m, k, model_tokens(c, m, &token, 1), 1);
       logits_dev(c, m->tok_embd, m->final_norm, m->eps, m->h, static_cast<float*>(d[0]));
     });
   });
 }
 
-int bb_model_absorb(bb_ctx* c, bb_model* m, const uint32_t* tokens, size_t n, size_t max_context) {
+// Every token id is checked before anything runs, and a KV history that would overflow grows
+// (kv_reserve), so the call does not stop half-way with the cache partly advanced.
+int bb_model_absorb(bb_ctx* c, bb_model* m, bb_cache* k, const uint32_t* tokens, size_t n, size_t max_context) {
   return guard([&] {
     need_ctx(c);
-    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
+    need_model_cache(c, m, k);
     need(tokens != nullptr || n == 0, BB_ERR_ARG, "null tokens");
     set_device(c);
     const size_t chunk = 512;  // agent.rs:31 PREFILL_CHUNK
     if (n == 0) return;
     const uint32_t* dt = model_tokens(c, m, tokens, n);
-    if (model_kv_len(m) + n <= max_context) {
-      for (size_t i = 0; i < n; i += chunk) model_run_dev(c, m, dt + i, std::min(chunk, n - i));
+    if (cache_kv_len(k) + n <= max_context) {
+      for (bb_kv_cache* kv : k->kv)
+        if (kv) kv_reserve(c, kv, kv->n + n);
+      for (size_t i = 0; i < n; i += chunk) model_run_dev(c, m, k, dt + i, std::min(chunk, n - i));
     } else {
+      for (bb_kv_cache* kv : k->kv)
+        if (kv) kv_reserve(c, kv, std::max(kv->n, max_context) + 1);
       for (size_t i = 0; i < n; ++i) {
-        model_run_dev(c, m, dt + i, 1);
-        const size_t len = model_kv_len(m);
-        if (len > max_context) model_evict(c, m, len - max_context);
+        model_run_dev(c, m, k, dt + i, 1);
+        const size_t len = cache_kv_len(k);
+        if (len > max_context) cache_evict(c, k, len - max_context);
       }
     }
     check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-  });
-}
-
-int bb_model_evict_front(bb_ctx* c, bb_model* m, size_t n) {
-  return guard([&] {
-    need_ctx(c);
-    need(m != nullptr && m->ctx == c, BB_ERR_ARG, "bad model");
-    set_device(c);
-    model_evict(c, m, n);
   });
 }
 

@@ -779,7 +779,7 @@ int bb_gguf_upload(bb_ctx* ctx, const bb_gguf* gp, size_t index, bb_tensor** out
   });
 }
 
-int bb_model_load(bb_ctx* ctx, const bb_gguf* gp, size_t kv_capacity, bb_model** out) {
+int bb_model_load(bb_ctx* ctx, const bb_gguf* gp, bb_model** out) {
   return guard([&] {
     const bb_gguf& g = need_g(gp);
     need(ctx != nullptr && out != nullptr, BB_ERR_ARG, "null argument");
@@ -851,7 +851,7 @@ int bb_model_load(bb_ctx* ctx, const bb_gguf* gp, size_t kv_capacity, bb_model**
       bb_tensor* te = upload("token_embd.weight", own.tensors);
       const float* fin = f32_of("token_embd_norm.weight");
       bb_model* m = nullptr;
-      check_code(bb_model_create(ctx, te, fin, layers.data(), layers.size(), a.eps, kv_capacity, &m));
+      check_code(bb_model_create(ctx, te, fin, layers.data(), layers.size(), a.eps, &m));
       bb::model_adopt(m, std::move(own));
       *out = m;
     } catch (...) {

@@ -6,7 +6,8 @@ Names follow the reference so call sites read alike:
   run_layers' FFN path (model.rs:105-130)               -> FfnStack.run_layers
   Model::conv_step_op / conv_batch (model.rs:399, :190) -> ConvOp.forward
   Model::attn_step / attn_batch (model.rs:430, :222)    -> AttnOp.forward (KvCache: cache.rs)
-  Model::run_layers(_batch) / forward_step, Agent::absorb -> Model (model.rs:99-181, agent.rs:454)
+  Model::run_layers(_batch) / forward_step, Agent::absorb -> Model (model.rs:97-181, agent.rs:454)
+  Cache (cache.rs:10-49), Cache: Clone                  -> Cache (Model.new_cache, Cache.clone)
 Arrays are numpy (host memory, BB_LOC_HOST) or torch CUDA tensors (device memory,
 BB_LOC_DEVICE). Everything runs on the GPU through libbebelm_moe.so; there is no other path.
 """
@@ -354,10 +355,11 @@ class AttnOp:
 
 
 class Model:
-    """The decoder with its caches (Model + Cache, model.rs:25-31, cache.rs:10-19) built from a
-    bebelm_amd.synth.ModelWeights: every operator, FFN and the logits head run on the GPU."""
+    """The decoder's weights (Model, model.rs:25-31) built from a bebelm_amd.synth.ModelWeights:
+    every operator, FFN and the logits head run on the GPU. The decode-time state is a Cache
+    (cache.rs:10-19); one model serves any number of caches (agent.rs:85-86)."""
 
-    def __init__(self, ctx, weights, kv_capacity):
+    def __init__(self, ctx, weights):
         mw = weights
         self.ctx, self.hidden, self.vocab = ctx, mw.hidden, mw.vocab
         self.token_embd = Tensor(ctx, mw.embd_dtype, mw.token_embd, (mw.hidden, mw.vocab))
@@ -383,7 +385,7 @@ class Model:
             fin = np.ascontiguousarray(mw.final_norm, np.float32)
             h = ctypes.c_void_p()
             check(lib().bb_model_create(ctx.handle, self.token_embd.handle, fin.ctypes.data, descs, len(mw.layers),
-                                        mw.eps, kv_capacity, ctypes.byref(h)))
+                                        mw.eps, ctypes.byref(h)))
             self.handle = h
         except Exception:
             self.handle = None
@@ -391,7 +393,7 @@ class Model:
             raise
 
     @classmethod
-    def load(cls, ctx, gguf, kv_capacity, validate=True):
+    def load(cls, ctx, gguf, validate=True):
         """Model::load (model.rs:36-50) from a GGUF (a path or an open gguf.GgufFile): with
         `validate`, config::validate first (the LFM2.5-8B-A1B constants); then the tensor-table
         check and the upload of every tensor into HBM (bb_model_load). The model owns its weights."""
@@ -403,7 +405,7 @@ class Model:
                 g.validate()
             g.check_tensors()
             h = ctypes.c_void_p()
-            check(lib().bb_model_load(ctx.handle, g.handle, kv_capacity, ctypes.byref(h)))
+            check(lib().bb_model_load(ctx.handle, g.handle, ctypes.byref(h)))
             self = cls.__new__(cls)
             self.ctx, self.handle = ctx, h
             arch = g.architecture() + "."
@@ -428,50 +430,85 @@ class Model:
         if self.token_embd is not None:
             self.token_embd.close()
 
+    def new_cache(self, kv_capacity=4096):
+        """Cache::new for this model (kv_capacity: the initial room of each KV history)."""
+        return Cache(self, kv_capacity)
+
+    def run_layers(self, tokens, cache):
+        """run_layers(token, &mut Cache) / run_layers_batch(tokens, &mut Cache): the final hidden
+        states f32[T*hidden]."""
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(tok.size * self.hidden, np.float32)
+        check(lib().bb_model_run_layers(self.ctx.handle, self.handle, tok.ctypes.data, tok.size, cache.handle,
+                                        out.ctypes.data, LOC_HOST))
+        return out
+
+    def forward_step(self, token, cache):
+        """Model::forward_step(&self, token, &mut Cache) (model.rs:97-103): next-token logits."""
+        logits = np.empty(self.vocab, np.float32)
+        check(lib().bb_model_forward_step(self.ctx.handle, self.handle, int(token), cache.handle, logits.ctypes.data,
+                                          LOC_HOST))
+        return logits
+
+    def absorb(self, cache, tokens, max_context):
+        """Agent::absorb(model, cache, tokens, max_context) (agent.rs:454-476)."""
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        check(lib().bb_model_absorb(self.ctx.handle, self.handle, cache.handle, tok.ctypes.data, tok.size,
+                                    max_context))
+
+
+class Cache:
+    """Cache (cache.rs:10-19) of one conversation on a Model: conv states, device KV histories and
+    the next position. Cache::new (cache.rs:21-28) when created; clone() is Cache: Clone
+    (Agent: Clone forks a prefilled prompt, agent.rs:87-91). Close it before its model."""
+
+    def __init__(self, model, kv_capacity=4096, _handle=None):
+        self.model, self.ctx = model, model.ctx
+        if _handle is not None:
+            self.handle = _handle
+            return
+        h = ctypes.c_void_p()
+        check(lib().bb_cache_create(self.ctx.handle, model.handle, kv_capacity, ctypes.byref(h)))
+        self.handle = h
+
+    def clone(self):
+        h = ctypes.c_void_p()
+        check(lib().bb_cache_clone(self.ctx.handle, self.handle, ctypes.byref(h)))
+        return Cache(self.model, _handle=h)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            check(lib().bb_cache_destroy(self.handle))
+            self.handle = None
+
     @property
     def pos(self):
         n = ctypes.c_size_t()
-        check(lib().bb_model_position(self.handle, ctypes.byref(n)))
+        check(lib().bb_cache_position(self.handle, ctypes.byref(n)))
         return n.value
 
     def kv_len(self):
         n = ctypes.c_size_t()
-        check(lib().bb_model_kv_length(self.handle, ctypes.byref(n)))
+        check(lib().bb_cache_kv_length(self.handle, ctypes.byref(n)))
         return n.value
 
     def reset(self):
-        check(lib().bb_model_reset(self.ctx.handle, self.handle))
-
-    def run_layers(self, tokens):
-        """run_layers / run_layers_batch: the final hidden states f32[T*hidden]."""
-        tok = np.ascontiguousarray(tokens, np.uint32)
-        out = np.empty(tok.size * self.hidden, np.float32)
-        check(lib().bb_model_run_layers(self.ctx.handle, self.handle, tok.ctypes.data, tok.size, out.ctypes.data,
-                                        LOC_HOST))
-        return out
-
-    def forward_step(self, token):
-        logits = np.empty(self.vocab, np.float32)
-        check(lib().bb_model_forward_step(self.ctx.handle, self.handle, int(token), logits.ctypes.data, LOC_HOST))
-        return logits
-
-    def absorb(self, tokens, max_context):
-        tok = np.ascontiguousarray(tokens, np.uint32)
-        check(lib().bb_model_absorb(self.ctx.handle, self.handle, tok.ctypes.data, tok.size, max_context))
+        check(lib().bb_cache_reset(self.ctx.handle, self.handle))
 
     def evict_front(self, n):
-        check(lib().bb_model_evict_front(self.ctx.handle, self.handle, n))
+        check(lib().bb_cache_evict_front(self.ctx.handle, self.handle, n))
 
     def layer_state(self, layer):
         """(conv state, k, v) of one layer; the absent ones are None."""
-        kind, size = self.layer_kinds[layer]
+        kind, size = self.model.layer_kinds[layer]
         if kind == "conv":
             st = np.empty(size, np.float32)
-            check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, st.ctypes.data, None, None, LOC_HOST))
+            check(lib().bb_cache_layer_state(self.ctx.handle, self.handle, layer, st.ctypes.data, None, None,
+                                             LOC_HOST))
             return st, None, None
         n = self.kv_len()
         k = np.empty(n * size, np.float32)
         v = np.empty(n * size, np.float32)
-        check(lib().bb_model_layer_state(self.ctx.handle, self.handle, layer, None, k.ctypes.data, v.ctypes.data,
+        check(lib().bb_cache_layer_state(self.ctx.handle, self.handle, layer, None, k.ctypes.data, v.ctypes.data,
                                          LOC_HOST))
         return None, k, v

@@ -53,12 +53,14 @@ def drive_decoder(args):
     ctx = Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
     mw = synth.model_weights(seed=0)
-    m = Model(ctx, mw, 4096)
+    m = Model(ctx, mw)
+    cache = m.new_cache(4096)
     g = np.random.default_rng(1)
-    m.absorb(g.integers(0, mw.vocab, 512).astype(np.uint32), 4096)
+    m.absorb(cache, g.integers(0, mw.vocab, 512).astype(np.uint32), 4096)
     for t in g.integers(0, mw.vocab, args.steps):
-        m.forward_step(int(t))
+        m.forward_step(int(t), cache)
     torch.cuda.synchronize()
+    cache.close()
     m.close()
     ctx.close()
 

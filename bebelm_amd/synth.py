@@ -13,6 +13,8 @@ Every tensor draws from its own PCG64 stream keyed by (config seed, tensor id), 
 can be regenerated alone. Gating follows the reference (sigmoid + selection-only bias,
 model.rs:485-495); the skewed config puts a Zipf(1.2) ranking into that bias (exp_probs_b).
 """
+import os
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -260,18 +262,28 @@ def config_layer(cfg_id, seed=0, layer=0, **kw):
     return moe_weights(seed, layer=layer, down_dtype=cfg.down_dtype, bias=bias, **kw)
 
 
+def _par_map(fn, items):
+    """[fn(i) for i in items] on a thread pool: every layer draws from its own seeded streams, so
+    the arrays are the same in any order (numpy's generators release the GIL while filling)."""
+    items = list(items)
+    workers = max(1, min(len(items), os.cpu_count() or 1, 16))
+    if workers == 1:
+        return [fn(i) for i in items]
+    with ThreadPoolExecutor(workers) as ex:
+        return list(ex.map(fn, items))
+
+
 def stack_layers(seed=0, hidden=HIDDEN, moe_ff=MOE_FF, dense_ff=DENSE_FF, n_experts=N_EXPERTS,
                  n_layers=N_LAYERS, n_dense=N_DENSE):
     """Config 5: layers < n_dense dense; MoE down in Q4_K on even layers, Q6_K on odd ones."""
-    out = []
-    for layer in range(n_layers):
+    def one(layer):
         gain = np.ones(hidden, np.float32)
         if layer < n_dense:
-            out.append((gain, dense_weights(seed, layer, hidden, dense_ff)))
-        else:
-            dd = Q4_K if layer % 2 == 0 else Q6_K
-            out.append((gain, moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=dd)))
-    return out
+            return gain, dense_weights(seed, layer, hidden, dense_ff)
+        dd = Q4_K if layer % 2 == 0 else Q6_K
+        return gain, moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=dd)
+
+    return _par_map(one, range(n_layers))
 
 
 # ---- the whole decoder (model.rs:25-31, 105-130) -------------------------------------------------
@@ -305,10 +317,13 @@ def model_weights(seed=0, hidden=HIDDEN, vocab=VOCAB, n_layers=N_LAYERS, n_dense
     short conv elsewhere, dense FFN below n_dense, MoE above (down Q4_K on even layers, Q6_K on
     odd); norm gains ~ 1 + N(0, 0.05)."""
     g = rng(seed, 9100)
-    layers = []
-    for layer in range(n_layers):
+    gains = []
+    for layer in range(n_layers):  # the norm gains share one stream: drawn in layer order
         an = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
         fn = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
+        gains.append((an, fn))
+
+    def one(layer):
         if layer in attention_layers:
             op = attn_weights(seed, layer, hidden, n_heads, n_kv_heads)
         else:
@@ -317,7 +332,9 @@ def model_weights(seed=0, hidden=HIDDEN, vocab=VOCAB, n_layers=N_LAYERS, n_dense
             ffn = dense_weights(seed, layer, hidden, dense_ff)
         else:
             ffn = moe_weights(seed, layer, hidden, moe_ff, n_experts, down_dtype=Q4_K if layer % 2 == 0 else Q6_K)
-        layers.append(DecoderLayerWeights(an, fn, op, ffn))
+        return DecoderLayerWeights(gains[layer][0], gains[layer][1], op, ffn)
+
+    layers = _par_map(one, range(n_layers))
     te = quant_tensor(rng(seed, 9101), embd_dtype, hidden, vocab)
     final = (1.0 + 0.05 * g.standard_normal(hidden)).astype(np.float32)
     return ModelWeights(hidden, vocab, embd_dtype, te, final, layers)

@@ -21,11 +21,16 @@ The output is one JSON line with `value` in tok/s. It also carries:
                 on all cores, the same on one core, and the CPU model
   prefill       (default run only) config 4 measured in the same process the same way: tok/s,
                 ms per step, the grouped GEMMs' µs and their int8 / bf16 MFMA fractions
+  decode_t1     (default run only) config 1, one token through one MoE block
+  prefill_t512  (default run only) config 3, 512 tokens through one MoE block (unbiased router)
+  ffn_stack     (default run only) config 5, the 24-layer FFN stack at one token
   decoder       (default run only) the whole decoder at LFM2.5-8B-A1B's full shape (24 layers:
                 short conv / GQA attention operators, 2 dense + 22 MoE FFNs, the 128000-row
                 logits head): a 512-token prompt absorbed as one prefill chunk, then one-token
-                forward_steps at that context; per-kernel times of a decode step; the C++
-                restatement's forward_step timed on this host at a short context
+                forward_steps at that context, and at 4,096 and 16,384 positions; per-kernel
+                times of a decode step; the C++ restatement's forward_step timed on this host
+                at the same 512-token context
+Each object carries its own ms_per_step, kernel_us, roofline and cpu_baseline.
 """
 import argparse
 import json
@@ -61,6 +66,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-4 prefill object of the default run")
     ap.add_argument("--no-decoder", action="store_true", help="skip the whole-decoder object of the default run")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the config 1, 3 and 5 objects (decode_t1, prefill_t512, ffn_stack) of the default run")
     ap.add_argument("--cpu-reps", type=int, default=20, help="timed repetitions of the CPU baseline")
     ap.add_argument("--logits-head", action="store_true",
                     help="time bb_logits_from_hidden (rmsnorm + Q6_K 2048 -> 128000 matvec) instead of a config")
@@ -161,10 +168,11 @@ def layer_work(w, counts, T, batched, prerouted=False):
     }
 
 
-def cpu_baseline(run_one, T, seconds, what, reps=20, one_core=True):
+def cpu_baseline(run_one, T, seconds, what, reps=20, one_core=True, reps_1core=None):
     """The reference path's C++ restatement on this host's cores: `reps` timed repetitions of
     about seconds / reps each (whole calls, at least one), tok/s as their median; then the same
-    on one core. run_one(i) runs call i (callers rotate weight sets by i)."""
+    on one core (reps_1core repetitions, default `reps`). run_one(i) runs call i (callers rotate
+    weight sets by i)."""
     from oracle import bbo
 
     try:
@@ -173,12 +181,12 @@ def cpu_baseline(run_one, T, seconds, what, reps=20, one_core=True):
         cores = os.cpu_count() or 1
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
 
-    def median_rate(threads, budget):
+    def median_rate(threads, budget, n_reps):
         bbo.set_threads(threads)
         run_one(0)  # warm-up: pages in weights, starts the thread pool
         rates, calls = [], 1
-        per_rep = budget / reps
-        for _ in range(reps):
+        per_rep = budget / n_reps
+        for _ in range(n_reps):
             n = 0
             t0 = time.perf_counter()
             while True:
@@ -191,24 +199,26 @@ def cpu_baseline(run_one, T, seconds, what, reps=20, one_core=True):
             rates.append(n * T / el)
         return float(np.median(rates)), calls - 1
 
-    value, n_all = median_rate(cores, seconds)
+    value, n_all = median_rate(cores, seconds, reps)
     out = {"value": value, "unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": bbo.cpu_model(),
            "oracle_build": os.path.basename(bbo.lib_path())}
     each = "one call each" if seconds / reps < 0.01 else f"about {seconds / reps:.2f} s each"
     sample = (f"median of {reps} repetitions ({n_all} calls, {each}) of the C++ "
               f"restatement of {what}, OpenMP over output rows")
     if one_core and cores > 1:
-        v1, n1 = median_rate(1, seconds)
+        r1 = reps_1core or reps
+        v1, n1 = median_rate(1, seconds * r1 / reps, r1)
         out["value_1core"] = v1
-        sample += f"; 1 core: {n1} calls in {reps} repetitions"
+        sample += f"; 1 core: {n1} calls in {r1} repetitions"
     bbo.set_threads(cores)
     out["sample"] = sample
     return out
 
 
-def run_config(args, ctx, config, steps, warmup, with_cpu):
+def run_config(args, ctx, config, steps, warmup, with_cpu, cpu_share=1.0):
     """Times `steps` steps of one configuration (after `warmup`), then the same steps again with
-    per-kernel HIP events; returns the bench fields of that configuration."""
+    per-kernel HIP events; returns the bench fields of that configuration. cpu_share scales the
+    CPU baseline's time budget (--cpu-seconds) for the secondary configurations."""
     import torch
 
     from bebelm_amd import synth
@@ -234,7 +244,7 @@ def run_config(args, ctx, config, steps, warmup, with_cpu):
         L = 1
     else:
         L = max(1, args.layers)
-        weights = [synth.config_layer(config, seed=args.seed, layer=l) for l in range(L)]
+        weights = synth._par_map(lambda l: synth.config_layer(config, seed=args.seed, layer=l), range(L))
         units = [MoeLayer(ctx, w) for w in weights]
         weight_bytes = int(sum(w.nbytes for w in weights))
     t_gen = time.perf_counter() - t_gen
@@ -353,24 +363,28 @@ def run_config(args, ctx, config, steps, warmup, with_cpu):
     if with_cpu:
         from oracle import bbo
 
+        secs = args.cpu_seconds * cpu_share
         if config == 5:
             layers_o = [(g, w) for g, w in spec]
             result["cpu_baseline"] = cpu_baseline(lambda i: bbo.ffn_stack(layers_o, x_host.reshape(-1), 1, 1e-5), T,
-                                                  args.cpu_seconds, "the 24-layer FFN stack (T=1)", args.cpu_reps)
+                                                  secs, "the 24-layer FFN stack (T=1)", args.cpu_reps)
         elif prefill:
-            # one call takes seconds: a few repetitions of one call each, all cores only
+            # one call takes about 0.3 s (T = 512) or 2 s (T = 4096) on all cores: repetitions of
+            # one call each. Config 3: 20 of them, then 3 on one core (about 5 s each); config 4:
+            # 5 on all cores only (one call on one core takes about 30 s, beyond the bench's
+            # budget; config 3's one-core figure is the same kernels' per-token rate)
             sample = weights[: min(L, 4)]
             xs = x_host.reshape(-1)
-            reps = 3
+            reps = 20 if config == 3 else 5
             result["cpu_baseline"] = cpu_baseline(lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T), T,
                                                   1e-3 * reps, f"moe_ffn_batch (T={T}, {len(sample)} rotated layers)",
-                                                  reps, one_core=False)
+                                                  reps, one_core=config == 3, reps_1core=3)
         else:
             sample = weights[: min(L, 4)]
             xs = x_host.reshape(-1)
             fn = (lambda i: bbo.moe_ffn(sample[i % len(sample)], xs)) if T == 1 else \
                 (lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T))
-            result["cpu_baseline"] = cpu_baseline(fn, T, args.cpu_seconds,
+            result["cpu_baseline"] = cpu_baseline(fn, T, secs,
                                                   f"moe_ffn{'_batch' if T > 1 else ''} (T={T}, {len(sample)} rotated layers)",
                                                   args.cpu_reps)
     if config == 5:
@@ -403,71 +417,96 @@ def decoder_bench(args, ctx, with_cpu):
         t0 = time.perf_counter()
         with gguf.GgufFile.open(path) as g:
             g.validate()
-            m = Model.load(ctx, g, 4096)
+            m = Model.load(ctx, g)
         up = time.perf_counter() - t0
         upload = {"file_gb": round(nbytes / 1e9, 3), "load_s": round(up, 3), "gb_s": round(nbytes / up / 1e9, 2),
                   "what": "bb_gguf_open + validate + bb_model_load (tensor table check, every tensor "
                           "copied from the mapping into HBM, MoE weights repacked on the GPU); file in page cache"}
     except OSError as e:  # no room for the file: build the same decoder from the arrays
         upload = {"skipped": f"could not write the GGUF file: {e}"}
-        m = Model(ctx, mw, 4096)
+        m = Model(ctx, mw)
     finally:
         if os.path.exists(path):
             os.remove(path)
         os.rmdir(tmpdir)
     prompt = np.random.default_rng(args.seed + 1).integers(0, mw.vocab, 512).astype(np.uint32)
+    cache = m.new_cache(4096)
 
     def prefill_once():
-        m.reset()
+        cache.reset()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        m.absorb(prompt, 4096)  # one chunk of 512 (agent.rs:31); returns after the stream drained
+        m.absorb(cache, prompt, 4096)  # one chunk of 512 (agent.rs:31); returns after the stream drained
         return time.perf_counter() - t0
 
     prefill_once()
     pre = sorted(prefill_once() for _ in range(3))[1]
-    # decode at a 512-token context: the one-token step with its logits back on the host
-    n_dec = 32
-    toks = np.random.default_rng(args.seed + 2).integers(0, mw.vocab, n_dec + 4)
-    for t in toks[:4]:
-        m.forward_step(int(t))
-    t0 = time.perf_counter()
-    for t in toks[4:]:
-        m.forward_step(int(t))
-    dec = (time.perf_counter() - t0) / n_dec
+    rng_dec = np.random.default_rng(args.seed + 2)
+
+    def decode_rate(n_dec):
+        """The one-token step with its logits back on the host at the cache's context."""
+        toks = rng_dec.integers(0, mw.vocab, n_dec + 4)
+        for t in toks[:4]:
+            m.forward_step(int(t), cache)
+        t0 = time.perf_counter()
+        for t in toks[4:]:
+            m.forward_step(int(t), cache)
+        return (time.perf_counter() - t0) / n_dec
+
+    # decode at a 512-token context
+    dec = decode_rate(32)
     # per-kernel times of decode steps (events stamped by each dispatch)
     ctx.reset_stats()
     ctx.profile(True)
-    for t in toks[:8]:
-        m.forward_step(int(t))
+    for t in rng_dec.integers(0, mw.vocab, 8):
+        m.forward_step(int(t), cache)
     stats = ctx.kernel_stats()
     ctx.profile(False)
     total = sum(v[0] for v in stats.values()) or 1.0
     per_step = {k: round(v[0] / 8 * 1e3, 1) for k, v in sorted(stats.items(), key=lambda kv: -kv[1][0]) if v[1]}
+    # long contexts (the reference's agent window is 32,768 positions, agent.rs:25-26): the
+    # prompt grows by chunks of 512 to 4,096 and then 16,384 positions, and the decode step is
+    # timed at each
+    long_ctx = {}
+    for n_ctx in (4096, 16384):
+        more = n_ctx - cache.kv_len()
+        t0 = time.perf_counter()
+        m.absorb(cache, rng_dec.integers(0, mw.vocab, more).astype(np.uint32), 32768)
+        ab = time.perf_counter() - t0
+        d = decode_rate(16)
+        long_ctx[f"ctx{n_ctx}"] = {"ms_per_token": round(d * 1e3, 3), "tok_s": round(1.0 / d, 1),
+                                   "absorb_ms": round(ab * 1e3, 1), "absorbed_tokens": int(more)}
     out = {
         "workload": "LFM2.5-8B-A1B shape: 24 layers (6 GQA attention, 18 short conv), 2 dense + 22 MoE FFNs, "
                     "vocab 128000, Q4_K/Q6_K synthetic weights",
         "prefill_512": {"ms": round(pre * 1e3, 2), "tok_s": round(512 / pre, 1)},
         "decode_t1_ctx512": {"ms_per_token": round(dec * 1e3, 3), "tok_s": round(1.0 / dec, 1),
                              "includes": "host call, logits copied back to the host"},
+        "decode_long_context": long_ctx,
         "decode_kernel_us_per_step": per_step,
         "decode_kernel_ms_per_step": round(total / 8, 3),
         "gguf_upload": upload,
     }
+    cache.close()
     m.close()
     if with_cpu:
         from oracle import bbo
 
-        om = bbo.Model(mw, 64)
-        om.absorb(list(prompt[:16]), 64)
+        # the restatement at the GPU figure's context: the same 512-token prompt absorbed
+        # (batched, as Agent::absorb does), then forward_steps at 512+ positions
+        om = bbo.Model(mw, 600)
         t0 = time.perf_counter()
-        reps = 3
-        for t in toks[:reps]:
+        om.absorb(list(prompt), 4096)
+        cpu_pre = time.perf_counter() - t0
+        toks = np.random.default_rng(args.seed + 3).integers(0, mw.vocab, 3)
+        t0 = time.perf_counter()
+        for t in toks:
             om.forward_step(int(t))
-        cpu = (time.perf_counter() - t0) / reps
+        cpu = (time.perf_counter() - t0) / len(toks)
         out["cpu_baseline"] = {"value": round(1.0 / cpu, 2), "unit": "tok/s", "cores": bbo.get_threads(),
-                               "kind": "port", "sample": f"{reps} forward_steps of the C++ restatement (Python "
-                               "composition of its operators) at a 16-token context"}
+                               "kind": "port", "prefill_512_tok_s": round(512 / cpu_pre, 1),
+                               "sample": f"the 512-token prompt absorbed in one chunk, then {len(toks)} forward_steps "
+                               "of the C++ restatement (Python composition of its operators) at a 512-token context"}
     return out
 
 
@@ -489,7 +528,7 @@ def main():
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
 
     def defaults(config):
-        steps = args.steps if args.steps is not None else (20 if config == 4 else 200)
+        steps = args.steps if args.steps is not None else (20 if config == 4 else 50 if config == 3 else 200)
         warmup = args.warmup if args.warmup is not None else (3 if config == 4 else 20)
         return steps, warmup
 
@@ -511,21 +550,34 @@ def main():
         "config": res.pop("config"),
         **res,
     }
-    if args.config == 2 and not args.no_prefill:
-        # the metric's prefill half: config 4 in the same process, measured the same way
-        ps, pw = defaults(4)
+    def sub(config, share):
+        """Another BASELINE configuration measured in the same process the same way, as an
+        object of the line."""
+        ps, pw = defaults(config)
         if args.steps is not None:
             ps = min(ps, args.steps)
         if args.warmup is not None:
             pw = min(pw, args.warmup)
-        p, ps, pw = run_config(args, ctx, 4, ps, pw, not args.no_cpu)
-        result["prefill"] = {
-            "metric": p["metric"], "value": p["value"], "unit": "tok/s", "steps": ps, "warmup": pw,
-            "ms_per_step": p["ms_per_step"], "config": p["config"], "gemms": p["gemms"],
-            "block_tflops": p["block_tflops"], "block_frac_of_bf16_peak": p["block_frac_of_bf16_peak"],
-            "kernel_us": p["kernel_us"], "roofline": p["roofline"], "cpu_baseline": p["cpu_baseline"],
-            "mean_hit_experts": p["mean_hit_experts"],
-        }
+        p, ps, pw = run_config(args, ctx, config, ps, pw, not args.no_cpu, share)
+        o = {"metric": p["metric"], "value": p["value"], "unit": "tok/s", "steps": ps, "warmup": pw,
+             "ms_per_step": p["ms_per_step"], "config": p["config"]}
+        for k in ("gemms", "block_tflops", "block_frac_of_bf16_peak", "block_hbm_gbps", "block_frac_of_8tbs"):
+            if k in p:
+                o[k] = p[k]
+        o.update({"kernel_us": p["kernel_us"], "roofline": p["roofline"], "cpu_baseline": p["cpu_baseline"],
+                  "mean_hit_experts": p["mean_hit_experts"]})
+        return o
+
+    if args.config == 2 and not args.no_others:
+        # the metric's other configurations: one token (config 1), 512-token prefill (config 3),
+        # the 24-layer FFN stack at one token (config 5)
+        result["decode_t1"] = sub(1, 0.4)
+        result["prefill_t512"] = sub(3, 1.0)
+    if args.config == 2 and not args.no_prefill:
+        # the metric's prefill half: config 4 in the same process, measured the same way
+        result["prefill"] = sub(4, 1.0)
+    if args.config == 2 and not args.no_others:
+        result["ffn_stack"] = sub(5, 0.5)
     if args.config == 2 and not args.no_decoder:
         result["decoder"] = decoder_bench(args, ctx, not args.no_cpu)
     ctx.close()

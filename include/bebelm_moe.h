@@ -59,6 +59,7 @@ typedef struct bb_conv_op bb_conv_op;
 typedef struct bb_attn_op bb_attn_op;
 typedef struct bb_kv_cache bb_kv_cache;
 typedef struct bb_model bb_model;
+typedef struct bb_cache bb_cache;
 typedef struct bb_gguf bb_gguf;
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -270,33 +271,51 @@ typedef struct {
   bb_dense* dense;
 } bb_decoder_layer;
 /* token_embd [hidden, vocab] (embedding rows and the tied logits head), final norm gain host
- * f32[hidden] (`token_embd_norm`), rmsnorm eps. The model owns the caches: a conv state per conv
- * layer and a device KV cache of kv_capacity positions per attention layer, starting empty at
- * position 0 (Cache::new). */
+ * f32[hidden] (`token_embd_norm`), rmsnorm eps. The model holds weights only (Model,
+ * model.rs:25-31): the decode-time state is a bb_cache, so one loaded model serves any number
+ * of caches (agent.rs:85-86: several agents on one model). Calls on one model are ordered on its
+ * context's stream (the model keeps per-call scratch buffers). */
 int bb_model_create(bb_ctx* ctx, const bb_tensor* token_embd, const float* final_norm, const bb_decoder_layer* layers,
-                    size_t n_layers, float eps, size_t kv_capacity, bb_model** out);
+                    size_t n_layers, float eps, bb_model** out);
+/* Destroy the model's caches first. */
 int bb_model_destroy(bb_model* m);
-/* Cache::new again: zero conv states, empty KV caches, position 0. */
-int bb_model_reset(bb_ctx* ctx, bb_model* m);
+
+/* Cache::new (cache.rs:21-28) for the layers of `m`: a zeroed conv state per conv layer, an
+ * empty device KV history per attention layer with room for kv_capacity positions (grown on
+ * demand, as the reference's Vec histories grow), position 0. The cache is used with `m` only
+ * and must be destroyed before it. */
+int bb_cache_create(bb_ctx* ctx, const bb_model* m, size_t kv_capacity, bb_cache** out);
+/* Cache: Clone (cache.rs:9; Agent: Clone, agent.rs:87-91): an independent copy of the conv
+ * states, KV histories and position, e.g. to fork a prefilled prompt into several continuations. */
+int bb_cache_clone(bb_ctx* ctx, const bb_cache* src, bb_cache** out);
+int bb_cache_destroy(bb_cache* cache);
+/* Cache::new again (Agent::clear, agent.rs): zero conv states, empty KV histories, position 0. */
+int bb_cache_reset(bb_ctx* ctx, bb_cache* cache);
 /* cache.pos (the next token's position) and Cache::kv_len (cache.rs:32-35). */
-int bb_model_position(const bb_model* m, size_t* pos);
-int bb_model_kv_length(const bb_model* m, size_t* n);
-/* Copies layer `layer`'s caches out: its conv state (conv layers, f32[(l_cache-1)*hidden]) or its
+int bb_cache_position(const bb_cache* cache, size_t* pos);
+int bb_cache_kv_length(const bb_cache* cache, size_t* n);
+/* Cache::evict_front (cache.rs:40-50) on every attention layer: a layer holding fewer than n
+ * positions is left as it is; pos is unchanged. */
+int bb_cache_evict_front(bb_ctx* ctx, bb_cache* cache, size_t n);
+/* Copies layer `layer`'s state out: its conv state (conv layers, f32[(l_cache-1)*hidden]) or its
  * n cached keys and values (attention layers, f32[n*kv_dim] each); NULL outputs are skipped. */
-int bb_model_layer_state(bb_ctx* ctx, const bb_model* m, size_t layer, float* conv_state, float* k, float* v, int loc);
-/* Model::run_layers (model.rs:105-130) for T == 1 and run_layers_batch (model.rs:146-181) for
- * T > 1: host token ids[T] at positions pos.., caches updated, final hidden states into h_out
- * f32[T*hidden] (may be NULL). */
-int bb_model_run_layers(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t T, float* h_out, int loc);
-/* Model::forward_step (model.rs:99-103): run_layers for one token, then logits_from_hidden
- * into logits f32[vocab]. */
-int bb_model_forward_step(bb_ctx* ctx, bb_model* m, uint32_t token, float* logits, int loc);
-/* Agent::absorb (agent.rs:454-465): when the whole batch fits max_context, run_layers_batch over
- * chunks of 512 tokens (agent.rs:31); otherwise token by token, sliding the KV window down to
- * max_context after each (Agent::trim_context, agent.rs:471-476). */
-int bb_model_absorb(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t n, size_t max_context);
-/* Cache::evict_front (cache.rs:40-50) on every attention layer. */
-int bb_model_evict_front(bb_ctx* ctx, bb_model* m, size_t n);
+int bb_cache_layer_state(bb_ctx* ctx, const bb_cache* cache, size_t layer, float* conv_state, float* k, float* v,
+                         int loc);
+
+/* Model::run_layers(&self, token, &mut Cache) (model.rs:105-130) for T == 1 and
+ * run_layers_batch(&self, tokens, &mut Cache) (model.rs:146-181) for T > 1: host token ids[T]
+ * at positions cache.pos.., the cache updated, final hidden states into h_out f32[T*hidden]
+ * (may be NULL). */
+int bb_model_run_layers(bb_ctx* ctx, bb_model* m, const uint32_t* tokens, size_t T, bb_cache* cache, float* h_out,
+                        int loc);
+/* Model::forward_step(&self, token, &mut Cache) (model.rs:97-103): run_layers for one token,
+ * then logits_from_hidden into logits f32[vocab]. */
+int bb_model_forward_step(bb_ctx* ctx, bb_model* m, uint32_t token, bb_cache* cache, float* logits, int loc);
+/* Agent::absorb(model, cache, tokens, max_context) (agent.rs:454-465): when the whole batch fits
+ * max_context, run_layers_batch over chunks of 512 tokens (agent.rs:31); otherwise token by
+ * token, sliding the KV window down to max_context after each (Agent::trim_context,
+ * agent.rs:471-476). Token ids are checked before anything runs. */
+int bb_model_absorb(bb_ctx* ctx, bb_model* m, bb_cache* cache, const uint32_t* tokens, size_t n, size_t max_context);
 
 /* ---- GGUF files (gguf.rs, config.rs:51-89, model.rs:36-50, :572-584, :619-660) ---------------- */
 /* GgufFile::open (gguf.rs:171-177): maps the file read-only and parses the header, the metadata
@@ -361,11 +380,11 @@ int bb_gguf_upload(bb_ctx* ctx, const bb_gguf* g, size_t index, bb_tensor** out)
 /* Model::load (model.rs:36-50) after the open: check_tensors, then every tensor the forward
  * pass reads uploaded to HBM, the operators, FFNs and the decoder built from them with the
  * file's sizes (hidden, heads and kv heads per layer, expert counts, conv length, RoPE base,
- * eps; the small F32 tensors read as precompute_f32 reads them, :54-67) and caches of
- * kv_capacity positions. The returned model owns all of it: bb_model_destroy frees it. The
+ * eps; the small F32 tensors read as precompute_f32 reads them, :54-67). Caches for it come
+ * from bb_cache_create. The returned model owns all of it: bb_model_destroy frees it. The
  * bb_gguf may be closed once this returns. Call bb_gguf_validate first to also pin the
  * LFM2.5-8B-A1B constants, as Model::load does. */
-int bb_model_load(bb_ctx* ctx, const bb_gguf* g, size_t kv_capacity, bb_model** out);
+int bb_model_load(bb_ctx* ctx, const bb_gguf* g, bb_model** out);
 
 #ifdef __cplusplus
 }

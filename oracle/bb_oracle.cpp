@@ -209,6 +209,8 @@ float dot_f32(const float* a, const float* b, size_t n) {
 //   3  multiply-then-add chains; the 8 lanes summed left to right
 //   4  left-to-right f32 sum of rounded products (scalar loop)
 //   5  f64 sum of the exact products, rounded once to f32
+//   6  multiply-then-add chains; lanes folded v_i + v_{i+4}, then (s0+s1)+(s2+s3) (what a
+//      non-AVX x86-64-v2 build computes when its reduce is the pairwise fold)
 float dot_variant(const float* a, const float* b, size_t n, int variant) {
   if (variant == 0) return dot_f32(a, b, n);
   if (variant == 4) {
@@ -222,6 +224,7 @@ float dot_variant(const float* a, const float* b, size_t n, int variant) {
     return float(s);
   }
   const bool fma = variant == 2;
+  const bool pairwise = variant == 2 || variant == 6;
   float acc[4][8] = {};
   size_t i = 0;
   while (i + 32 <= n) {
@@ -241,7 +244,7 @@ float dot_variant(const float* a, const float* b, size_t n, int variant) {
   float sum;
   if (variant == 1) {
     sum = reduce_add8(v);
-  } else if (variant == 2) {
+  } else if (pairwise) {
     float f[4];
     for (int l = 0; l < 4; ++l) f[l] = v[l] + v[l + 4];
     sum = (f[0] + f[1]) + (f[2] + f[3]);

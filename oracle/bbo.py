@@ -210,7 +210,8 @@ def dot(a, b):
 # assumes for the reference; 1-5 are the other plausible ones.
 DOT_VARIANTS = {0: "FMA chains, AVX reduce tree", 1: "mul+add chains, AVX reduce tree",
                 2: "FMA chains, pairwise lane fold", 3: "mul+add chains, lanes left to right",
-                4: "scalar left-to-right f32", 5: "f64 exact products, one rounding"}
+                4: "scalar left-to-right f32", 5: "f64 exact products, one rounding",
+                6: "mul+add chains, pairwise lane fold"}
 
 
 def dot_variant(a, b, variant):
@@ -493,6 +494,11 @@ class KvCache:
         self.v = np.zeros(cap * kv_dim, np.float32)
         self.n = 0
 
+    def copy(self):
+        c = KvCache(self.kv_dim, self.cap)
+        c.k[:], c.v[:], c.n = self.k, self.v, self.n
+        return c
+
 
 def _attn_struct(w):
     return AttnOp(w.hidden, w.n_heads, w.n_kv_heads, w.head_dim, w.q_dtype, w.k_dtype, w.v_dtype, w.o_dtype,
@@ -534,6 +540,14 @@ class Model:
 
     def kv_len(self):
         return max([c.n for c in self.state.values() if isinstance(c, KvCache)] or [0])
+
+    def fork(self):
+        """Cache: Clone (cache.rs:9): a model over the same weights with a copy of this one's
+        caches and position, which then evolve independently."""
+        other = Model.__new__(Model)
+        other.mw, other.cap, other.pos = self.mw, self.cap, self.pos
+        other.state = {i: (c.copy() if isinstance(c, KvCache) else c.copy()) for i, c in self.state.items()}
+        return other
 
     def embed(self, tokens):
         H = self.mw.hidden

@@ -1,7 +1,9 @@
 """The whole decoder on the GPU (Model::run_layers / run_layers_batch / forward_step,
-model.rs:99-181, and Agent::absorb's chunked prefill and sliding window, agent.rs:454-476)
+model.rs:97-181, and Agent::absorb's chunked prefill and sliding window, agent.rs:454-476)
 against the CPU restatement: embedding, 24 layers of rmsnorm + short-conv or GQA attention +
-rmsnorm + dense or MoE FFN, the caches, the final norm and the logits head.
+rmsnorm + dense or MoE FFN, the caches, the final norm and the logits head. The decode-time
+state is a Cache separate from the model's weights (cache.rs:10-49): one model serves several
+caches, and a cache can be cloned mid-prompt (agent.rs:85-94).
 
 The bar is bit-exactness, with the one documented divergence of the hidden-size rmsnorm (an f64
 tree sum here, left to right in the reference; the f32 results agree unless the two f64 sums
@@ -32,9 +34,10 @@ def check(got, want, what):
     assert diff == 0, f"{what}: {diff} values differ in bits"
 
 
-def check_caches(gm, om, what):
+def check_caches(gc, om, what):
+    """gc: a GPU Cache; om: the oracle's bbo.Model (weights + caches)."""
     for i in sorted(om.state):
-        st, k, v = gm.layer_state(i)
+        st, k, v = gc.layer_state(i)
         c = om.state[i]
         if isinstance(c, bbo.KvCache):
             check(k, c.k[:c.n * c.kv_dim], f"{what}: layer {i} keys")
@@ -50,41 +53,94 @@ def small_weights():
 
 def test_small_model_prefill_chunks_and_decode(gpu_ctx):
     mw = small_weights()
-    gm = Model(gpu_ctx, mw, 800)
+    gm = Model(gpu_ctx, mw)
+    gc = gm.new_cache(800)
     om = bbo.Model(mw, 800)
     try:
         ids = list(np.random.default_rng(1).integers(0, mw.vocab, 600))
         log("small model: absorb 600 tokens (chunks of 512 + 88)")
-        gm.absorb(ids, max_context=700)
+        gm.absorb(gc, ids, max_context=700)
         om.absorb(ids, max_context=700)
-        assert gm.pos == om.pos == 600 and gm.kv_len() == om.kv_len() == 600
-        check_caches(gm, om, "after absorb")
+        assert gc.pos == om.pos == 600 and gc.kv_len() == om.kv_len() == 600
+        check_caches(gc, om, "after absorb")
         for step, tok in enumerate((7, 123, 999)):
             log(f"small model: forward_step {step}")
-            check(gm.forward_step(tok), om.forward_step(tok), f"logits step {step}")
-        check_caches(gm, om, "after decode")
+            check(gm.forward_step(tok, gc), om.forward_step(tok), f"logits step {step}")
+        check_caches(gc, om, "after decode")
     finally:
+        gc.close()
+        gm.close()
+
+
+def test_one_model_several_caches(gpu_ctx):
+    # One weight upload, two conversations interleaved on different prompts, and a third forked
+    # from the first mid-prompt (Cache: Clone); each continues on its own and must equal an
+    # independent oracle model fed the same tokens (agent.rs:85-94).
+    mw = small_weights()
+    gm = Model(gpu_ctx, mw)
+    ca, cb = gm.new_cache(16), gm.new_cache(700)   # ca starts small: its KV histories must grow
+    oa, ob = bbo.Model(mw, 800), bbo.Model(mw, 800)
+    cc = None
+    try:
+        g = np.random.default_rng(4)
+        pa = list(g.integers(0, mw.vocab, 300))
+        pb = list(g.integers(0, mw.vocab, 41))
+        log("two caches: absorb prompt A part 1, prompt B, prompt A part 2 (interleaved)")
+        gm.absorb(ca, pa[:200], max_context=700)
+        oa.absorb(pa[:200], max_context=700)
+        gm.absorb(cb, pb, max_context=700)
+        ob.absorb(pb, max_context=700)
+        log("two caches: fork A at position 200")
+        cc = ca.clone()
+        oc = oa.fork()
+        gm.absorb(ca, pa[200:], max_context=700)
+        oa.absorb(pa[200:], max_context=700)
+        assert (ca.pos, cb.pos, cc.pos) == (300, 41, 200)
+        check_caches(ca, oa, "cache A")
+        check_caches(cb, ob, "cache B")
+        check_caches(cc, oc, "fork of A")
+        for step, (ta, tb, tc) in enumerate(((5, 6, 7), (900, 17, 400), (1, 2, 3))):
+            log(f"two caches and a fork: interleaved forward_step {step}")
+            check(gm.forward_step(tb, cb), ob.forward_step(tb), f"cache B logits step {step}")
+            check(gm.forward_step(tc, cc), oc.forward_step(tc), f"fork logits step {step}")
+            check(gm.forward_step(ta, ca), oa.forward_step(ta), f"cache A logits step {step}")
+        log("fork continues with a prompt of its own (batched)")
+        tail = list(g.integers(0, mw.vocab, 37))
+        gm.absorb(cc, tail, max_context=700)
+        oc.absorb(tail, max_context=700)
+        check_caches(cc, oc, "fork after its own prompt")
+        check_caches(ca, oa, "cache A untouched by the fork")
+        assert (ca.pos, cb.pos, cc.pos) == (303, 44, 240)
+    finally:
+        for c in (ca, cb, cc):
+            if c is not None:
+                c.close()
         gm.close()
 
 
 def test_small_model_sliding_window(gpu_ctx):
     mw = small_weights()
-    gm = Model(gpu_ctx, mw, 64)
+    gm = Model(gpu_ctx, mw)
+    gc = gm.new_cache(8)   # grows to the window as the reference's Vec histories do
     om = bbo.Model(mw, 64)
     try:
         ids = list(range(30, 60))
-        gm.absorb(ids[:10], max_context=20)
+        gm.absorb(gc, ids[:10], max_context=20)
         om.absorb(ids[:10], max_context=20)
         log("small model: absorb past max_context (token by token, trimming)")
-        gm.absorb(ids[10:], max_context=20)
+        gm.absorb(gc, ids[10:], max_context=20)
         om.absorb(ids[10:], max_context=20)
-        assert gm.kv_len() == om.kv_len() == 20 and gm.pos == om.pos == 30
-        check_caches(gm, om, "after sliding")
-        check(gm.forward_step(3), om.forward_step(3), "logits after sliding")
-        gm.reset()
+        assert gc.kv_len() == om.kv_len() == 20 and gc.pos == om.pos == 30
+        check_caches(gc, om, "after sliding")
+        check(gm.forward_step(3, gc), om.forward_step(3), "logits after sliding")
+        gc.evict_front(25)  # more than any layer holds: Cache::evict_front leaves it as it is
+        assert gc.kv_len() == 21
+        gc.reset()
         om.reset()
-        check(gm.run_layers([9, 8, 7]), om.run_layers([9, 8, 7]), "hidden states after reset")
+        assert gc.pos == 0 and gc.kv_len() == 0
+        check(gm.run_layers([9, 8, 7], gc), om.run_layers([9, 8, 7]), "hidden states after reset")
     finally:
+        gc.close()
         gm.close()
 
 
@@ -93,15 +149,45 @@ def test_full_size_decoder(gpu_ctx):
     # + 22 MoE FFNs, 32 heads / 8 kv heads of 64, vocab 128000
     log("full-size decoder: generating weights")
     mw = synth.model_weights(seed=0)
-    gm = Model(gpu_ctx, mw, 64)
+    gm = Model(gpu_ctx, mw)
+    gc = gm.new_cache(64)
     om = bbo.Model(mw, 64)
     try:
         ids = [1, 500, 70000, 127999, 42]
         log("full-size decoder: prefill 5 tokens")
-        check(gm.run_layers(ids), om.run_layers(ids), "prefill hidden states")
+        check(gm.run_layers(ids, gc), om.run_layers(ids), "prefill hidden states")
         for step, tok in enumerate((17, 99)):
             log(f"full-size decoder: forward_step {step}")
-            check(gm.forward_step(tok), om.forward_step(tok), f"logits step {step}")
-        check_caches(gm, om, "full size")
+            check(gm.forward_step(tok, gc), om.forward_step(tok), f"logits step {step}")
+        check_caches(gc, om, "full size")
     finally:
+        gc.close()
+        gm.close()
+
+
+def test_long_context_decoder(gpu_ctx):
+    # The reference's agent keeps a 32,768-position window (agent.rs:25-26). A decoder of reduced
+    # width (hidden 256, 4 heads / 1 kv head of 64: the CPU restatement's attention over 16K
+    # positions then takes seconds, not minutes) with two attention layers absorbs 16,400 tokens
+    # in chunks of 512 and decodes two more: every score row past 15,360 positions leaves LDS for
+    # global memory, in the batched softmax of the prefill chunks and in the one-token softmax-V.
+    mw = synth.model_weights(seed=7, hidden=256, vocab=512, n_layers=4, n_dense=1, attention_layers=(1, 3),
+                             moe_ff=256, dense_ff=256, n_experts=4, n_heads=4, n_kv_heads=1)
+    gm = Model(gpu_ctx, mw)
+    gc = gm.new_cache(1024)  # grows as the prompt comes in
+    om = bbo.Model(mw, 16500)
+    try:
+        ids = list(np.random.default_rng(3).integers(0, mw.vocab, 16400))
+        for a in range(0, len(ids), 4096):
+            log(f"long context: absorb tokens {a}..{min(a + 4096, len(ids))}")
+            gm.absorb(gc, ids[a:a + 4096], max_context=32768)
+            om.absorb(ids[a:a + 4096], max_context=32768)
+        assert gc.pos == om.pos == 16400 and gc.kv_len() == 16400
+        check_caches(gc, om, "after a 16,400-token prompt")
+        for step, tok in enumerate((11, 500)):
+            log(f"long context: forward_step {step} at {16400 + step} positions")
+            check(gm.forward_step(tok, gc), om.forward_step(tok), f"logits at {16400 + step} positions")
+        check_caches(gc, om, "after decoding at 16,401 positions")
+    finally:
+        gc.close()
         gm.close()

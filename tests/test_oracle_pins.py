@@ -137,22 +137,33 @@ def test_router_dot_close_to_exact(oracle):
         assert abs(got - exact) <= 1e-5 * float(np.sum(np.abs(a.astype(np.float64) * b)))
 
 
-def test_router_dot_chain_structure(oracle):
-    # One nonzero product per chain position: the result must equal the reduce-tree formula.
-    n = 2048
+def test_router_dot_reduce_order_is_the_avx_tree(oracle):
+    # The restatement assumes the `wide` AVX reduce ((v0+v4)+(v2+v6))+((v1+v5)+(v3+v7)) of the
+    # eight lane values (parity unpinned: the crate is not vendored). These lane values make each
+    # candidate order give a different f32 result, worked out by hand from the rounding of
+    # 2^24 + 1 (a tie, which rounds to the even 2^24):
+    #   AVX tree:        ((2^24 + 1) + (1 + 0)) + ((-2^24 + 0) + (1 + 0)) = 2^24 - (2^24 - 1) = 1
+    #   pairwise fold:   f = (2^24 + 1, -2^24 + 0, 1 + 0, 1 + 0) = (2^24, -2^24, 1, 1) -> 0 + 2 = 2
+    #   left to right:   2^24 - 2^24 + 1 + 1 + 1 = 3 (also the exact sum)
+    # One product per chain (chains 0..7 only, b = 1), so lane l's value is a[l] exactly.
+    n = 32
     a = np.zeros(n, np.float32)
+    a[:8] = [2.0 ** 24, -2.0 ** 24, 1.0, 1.0, 1.0, 0.0, 0.0, 0.0]
     b = np.ones(n, np.float32)
-    vals = np.float32(1.0) + np.arange(32, dtype=np.float32) * np.float32(2.0 ** -20)
-    a[:32] = vals
-    a[1024:1056] = np.float32(3.0) * vals
-    got = np.float32(oracle.dot(a, b))
-    acc = [np.float32(np.float32(a[c] * 1) + np.float32(a[1024 + c]) * np.float32(1)) for c in range(32)]
-    acc = [np.float32(np.float32(0) + a[c]) for c in range(32)]
-    acc = [np.float32(acc[c] + a[1024 + c]) for c in range(32)]
-    v = [np.float32(np.float32(acc[l] + acc[8 + l]) + np.float32(acc[16 + l] + acc[24 + l])) for l in range(8)]
-    want = np.float32(np.float32(np.float32(v[0] + v[4]) + np.float32(v[2] + v[6]))
-                      + np.float32(np.float32(v[1] + v[5]) + np.float32(v[3] + v[7])))
-    assert got.view(np.uint32) == want.view(np.uint32)
+    assert np.float32(oracle.dot(a, b)) == np.float32(1.0)
+    assert np.float32(oracle.dot_variant(a, b, 0)) == np.float32(1.0)
+    assert np.float32(oracle.dot_variant(a, b, 1)) == np.float32(1.0)  # no FMA, same tree
+    assert np.float32(oracle.dot_variant(a, b, 2)) == np.float32(2.0)
+    assert np.float32(oracle.dot_variant(a, b, 6)) == np.float32(2.0)
+    assert np.float32(oracle.dot_variant(a, b, 3)) == np.float32(3.0)
+    assert np.float32(oracle.dot_variant(a, b, 5)) == np.float32(3.0)
+    # the lane combine (acc0 + acc1) + (acc2 + acc3) of one lane: chains l, 8+l, 16+l, 24+l
+    c = np.zeros(n, np.float32)
+    c[[0, 8, 16, 24]] = [2.0 ** 24, 1.0, 1.0, -2.0 ** 24]
+    # (2^24 + 1) + (1 - 2^24) = 2^24 - (2^24 - 1) = 1; the scalar left-to-right sum instead gives
+    # ((2^24 + 1) + 1) - 2^24 = (2^24 + 1) - 2^24 = 2^24 - 2^24 = 0
+    assert np.float32(oracle.dot(c, b)) == np.float32(1.0)
+    assert np.float32(oracle.dot_variant(c, b, 4)) == np.float32(0.0)
 
 
 def test_pack_q4k_scales_inverts_get_scale_min_k4(oracle):

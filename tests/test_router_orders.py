@@ -6,8 +6,8 @@ is a rounded multiply and an add (.github/workflows/ci.yml:28-35). The restateme
 GPU) assume FMA chains and the AVX reduce tree; the last bits of a logit are therefore not
 pinned by the reference. What must hold is that the routing does not depend on them: for every
 token of BASELINE configs 1-5, the gating of model.rs:485-495 applied to the logits of each
-plausible evaluation order (oracle.DOT_VARIANTS: FMA or not, AVX tree, pairwise fold, left to
-right, and the once-rounded f64 sum) selects the same experts in the same order.
+plausible evaluation order (oracle.DOT_VARIANTS: FMA or not, each with the AVX tree and the
+pairwise fold, lanes left to right, and the once-rounded f64 sum) selects the same experts in the same order.
 
 The test also states the margin this rests on: the smallest selection margin key[k-1] - key[k]
 recorded in the golden fixtures, against the largest change of any key between orders.
@@ -22,7 +22,7 @@ from bebelm_amd import synth
 from golden import make_fixtures as mf
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-VARIANTS = (0, 1, 2, 3, 4, 5)
+VARIANTS = (0, 1, 2, 3, 4, 5, 6)
 
 
 def keys(logits, bias):

@@ -51,3 +51,32 @@ def test_noalloc_matches_forward(gpu_ctx, oracle):
         assert b"scratch" in _lib.lib().bb_last_error()
     finally:
         layer.close()
+
+
+def test_noalloc_at_the_scratch_limit(gpu_ctx):
+    # hidden = ff = 2048, 32 experts, k = 4: 440 tokens fill the scratch area up to its tail
+    # slack (the padding every allocated workspace has); 441 tokens are refused.
+    import torch
+
+    w = synth.moe_weights(5, hidden=2048, moe_ff=2048)
+    layer = MoeLayer(gpu_ctx, w)
+    try:
+        for t in (440, 17):
+            print(f"noalloc: T={t} (hidden = ff = 2048)", flush=True)
+            x = torch.from_numpy(synth.hidden_states(29, t)).cuda()
+            want = torch.empty_like(x)
+            got = torch.full_like(x, float("nan"))
+            torch.cuda.synchronize()
+            layer.forward(x, t, want)
+            gpu_ctx.synchronize()
+            _lib.check(noalloc(gpu_ctx, layer, x, t, got))
+            gpu_ctx.synchronize()
+            assert np.array_equal(got.cpu().numpy().view(np.uint32), want.cpu().numpy().view(np.uint32)), \
+                f"T={t}: noalloc differs from bb_moe_forward"
+        x = torch.zeros((441, 2048), dtype=torch.float32, device="cuda")
+        out = torch.empty_like(x)
+        torch.cuda.synchronize()
+        assert noalloc(gpu_ctx, layer, x, 441, out) == _lib.BB_ERR_RANGE
+        assert b"scratch" in _lib.lib().bb_last_error()
+    finally:
+        layer.close()
