@@ -237,7 +237,9 @@ hipError_t launch_residual_norm(hipStream_t s, float* h, const float* slots, con
 
 // ---- decoder-layer operators (bb_ops.hip) ----
 constexpr int OPS_HD_MAX = 256;     // head_dim bound of the attention kernels
-constexpr int OPS_ROW_LDS = 15360;  // score rows up to this length are worked on in LDS (60 KB)
+// score rows up to this length are worked on in LDS: 40000 floats (156 KB of the CU's 160 KB, one
+// such wave per CU), past the reference agent's 32,768-position window (agent.rs:25-26)
+constexpr int OPS_ROW_LDS = 40000;
 // out[t][c] = causal conv of token t over [state; bx] (op: bx = B·x_gate from the in_proj output
 // src [T][3C], and out = C·conv); the state is read, not written.
 hipError_t launch_conv(hipStream_t s, bool op, const float* src, const float* state, const float* w, int C, int L,

@@ -241,17 +241,30 @@ __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, fl
   for (int j = lane; j < n; j += 64) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
   __syncthreads();
   if (lane == 0) {
-    // left to right; eight values read ahead of their adds
+    // left to right; the next 16 values are read while the adds of the current 16 run (the adds
+    // are one dependent chain, the reads are not)
+    constexpr int U = 16;
     double sum = 0.0;
-    int j = 0;
-    for (; j + 8 <= n; j += 8) {
-      float e[8];
+    const int nfull = n / U;
+    float ea[U], eb[U];
+    auto rd = [&](float(&e)[U], int c) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) e[u] = r.ld(j + u);
+      for (int u = 0; u < U; ++u) e[u] = r.ld(c * U + u);
+    };
+    auto add = [&](const float(&e)[U]) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sum += (double)e[u];
+      for (int u = 0; u < U; ++u) sum += (double)e[u];
+    };
+    if (nfull > 0) rd(ea, 0);
+    int c = 0;
+    for (; c + 2 <= nfull; c += 2) {
+      rd(eb, c + 1);
+      add(ea);
+      if (c + 2 < nfull) rd(ea, c + 2);
+      add(eb);
     }
-    for (; j < n; ++j) sum += (double)r.ld(j);
+    if (c < nfull) add(ea);
+    for (int j = nfull * U; j < n; ++j) sum += (double)r.ld(j);
     *s_inv = (float)(1.0 / sum);
   }
   __syncthreads();

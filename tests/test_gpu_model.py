@@ -169,8 +169,9 @@ def test_long_context_decoder(gpu_ctx):
     # The reference's agent keeps a 32,768-position window (agent.rs:25-26). A decoder of reduced
     # width (hidden 256, 4 heads / 1 kv head of 64: the CPU restatement's attention over 16K
     # positions then takes seconds, not minutes) with two attention layers absorbs 16,400 tokens
-    # in chunks of 512 and decodes two more: every score row past 15,360 positions leaves LDS for
-    # global memory, in the batched softmax of the prefill chunks and in the one-token softmax-V.
+    # in chunks of 512 and decodes two more: score rows of up to 16,401 positions in LDS (up to
+    # 40,000 fit; longer ones are worked on in global memory, tests/test_gpu_ops.py), in the
+    # batched softmax of the prefill chunks and in the one-token softmax-V.
     mw = synth.model_weights(seed=7, hidden=256, vocab=512, n_layers=4, n_dense=1, attention_layers=(1, 3),
                              moe_ff=256, dense_ff=256, n_experts=4, n_heads=4, n_kv_heads=1)
     gm = Model(gpu_ctx, mw)

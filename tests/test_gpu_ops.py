@@ -64,7 +64,7 @@ def test_conv_prefill_matches_oracle(gpu_ctx, oracle, C, L, n):
     same(one, oracle.conv_step(st, bx[:C], w, C, L), "conv_step")
 
 
-@pytest.mark.parametrize("n", [1, 3, 64, 65, 1000, 4096, 20000])
+@pytest.mark.parametrize("n", [1, 3, 64, 65, 1000, 4096, 20000, 40000, 41000])
 def test_softmax_matches_oracle(gpu_ctx, oracle, n):
     g = np.random.default_rng(n)
     rows = 3
@@ -78,7 +78,8 @@ def test_softmax_matches_oracle(gpu_ctx, oracle, n):
 
 
 @pytest.mark.parametrize("n_ctx,nh,nkv,hd", [(1, 1, 1, 2), (2, 1, 1, 2), (1, 2, 1, 2), (37, 8, 2, 64),
-                                             (300, 32, 8, 64), (129, 4, 4, 40), (1000, 32, 8, 64), (16000, 8, 2, 64)])
+                                             (300, 32, 8, 64), (129, 4, 4, 40), (1000, 32, 8, 64), (16000, 8, 2, 64),
+                                             (32769, 8, 2, 64), (41000, 4, 1, 64)])
 def test_attention_decode_matches_oracle(gpu_ctx, oracle, n_ctx, nh, nkv, hd):
     g = np.random.default_rng(n_ctx * 131 + nh)
     q = g.standard_normal(nh * hd).astype(np.float32)
