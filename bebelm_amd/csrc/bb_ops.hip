@@ -20,11 +20,13 @@
 //             cosf of the reference's angle sequence (theta from (float)pos, times
 //             powf(base, -2/d) per pair): the same functions the reference's f32 sin_cos calls.
 #include "bb_device.h"
+#include <utility>
 #include "bb_internal.h"
 
 namespace bb {
 
 constexpr int PV_CHUNK = 32;    // value-column loads in flight per lane in P·V of one row
+constexpr int PVL_MIN_LD = 0;   // rows from this length take the softmax + k_attn_pv_long pair
 constexpr int AT_PV_MIN_T = 8;  // batches of this many tokens take the tiled softmax + P·V
 
 // ---- gated short conv ------------------------------------------------------------------------
@@ -231,13 +233,25 @@ struct Row {
   }
 };
 
+// A score row of n floats into LDS by one wave: whole chunks of 64 by LDS DMA, all issued before
+// the one wait (a plain load-then-store loop waited for every load in turn: at 16K positions,
+// 256 round trips a row), the partial last chunk by plain loads.
+__device__ __forceinline__ void row_to_lds(const float* src, float* lrow, int n) {
+  const int lane = threadIdx.x & 63, nfull = n / 64;
+  for (int c = 0; c < nfull; ++c) __builtin_amdgcn_global_load_lds(src + 64 * c + lane, lrow + 64 * c, 4, 0, 0);
+  if (64 * nfull + lane < n) lrow[64 * nfull + lane] = src[64 * nfull + lane];
+  __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): the copies landed
+}
+
 // softmax.rs:9-22 on row r[0..n) by one wave (exps written back, then scaled).
 template <bool LDS>
 __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, float* s_inv) {
   const int lane = threadIdx.x;
   float m = -__builtin_inff();
+#pragma unroll 8
   for (int j = lane; j < n; j += 64) m = fmaxf(m, r.ld(j));
   m = wave_max(m);
+#pragma unroll 4
   for (int j = lane; j < n; j += 64) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
   __syncthreads();
   if (lane == 0) {
@@ -269,6 +283,7 @@ __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, fl
   }
   __syncthreads();
   const float inv = *s_inv;
+#pragma unroll 8
   for (int j = lane; j < n; j += 64) r.st(j, r.ld(j) * inv);
   __syncthreads();
 }
@@ -286,7 +301,7 @@ __global__ void __launch_bounds__(64) k_attn_softmax_pv(float* sc, const float* 
   const int n = n0 + t + 1;
   float* s = sc + ((size_t)t * n_heads + h) * ld;
   if constexpr (LDS)
-    for (int j = lane; j < n; j += 64) lrow[j] = s[j];
+    row_to_lds(s, lrow, n);
   __syncthreads();
   const Row<LDS> r{LDS ? lrow : s};
   wave_softmax<LDS>(r, n, exptab, &s_inv);
@@ -411,7 +426,7 @@ __global__ void __launch_bounds__(64) k_attn_softmax(float* sc, int n0, int n_he
   const int n = n0 + t + 1;
   float* s = sc + ((size_t)t * n_heads + h) * ld;
   if constexpr (LDS)
-    for (int j = lane; j < n; j += 64) lrow[j] = s[j];
+    row_to_lds(s, lrow, n);
   __syncthreads();
   wave_softmax<LDS>(Row<LDS>{LDS ? lrow : s}, n, exptab, &s_inv);
   if constexpr (LDS)
@@ -475,6 +490,99 @@ __global__ void __launch_bounds__(256) k_attn_pv_tile(const float* __restrict__ 
   }
 }
 
+// P·V of a few tokens over long rows (after k_attn_softmax): out[t][h][d] = Σ_j p[t][h][j]·v[j][g][d]
+// in position order from 0.0 (attention.rs:46-54), the sums of k_attn_softmax_pv. The chains are
+// serial, so what bounds a long row is feeding them: one wave per head keeps too few value loads
+// in flight. Here block (kv head g, dim slice q, token t) is one wave whose lane (hh, d) is head
+// hh of the group and dim d of the slice (G heads x 64/G dims), so the slice's values of a
+// position (64/G floats, shared by the G heads) and the group's probabilities are fetched once,
+// by LDS DMA into a ring of PVL_R chunks of 64 positions, R-1 chunks ahead of the sums.
+constexpr int PVL_CH = 64;
+template <int G>
+struct PvlCfg {
+  static constexpr int DS = 64 / G;                       // dims of a slice
+  static constexpr int NV = DS / 4;                       // 16-byte copies of a chunk's values (1 KB each)
+  static constexpr int NI = NV + G;                       // copies per chunk (G x 256-byte probability rows)
+  static constexpr int R = 63 / NI + 1 < 8 ? 63 / NI + 1 : 8;  // ring slots ((R-1)·NI fits vmcnt)
+};
+
+// Ring slot I of k_attn_pv_long<G>: a chunk's values [64][DS] then its probabilities [G][64].
+// Every slot is an LDS object of its own (a function-local array per instantiation), so the
+// compiler knows which copies in flight a read of one slot can be behind; with one array indexed
+// by slot it waited for every copy before every read.
+template <int G, int I>
+__device__ __forceinline__ float* pvl_slot() {
+  __shared__ __align__(16) float a[PVL_CH * PvlCfg<G>::DS + G * PVL_CH];
+  return a;
+}
+
+template <class F, int... I>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+template <int G>
+__global__ void __launch_bounds__(64) k_attn_pv_long(const float* __restrict__ p, const float* __restrict__ vc,
+                                                    int n0, int n_heads, int n_kv, int ld, float* __restrict__ out) {
+  using C = PvlCfg<G>;
+  constexpr int DS = C::DS, R = C::R, NV = C::NV, NI = C::NI;
+  static_assert(DS >= 4 && DS % 4 == 0, "slices of at least 4 dims");
+  const int g = blockIdx.x, q = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+  const int hh = lane / DS, dl = lane % DS;
+  const int n = n0 + t + 1;
+  const int nch = (n + PVL_CH - 1) / PVL_CH;
+  const float* prow = p + ((size_t)t * n_heads + (size_t)g * G) * ld;
+  // chunk c into slot S: value copy k of lane l = bytes 1024k + 16l of the chunk's [64][DS]
+  // floats (position (1024k + 16l) / (4 DS)); probability copy k = head k's 64 values. Positions
+  // past the row repeat its last one (read, never summed).
+  auto issue = [&](auto S, int c) {
+    float* slot = pvl_slot<G, decltype(S)::value>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's earlier reads are done
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int byte = 1024 * k + 16 * lane, r = byte / (4 * DS), off = byte % (4 * DS);
+      const int j = min(c * PVL_CH + r, n - 1);
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(vc + ((size_t)j * n_kv + g) * 64 + q * DS) + off;
+      __builtin_amdgcn_global_load_lds(src, reinterpret_cast<uint8_t*>(slot) + 1024 * k, 16, 0, 0);
+    }
+    const int j = min(c * PVL_CH + lane, n - 1);
+#pragma unroll
+    for (int k = 0; k < G; ++k)
+      __builtin_amdgcn_global_load_lds(prow + (size_t)k * ld + j, slot + PVL_CH * DS + k * PVL_CH, 4, 0, 0);
+  };
+  unroll_seq([&](auto S) { if (decltype(S)::value < nch) issue(S, decltype(S)::value); },
+             std::make_integer_sequence<int, R - 1>{});
+  float o = 0.0f;
+  // chunk c0 + u sits in slot u (c0 a multiple of R): every read names its slot at compile time
+  for (int c0 = 0; c0 < nch; c0 += R) {
+    unroll_seq(
+        [&](auto U) {
+          constexpr int u = decltype(U)::value;
+          const int c = c0 + u;
+          if (c >= nch) return;
+          if (c + R - 1 < nch) {
+            issue(std::integral_constant<int, (u + R - 1) % R>{}, c + R - 1);
+            constexpr int WL = (R - 1) * NI;  // copies of the chunks after c still in flight
+            __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
+          } else {
+            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+          }
+          const float* slot = pvl_slot<G, u>();
+          const float* svs = slot + dl;
+          const float* sps = slot + PVL_CH * DS + hh * PVL_CH;
+          const int jn = min(PVL_CH, n - c * PVL_CH);
+          if (jn == PVL_CH) {
+#pragma unroll
+            for (int jj = 0; jj < PVL_CH; ++jj) o += sps[jj] * svs[jj * DS];
+          } else {
+            for (int jj = 0; jj < jn; ++jj) o += sps[jj] * svs[jj * DS];
+          }
+        },
+        std::make_integer_sequence<int, R>{});
+  }
+  out[((size_t)t * n_heads + (size_t)g * G + hh) * 64 + q * DS + dl] = o;
+}
+
 hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
                               int hd, float scale, float* scores) {
   const int ld = n0 + T;
@@ -509,6 +617,25 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
               n_kv, ld, out);
     return hipGetLastError();
   }
+  const int G = n_heads / n_kv;
+  if (hd == AT_HD && ld >= PVL_MIN_LD && (G == 1 || G == 2 || G == 4 || G == 8 || G == 16)) {
+    // long rows: the softmax, then P·V with the values streamed through LDS (k_attn_pv_long)
+    if (ld <= OPS_ROW_LDS)
+      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, n0, n_heads, ld);
+    else
+      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64), 0, s, scores, n0, n_heads, ld);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid(n_kv, G, T);
+    switch (G) {
+      case 1: BB_LAUNCH(k_attn_pv_long<1>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 2: BB_LAUNCH(k_attn_pv_long<2>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 4: BB_LAUNCH(k_attn_pv_long<4>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 8: BB_LAUNCH(k_attn_pv_long<8>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      default: BB_LAUNCH(k_attn_pv_long<16>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+    }
+    return hipGetLastError();
+  }
   if (ld <= OPS_ROW_LDS)
     BB_LAUNCH(k_attn_softmax_pv<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, vc, n0, n_heads, n_kv, hd,
               ld, out);
@@ -527,7 +654,7 @@ __global__ void __launch_bounds__(64) k_softmax(float* x, int n) {
   if (threadIdx.x < 32) exptab[threadIdx.x] = exp_table_entry();
   float* g = x + (size_t)blockIdx.x * n;
   if constexpr (LDS)
-    for (int j = threadIdx.x; j < n; j += 64) lrow[j] = g[j];
+    row_to_lds(g, lrow, n);
   __syncthreads();
   wave_softmax<LDS>(Row<LDS>{LDS ? lrow : g}, n, exptab, &s_inv);
   if constexpr (LDS)

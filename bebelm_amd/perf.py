@@ -79,7 +79,17 @@ def drive(args):
     T = cfg.tokens
     ctx = Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    layers = [MoeLayer(ctx, synth.config_layer(args.config, seed=0, layer=l)) for l in range(args.layers)]
+    if args.config == 5:
+        # the 24-layer FFN stack (bench.py's config 5): all layers resident, one token per step
+        from bebelm_amd.model import DenseLayer, FfnStack
+
+        spec = synth.stack_layers(seed=0)
+        built = [(g, MoeLayer(ctx, w) if isinstance(w, synth.MoeWeights) else DenseLayer(ctx, w)) for g, w in spec]
+        layers = [FfnStack(ctx, built)]
+    else:
+        built = []
+        weights = synth._par_map(lambda l: synth.config_layer(args.config, seed=0, layer=l), range(args.layers))
+        layers = [MoeLayer(ctx, w) for w in weights]
     x = torch.from_numpy(synth.hidden_states(0, T)).cuda()
     out = torch.empty_like(x)
     for i in range(args.steps):
@@ -92,6 +102,8 @@ def drive(args):
         dst.copy_(src)
     torch.cuda.synchronize()
     for l in layers:
+        l.close()
+    for _, l in built:
         l.close()
     ctx.close()
     print("perf drive done", flush=True)

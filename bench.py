@@ -474,8 +474,18 @@ def decoder_bench(args, ctx, with_cpu):
         m.absorb(cache, rng_dec.integers(0, mw.vocab, more).astype(np.uint32), 32768)
         ab = time.perf_counter() - t0
         d = decode_rate(16)
+        ctx.reset_stats()
+        ctx.profile(True)
+        for t in rng_dec.integers(0, mw.vocab, 4):
+            m.forward_step(int(t), cache)
+        st = ctx.kernel_stats()
+        ctx.profile(False)
         long_ctx[f"ctx{n_ctx}"] = {"ms_per_token": round(d * 1e3, 3), "tok_s": round(1.0 / d, 1),
-                                   "absorb_ms": round(ab * 1e3, 1), "absorbed_tokens": int(more)}
+                                   "absorb_ms": round(ab * 1e3, 1), "absorbed_tokens": int(more),
+                                   "kernel_ms_per_step": round(sum(v[0] for v in st.values()) / 4, 3),
+                                   "attention_kernel_us_per_step": {
+                                       k: round(v[0] / 4 * 1e3, 1) for k, v in st.items()
+                                       if k.startswith("attn") and v[1]}}
     out = {
         "workload": "LFM2.5-8B-A1B shape: 24 layers (6 GQA attention, 18 short conv), 2 dense + 22 MoE FFNs, "
                     "vocab 128000, Q4_K/Q6_K synthetic weights",

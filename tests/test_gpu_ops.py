@@ -79,7 +79,8 @@ def test_softmax_matches_oracle(gpu_ctx, oracle, n):
 
 @pytest.mark.parametrize("n_ctx,nh,nkv,hd", [(1, 1, 1, 2), (2, 1, 1, 2), (1, 2, 1, 2), (37, 8, 2, 64),
                                              (300, 32, 8, 64), (129, 4, 4, 40), (1000, 32, 8, 64), (16000, 8, 2, 64),
-                                             (32769, 8, 2, 64), (41000, 4, 1, 64)])
+                                             (32769, 8, 2, 64), (41000, 4, 1, 64), (500, 4, 4, 64),
+                                             (700, 4, 2, 64), (900, 16, 2, 64), (333, 16, 1, 64), (65, 2, 2, 64)])
 def test_attention_decode_matches_oracle(gpu_ctx, oracle, n_ctx, nh, nkv, hd):
     g = np.random.default_rng(n_ctx * 131 + nh)
     q = g.standard_normal(nh * hd).astype(np.float32)
