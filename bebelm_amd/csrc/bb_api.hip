@@ -322,6 +322,7 @@ struct MoeWs {
   float* slots;
   int8_t* aq;     // Q8 of act (batched path)
   float* aq_sx;
+  uint16_t* aq_ms = nullptr;
 };
 
 // Workspace of one call: the context's (grown on demand) or a fixed region given by the caller
@@ -339,6 +340,7 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegi
     w.xq.q = cv.take<int8_t>(T * H);
     w.xq.sx = cv.take<float>(T * H / 256);
     w.xq.pairs = batched ? nullptr : cv.take<uint32_t>(T * H / 256 * 12);
+    w.xq.ms = batched && bb::gemm_reads_ms(m->gu_dtype, T * K, E) ? cv.take<uint16_t>(T * H / 256 * 16) : nullptr;
     w.rb.logits = cv.take<float>(T * E);
     w.rb.sel = cv.take<int32_t>(T * K);
     w.rb.wts = cv.take<float>(T * K);
@@ -353,6 +355,7 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegi
     if (batched) {
       w.aq = cv.take<int8_t>(T * K * F);
       w.aq_sx = cv.take<float>(T * K * F / 256);
+      w.aq_ms = bb::gemm_reads_ms(m->dn_dtype, T * K, E) ? cv.take<uint16_t>(T * K * F / 256 * 16) : nullptr;
     }
     if (pass == 0) {
       // the scratch area keeps the PAD bytes of tail slack every dev_alloc'd workspace has
@@ -404,12 +407,14 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
       launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
     launch(c, bb::K_GEMM_GATEUP, [&] {
       return bb::launch_gemm_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
-                                    w.rb, bb::GemmX{w.xq.q, w.xq.sx}, w.act);
+                                    w.rb, bb::GemmX{w.xq.q, w.xq.sx, w.xq.ms}, w.act);
     });
-    launch(c, bb::K_QUANT, [&] { return bb::launch_quant_rows(c->stream, w.act, n_ent, m->F, w.aq, w.aq_sx); });
+    launch(c, bb::K_QUANT, [&] {
+      return bb::launch_quant_rows(c->stream, w.act, n_ent, m->F, w.aq, w.aq_sx, w.aq_ms);
+    });
     launch(c, bb::K_GEMM_DOWN, [&] {
       return bb::launch_gemm_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->E, m->K,
-                                  w.rb, bb::GemmX{w.aq, w.aq_sx}, w.slots);
+                                  w.rb, bb::GemmX{w.aq, w.aq_sx, w.aq_ms}, w.slots);
     });
   } else {
     const int batch_mode = T > 1;

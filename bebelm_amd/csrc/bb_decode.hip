@@ -124,7 +124,8 @@ __global__ void __launch_bounds__(1024) k_route(const float* __restrict__ Wr, co
     const float* col = &xT[tk][i0 & 31][i0 >> 5];
     const float4 v = make_float4(col[0], col[XT_STRIDE], col[2 * XT_STRIDE], col[3 * XT_STRIDE]);
     wave_quantize_xq(v, xq.q + (size_t)t * H + bk * QK, xq.sx + (size_t)t * nbx + bk,
-                     xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr);
+                     xq.pairs ? xq.pairs + ((size_t)t * nbx + bk) * 12 : nullptr,
+                     xq.ms ? xq.ms + ((size_t)t * nbx + bk) * 16 : nullptr);
   }
 }
 

@@ -97,6 +97,7 @@ struct XQBufs {
   int8_t* q;
   float* sx;
   uint32_t* pairs;
+  uint16_t* ms = nullptr;  // per 256-block: the split per-32 sums (min_split_record), when set
 };
 
 // Decode / small-batch path limits: T*k (token, slot) entries per call; members of one expert
@@ -181,7 +182,16 @@ int gemm_member_tiles(int n_ent, int E);
 struct GemmX {
   const int8_t* q;  // Q8 rows
   const float* sx;  // per-256 scales of the rows
+  // per-256 split per-32 sums of the rows (16 halves, min_split_record), or null: then the Q4_K
+  // GEMMs form the min term with a third int8 pass instead of one f16 MFMA
+  const uint16_t* ms = nullptr;
 };
+// Q4_K GEMMs whose groups hold 128+ members on average read the min-term records (tiles of 64
+// members with the f16 min pass); smaller launches never do, so their callers carve none
+constexpr int GEMM_MS_MIN_AVG = 128;
+inline bool gemm_reads_ms(int dtype, size_t n_ent, size_t E) {
+  return dtype == BB_Q4_K && n_ent >= (size_t)GEMM_MS_MIN_AVG * E;
+}
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
                               int E, int K, const RouteBufs& rb, GemmX x, float* act);
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
@@ -202,7 +212,8 @@ constexpr size_t PROJ_GEMM_MIN_T = 32;
 hipError_t launch_one_group(hipStream_t s, int T, RouteBufs rb);
 
 // Q8 rows (quants and per-256 scales only) of n_rows vectors of n floats.
-hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx);
+hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx,
+                             uint16_t* ms = nullptr);
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out);
 

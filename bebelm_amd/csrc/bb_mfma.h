@@ -24,6 +24,8 @@ namespace bb {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 enum : int { GEMM_GATEUP = 0, GEMM_DOWN = 1 };
 
@@ -72,6 +74,7 @@ struct Q4Lane {
   float dd, dm;
   uint32_t hs[2], ls[2];  // sub-block 2g + h: sc >> 3, sc & 7
   int ms[2];              // its min in every byte
+  int m[2];               // its min
 };
 
 __device__ __forceinline__ Q4Lane q4_lane(uint4 hd, int g) {
@@ -92,6 +95,7 @@ __device__ __forceinline__ Q4Lane q4_lane(uint4 hd, int g) {
     o.hs[h] = scv >> 3;
     o.ls[h] = scv & 7u;
     o.ms[h] = (int)splat_byte(mw >> (sh + 8 * h));
+    o.m[h] = (int)((mw >> (sh + 8 * h)) & 0xffu);
   }
   return o;
 }
@@ -109,9 +113,13 @@ __device__ __forceinline__ void q4_step_ops(const uint4 qv, int h, const Q4Lane&
   }
 }
 
-template <int MT>
-__device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, const float* sb, int row,
-                                         float (&acc)[MT][4]) {
+// MF: the min term sm from the members' sum records in msb (min_split_record: member m's 16
+// halves at msb + 32m, lane group g's four at + 8g) by one f16 MFMA per member tile, against
+// weights [64·m_{2g}, 64·m_{2g+1}, m_{2g}, m_{2g+1}]: sm arrives as an exact f32, instead of a
+// third int8 pass over the block (four MFMAs) and a conversion.
+template <int MT, bool MF = false>
+__device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, const float* sb, const uint8_t* msb,
+                                         int row, float (&acc)[MT][4]) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const Q4Lane L = q4_lane(*reinterpret_cast<const uint4*>(wt + 16 * row), g);
   uint4 qv[2];
@@ -149,17 +157,25 @@ __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, c
   v4i Bh[4], Bl[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) q4_step_ops(qv[s & 1], s >> 1, L, Bh[s], Bl[s]);
+  v4h bmin;
+  if constexpr (MF)
+    bmin = (v4h){(_Float16)(64 * L.m[0]), (_Float16)(64 * L.m[1]), (_Float16)L.m[0], (_Float16)L.m[1]};
   v4i ax[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) ax[s] = read_x16(xb, r, 4 * g + s);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     v4i D[3] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+    v4f Dmf = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (MF) {
+      const v4h am = *reinterpret_cast<const v4h*>(msb + (mt * 16 + r) * 32 + 8 * g);
+      Dmf = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bmin, Dmf, 0, 0, 0);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       D[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bh[s], D[0], 0, 0, 0);
       D[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bl[s], D[1], 0, 0, 0);
-      D[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bm[s >> 1], D[2], 0, 0, 0);
+      if constexpr (!MF) D[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[s], Bm[s >> 1], D[2], 0, 0, 0);
       if (mt + 1 < MT) ax[s] = read_x16(xb, (mt + 1) * 16 + r, 4 * g + s);
     }
     const float4 sx4 = *reinterpret_cast<const float4*>(sb + mt * 16 + 4 * g);
@@ -167,7 +183,8 @@ __device__ __forceinline__ void q4_block(const uint8_t* wt, const uint8_t* xb, c
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int sd = 8 * D[0][i] + D[1][i];
-      const float v = sxv[i] * ((L.dd * (float)sd) - (L.dm * (float)D[2][i]));
+      const float smf = MF ? Dmf[i] : (float)D[2][i];
+      const float v = sxv[i] * ((L.dd * (float)sd) - (L.dm * smf));
       acc[mt][i] += v;
     }
   }

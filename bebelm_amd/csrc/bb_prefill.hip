@@ -26,6 +26,7 @@
 #include "bb_internal.h"
 #include "bb_members.h"
 #include "bb_mfma.h"
+#include "bb_rowlane.h"
 
 namespace bb {
 
@@ -288,16 +289,21 @@ __device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // spare bytes), so the copies a wave has in flight after a super-block are a known count.
 // PARTS selects the weight copies, the activation copies or both (the weights of the first
 // super-block are requested before the member rows are known).
-template <int DT, int MT>
+// MF: the Q4_K min term from the activations' split per-32 sums (one f16 MFMA per member tile,
+// min_split_record) instead of a third int8 pass; the stage then also holds the members' sum
+// records (32 bytes each), copied after the activations.
+template <int DT, int MT, bool MF = false>
 struct GemmCfg {
   static constexpr int TB = GemmTraits<DT>::TB;
   static constexpr int NBM = 16 * MT;
   static constexpr int W_UNITS = 2 * TB / 16;
   static constexpr int WCH = (W_UNITS + 63) / 64;
   static constexpr int XCH = NBM * QK / 1024;
+  static constexpr int MSCH = MF ? (NBM * 32 + 1023) / 1024 : 0;  // 1 KB = 32 members' records
   static constexpr int SCH = (NBM + 63) / 64;
-  static constexpr int OPS = (WCH + XCH + SCH + 7) / 8;
+  static constexpr int OPS = (WCH + XCH + MSCH + SCH + 7) / 8;
   static constexpr int SB_FLOATS = (SCH + 1) * 64;  // scales, then the spare copies' bytes
+  static constexpr int MS_BYTES = MSCH * 1024;      // the records (the last copy's tail is spare)
 };
 
 // Waves per SIMD the registers of k_gemm are budgeted for: two blocks of 8 waves share a CU
@@ -306,10 +312,10 @@ constexpr int gemm_waves_per_simd(int dt) { return dt == DT_Q4_K ? 4 : 2; }
 
 enum : int { ISSUE_W = 1, ISSUE_X = 2, ISSUE_ALL = 3 };
 
-template <int DT, int MT, int PARTS>
+template <int DT, int MT, int PARTS, bool MF = false>
 __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes, GemmX x, int n_in, int b,
                                            const int32_t* rowidx, uint8_t* wb, uint8_t* xb, float* sb) {
-  using C = GemmCfg<DT, MT>;
+  using C = GemmCfg<DT, MT, MF>;
   constexpr int TB = C::TB;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nb = n_in / QK;
@@ -330,8 +336,16 @@ __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes,
         const int i = j - C::WCH;
         const int u = i * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
         __builtin_amdgcn_global_load_lds(x.q + (size_t)rowidx[m] * n_in + b * QK + 16 * c, xb + i * 1024, 16, 0, 0);
+      } else if (j < C::WCH + C::XCH + C::MSCH) {
+        // sum records: lane l copies half l & 1 of member 32i + l/2's record (members past the
+        // tile repeat its last one into the spare tail)
+        const int i = j - C::WCH - C::XCH;
+        const int m = min(32 * i + (lane >> 1), C::NBM - 1);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(x.ms) + ((size_t)rowidx[m] * nb + b) * 32 + 16 * (lane & 1);
+        uint8_t* dst = reinterpret_cast<uint8_t*>(sb + C::SB_FLOATS) + i * 1024;
+        __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
       } else {
-        const int i = min(j - C::WCH - C::XCH, C::SCH);  // SCH: the spare bytes
+        const int i = min(j - C::WCH - C::XCH - C::MSCH, C::SCH);  // SCH: the spare bytes
         const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
         __builtin_amdgcn_global_load_lds(x.sx + (size_t)rowidx[m] * nb + b, sb + i * 64, 4, 0, 0);
       }
@@ -350,12 +364,12 @@ __device__ __forceinline__ void lds_dma4(const uint8_t* src, uint8_t* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
 }
 
-template <int DT, int MT>
+template <int DT, int MT, bool MF = false>
 struct IssuePlan {
-  uint8_t* src[8];  // GemmCfg<DT, MT>::OPS <= 8 used
+  uint8_t* src[8];  // GemmCfg<DT, MT, MF>::OPS <= 8 used
 
   __device__ __forceinline__ void issue(int b, uint8_t* wb, uint8_t* xb, float* sb) {
-    using C = GemmCfg<DT, MT>;
+    using C = GemmCfg<DT, MT, MF>;
     constexpr int TB = C::TB;
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
@@ -366,17 +380,20 @@ struct IssuePlan {
           lds_dma16(src[t] + (size_t)b * TB, wb + j * 1024);
       } else if (j < C::WCH + C::XCH) {
         lds_dma16(src[t] + (size_t)b * QK, xb + (j - C::WCH) * 1024);
+      } else if (j < C::WCH + C::XCH + C::MSCH) {
+        lds_dma16(src[t] + (size_t)b * 32, reinterpret_cast<uint8_t*>(sb) + 4 * C::SB_FLOATS +
+                                               (j - C::WCH - C::XCH) * 1024);
       } else {
-        lds_dma4(src[t] + 4 * b, reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH, C::SCH) * 64));
+        lds_dma4(src[t] + 4 * b, reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH - C::MSCH, C::SCH) * 64));
       }
     }
   }
 };
 
-template <int DT, int MT>
-__device__ __forceinline__ void plan_build(IssuePlan<DT, MT>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
+template <int DT, int MT, bool MF>
+__device__ __forceinline__ void plan_build(IssuePlan<DT, MT, MF>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
                                            int n_in, const int32_t* rowidx) {
-  using C = GemmCfg<DT, MT>;
+  using C = GemmCfg<DT, MT, MF>;
   static_assert(C::OPS <= 8, "copy plan size");
   constexpr int TB = C::TB;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -391,8 +408,11 @@ __device__ __forceinline__ void plan_build(IssuePlan<DT, MT>& p, const uint8_t* 
     } else if (j < C::WCH + C::XCH) {
       const int u = (j - C::WCH) * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
       p.src[t] = (uint8_t*)(x.q + (size_t)rowidx[m] * n_in + 16 * c);
+    } else if (j < C::WCH + C::XCH + C::MSCH) {
+      const int m = min(32 * (j - C::WCH - C::XCH) + (lane >> 1), C::NBM - 1);
+      p.src[t] = (uint8_t*)(x.ms + (size_t)rowidx[m] * nb * 16 + 8 * (lane & 1));
     } else {
-      const int i = min(j - C::WCH - C::XCH, C::SCH);
+      const int i = min(j - C::WCH - C::XCH - C::MSCH, C::SCH);
       const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
       p.src[t] = (uint8_t*)(x.sx + (size_t)rowidx[m] * nb);
     }
@@ -403,13 +423,13 @@ __device__ __forceinline__ void plan_build(IssuePlan<DT, MT>& p, const uint8_t* 
 // IssuePlan's copies through buffer resources: a lane's 32-bit source offset of each copy is fixed
 // and super-block b adds a wave-uniform offset (b times the stream's stride), so a copy costs no
 // vector address arithmetic. For inputs whose offsets fit 31 bits.
-template <int DT, int MT>
+template <int DT, int MT, bool MF = false>
 struct BufPlan {
-  __amdgpu_buffer_rsrc_t rw, rx, rs;
-  uint32_t off[8];  // GemmCfg<DT, MT>::OPS <= 8 used
+  __amdgpu_buffer_rsrc_t rw, rx, rs, rm;
+  uint32_t off[8];  // GemmCfg<DT, MT, MF>::OPS <= 8 used
 
   __device__ __forceinline__ void issue(int b, uint8_t* wb, uint8_t* xb, float* sb) {
-    using C = GemmCfg<DT, MT>;
+    using C = GemmCfg<DT, MT, MF>;
     constexpr int TB = C::TB;
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
@@ -419,18 +439,22 @@ struct BufPlan {
         if (j * 64 + lane < C::W_UNITS) buf_dma16(rw, off[t], (uint32_t)(b * TB), wb + j * 1024);
       } else if (j < C::WCH + C::XCH) {
         buf_dma16(rx, off[t], (uint32_t)(b * QK), xb + (j - C::WCH) * 1024);
+      } else if (j < C::WCH + C::XCH + C::MSCH) {
+        buf_dma16(rm, off[t], (uint32_t)(b * 32), reinterpret_cast<uint8_t*>(sb) + 4 * C::SB_FLOATS +
+                                                      (j - C::WCH - C::XCH) * 1024);
       } else {
-        buf_dma4(rs, off[t], (uint32_t)(4 * b), reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH, C::SCH) * 64));
+        buf_dma4(rs, off[t], (uint32_t)(4 * b),
+                 reinterpret_cast<uint8_t*>(sb + min(j - C::WCH - C::XCH - C::MSCH, C::SCH) * 64));
       }
     }
   }
 };
 
 // w0: the block's two packed tiles (wave-uniform); x_rows: rows of x.q / x.sx.
-template <int DT, int MT>
-__device__ __forceinline__ void bufplan_build(BufPlan<DT, MT>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
+template <int DT, int MT, bool MF>
+__device__ __forceinline__ void bufplan_build(BufPlan<DT, MT, MF>& p, const uint8_t* w0, size_t tile_bytes, GemmX x,
                                               int n_in, int x_rows, const int32_t* rowidx) {
-  using C = GemmCfg<DT, MT>;
+  using C = GemmCfg<DT, MT, MF>;
   static_assert(C::OPS <= 8, "copy plan size");
   constexpr int TB = C::TB;
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -438,6 +462,7 @@ __device__ __forceinline__ void bufplan_build(BufPlan<DT, MT>& p, const uint8_t*
   p.rw = buf_rsrc(w0, (uint32_t)(2 * tile_bytes));
   p.rx = buf_rsrc(x.q, (uint32_t)x_rows * (uint32_t)n_in);
   p.rs = buf_rsrc(x.sx, (uint32_t)x_rows * (uint32_t)nb * 4u);
+  p.rm = MF ? buf_rsrc(x.ms, (uint32_t)x_rows * (uint32_t)nb * 32u) : p.rs;
 #pragma unroll
   for (int t = 0; t < C::OPS; ++t) {
     const int j = w + 8 * t;
@@ -448,23 +473,28 @@ __device__ __forceinline__ void bufplan_build(BufPlan<DT, MT>& p, const uint8_t*
     } else if (j < C::WCH + C::XCH) {
       const int u = (j - C::WCH) * 64 + lane, m = u >> 4, c = (u & 15) ^ (m & 15);
       p.off[t] = (uint32_t)rowidx[m] * (uint32_t)n_in + 16u * (uint32_t)c;
+    } else if (j < C::WCH + C::XCH + C::MSCH) {
+      const int m = min(32 * (j - C::WCH - C::XCH) + (lane >> 1), C::NBM - 1);
+      p.off[t] = (uint32_t)rowidx[m] * (uint32_t)nb * 32u + 16u * (uint32_t)(lane & 1);
     } else {
-      const int i = min(j - C::WCH - C::XCH, C::SCH);
+      const int i = min(j - C::WCH - C::XCH - C::MSCH, C::SCH);
       const int m = min((i < C::SCH ? i : 0) * 64 + lane, C::NBM - 1);
       p.off[t] = (uint32_t)rowidx[m] * (uint32_t)nb * 4u;
     }
   }
 }
 
-template <int DT, int KIND, int MT, bool BUF = false>
+template <int DT, int KIND, int MT, bool BUF = false, bool MF = false>
 __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uint8_t* __restrict__ wpk, size_t stride_e, int n_in, int K,
                                               int n_out, int E, int n_ent, RouteBufs rb, GemmX x,
                                               float* __restrict__ out) {
-  using C = GemmCfg<DT, MT>;
+  static_assert(!MF || (DT == DT_Q4_K && MT > 1), "the f16 min term serves the Q4_K member tiles of 64 and 80");
+  using C = GemmCfg<DT, MT, MF>;
   constexpr int TB = C::TB;
   constexpr int NBM = C::NBM;  // members per tile
-  // double-buffered stages: the weights, then the activations followed by their scales
-  constexpr int XS = NBM * QK + 4 * C::SB_FLOATS;
+  // double-buffered stages: the weights, then the activations followed by their scales (and, MF,
+  // the members' sum records)
+  constexpr int XS = NBM * QK + 4 * C::SB_FLOATS + (MF ? C::MS_BYTES : 0);
   __shared__ __align__(16) uint8_t wb0[2 * TB], wb1[2 * TB];
   __shared__ __align__(16) uint8_t xb0[XS], xb1[XS];
   float* const sb0 = reinterpret_cast<float*>(xb0 + NBM * QK);
@@ -524,11 +554,11 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
       const int i = k * 512 + tid;
       sr.v[k] = i < n_ent ? rb.sel[i] : -1;
     }
-    if (!BY_HIT && mt_e == 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    if (!BY_HIT && mt_e == 0) gemm_issue<DT, MT, ISSUE_W, MF>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     if (all_tokens) {
       if (tid < NBM) rowidx[tid] = min(tid, n_tok - 1);
       lds_barrier();
-      gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+      gemm_issue<DT, MT, ISSUE_X, MF>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     }
     const bool live = BY_HIT ? hit_expert_tile(E, NBM, e, mt_e, ti, sr, cnt) : expert_tile(E, NBM, e, mt_e, ti, sr, cnt);
     if (!live) {
@@ -536,7 +566,7 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
       return;
     }
     if (BY_HIT) w0 = wpk + (size_t)ti.e * stride_e + (size_t)(2 * rtile) * tile_bytes;
-    if (BY_HIT || mt_e > 0) gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    if (BY_HIT || mt_e > 0) gemm_issue<DT, MT, ISSUE_W, MF>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_list(sr, n_ent, ti.e, mem);
     if (all_tokens) {
       // output row of token n: its group position, or -1 when it did not choose the expert
@@ -549,7 +579,7 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
   } else {
     if (!find_tile(rb, E, NBM, mtile, ti, sh)) return;
     w0 = wpk + (size_t)__builtin_amdgcn_readfirstlane(ti.e) * stride_e + (size_t)(2 * rtile) * tile_bytes;
-    gemm_issue<DT, MT, ISSUE_W>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+    gemm_issue<DT, MT, ISSUE_W, MF>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
     member_rows<KIND>(rb, ti, K, NBM, rowidx, outrow);
   }
   const float start = ti.g > 1 ? 0.0f : -0.0f;
@@ -560,20 +590,21 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
     for (int i = 0; i < 4; ++i) acc[mt][i] = start;
   lds_barrier();  // rowidx, outrow; the first block's copies stay in flight
   if (MT > 1 || !(KIND == GEMM_GATEUP && n_ent / K <= 16))
-    gemm_issue<DT, MT, ISSUE_X>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
-  using Plan = std::conditional_t<BUF, BufPlan<DT, MT>, IssuePlan<DT, MT>>;
+    gemm_issue<DT, MT, ISSUE_X, MF>(w0, tile_bytes, x, n_in, 0, rowidx, wb0, xb0, sb0);
+  using Plan = std::conditional_t<BUF, BufPlan<DT, MT, MF>, IssuePlan<DT, MT, MF>>;
   Plan plan;
   if constexpr (MT > 1) {
-    if constexpr (BUF) bufplan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, KIND == GEMM_GATEUP ? n_ent / K : n_ent,
+    if constexpr (BUF) bufplan_build<DT, MT, MF>(plan, w0, tile_bytes, x, n_in, KIND == GEMM_GATEUP ? n_ent / K : n_ent,
                                              rowidx);
-    else plan_build<DT, MT>(plan, w0, tile_bytes, x, n_in, rowidx);
+    else plan_build<DT, MT, MF>(plan, w0, tile_bytes, x, n_in, rowidx);
   }
   // The super-block loop over the first M member tiles (the copies still bring all MT).
   auto sweep = [&](auto m) {
     constexpr int M = decltype(m)::value;
     float(&am)[M][4] = reinterpret_cast<float(&)[M][4]>(acc);
     auto block = [&](const uint8_t* wb, const uint8_t* xb, const float* sb) {
-      if constexpr (DT == DT_Q4_K) q4_block<M>(wb + wo, xb, sb, row, am);
+      if constexpr (DT == DT_Q4_K)
+        q4_block<M, MF>(wb + wo, xb, sb, reinterpret_cast<const uint8_t*>(sb) + 4 * C::SB_FLOATS, row, am);
       else q6_block<M>(wb + wo, xb, sb, row, am);
     };
     for (int b = 0; b < nb; b += 2) {
@@ -582,7 +613,7 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
       __syncthreads();
       if (b + 1 < nb) {
         if constexpr (MT > 1) plan.issue(b + 1, wb1, xb1, sb1);
-        else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
+        else gemm_issue<DT, MT, ISSUE_ALL, MF>(w0, tile_bytes, x, n_in, b + 1, rowidx, wb1, xb1, sb1);
       }
       block(wb0, xb0, sb0);
       if (b + 1 >= nb) break;
@@ -590,7 +621,7 @@ __global__ void __launch_bounds__(512, gemm_waves_per_simd(DT)) k_gemm(const uin
       __syncthreads();
       if (b + 2 < nb) {
         if constexpr (MT > 1) plan.issue(b + 2, wb0, xb0, sb0);
-        else gemm_issue<DT, MT, ISSUE_ALL>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
+        else gemm_issue<DT, MT, ISSUE_ALL, MF>(w0, tile_bytes, x, n_in, b + 2, rowidx, wb0, xb0, sb0);
       }
       block(wb1, xb1, sb1);
     }
@@ -1254,7 +1285,10 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   // Q4_K groups of 48+ members on average: member tiles of 80 (groups of 64 +- 8 then take one
   // tile where tiles of 64 often took a second one nearly empty); one group of known size takes
   // the tile that pads it less
-  if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E)
+  // (launches that read the min-term records keep tiles of 64: with the records' LDS and the f16
+  // pass's registers, tiles of 80 fit one block per SIMD pair less)
+  const bool ms = x.ms && gemm_reads_ms(DT, n_ent, E);
+  if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E && !ms)
     mt = E > 1 || (n_ent + 79) / 80 * 5 < (n_ent + 63) / 64 * 4 ? 5 : 4;
   if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
     // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048)
@@ -1286,6 +1320,9 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
               out);
   else if (DT == DT_Q4_K && mt == 5)
     BB_LAUNCH((k_gemm<DT_Q4_K, KIND, 5>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
+  else if (DT == DT_Q4_K && mt == 4 && buf && ms)
+    BB_LAUNCH((k_gemm<DT_Q4_K, KIND, 4, true, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent,
+              rb, x, out);
   else if (mt == 4 && buf)
     BB_LAUNCH((k_gemm<DT, KIND, 4, true>), grid, dim3(512), 0, s, w, stride_e, n_in, K, n_out, E, n_ent, rb, x, out);
   else if (mt == 4)
@@ -1327,7 +1364,8 @@ hipError_t launch_one_group(hipStream_t s, int T, RouteBufs rb) {
 // ---- Q8 rows ---------------------------------------------------------------------------------------
 // One wave per 256-block: amax, scale amax/127, quants round(v·127/amax) (kernels/matmul.rs:141-160).
 __global__ void __launch_bounds__(256) k_quant_rows(const float* __restrict__ x, size_t n_rows, int n,
-                                                    int8_t* __restrict__ q, float* __restrict__ sx) {
+                                                    int8_t* __restrict__ q, float* __restrict__ sx,
+                                                    uint16_t* __restrict__ ms) {
   const int lane = threadIdx.x & 63;
   const size_t nbk = n / QK;
   const size_t wi = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1340,12 +1378,20 @@ __global__ void __launch_bounds__(256) k_quant_rows(const float* __restrict__ x,
   reinterpret_cast<uint32_t*>(q + wi * QK)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
                                                    ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
   if (lane == 0) sx[wi] = amax / 127.0f;
+  if (ms) {
+    int t = q0 + q1 + q2 + q3;
+    t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xf, 0xf, false);  // quad [1,0,3,2]
+    t += __builtin_amdgcn_update_dpp(0, t, 0x4E, 0xf, 0xf, false);  // quad [2,3,0,1]
+    t += __builtin_amdgcn_update_dpp(0, t, 0x141, 0xf, 0xf, false);  // row half-mirror: lanes 8j..8j+7 hold S_j
+    min_split_record(t, ms + wi * 16);
+  }
 }
 
-hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx) {
+hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx,
+                             uint16_t* ms) {
   const size_t waves = n_rows * (size_t)(n / QK);
   if (waves == 0) return hipSuccess;
-  BB_LAUNCH(k_quant_rows, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_rows, n, q, sx);
+  BB_LAUNCH(k_quant_rows, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, x, n_rows, n, q, sx, ms);
   return hipGetLastError();
 }
 

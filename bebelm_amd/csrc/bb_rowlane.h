@@ -31,8 +31,26 @@ __device__ __forceinline__ uint32_t pack16(int lo, int hi) { return ((uint32_t)l
 
 // Q8 quantisation of one 256-block by one wave into the XQ record (lane L holds elements
 // 4L..4L+3). The quants, scale and sums are those of quantize_q8 (matmul.rs:141-160).
+// The min term of a Q4_K block, sm = Σ_j m_j·S_j over the eight per-32 sums S_j of the Q8
+// activations (|S_j| <= 4064), as one f16 MFMA (16x16x16): each S_j is split S = 64·Sh + Sl with
+// Sl = S & 63 in [0, 63] and Sh = S >> 6 in [-64, 63], both exact in f16, and the weights take
+// 64·m_j (<= 4032) and m_j (<= 63), exact too. Every product (<= 258048) and every partial sum of
+// the 16 (<= 2.1e6 < 2^24) is an exact integer in f32, so the MFMA returns sm exactly, in any
+// order of its sums. The record of a 256-block: 16 halves, lane group g's four
+// [Sh_{2g}, Sh_{2g+1}, Sl_{2g}, Sl_{2g+1}] (the sub-blocks of its qs bytes in the GEMM's order).
+// s32: S_j in lanes 8j..8j+7 of the wave.
+__device__ __forceinline__ void min_split_record(int s32, uint16_t* __restrict__ ms) {
+  const int lane = threadIdx.x & 63;
+  if ((lane & 7) == 0) {
+    const int j = lane >> 3, g = j >> 1, o = j & 1;
+    const _Float16 hs = (_Float16)(s32 >> 6), ls = (_Float16)(s32 & 63);
+    ms[4 * g + o] = __builtin_bit_cast(uint16_t, hs);
+    ms[4 * g + 2 + o] = __builtin_bit_cast(uint16_t, ls);
+  }
+}
+
 __device__ __forceinline__ void wave_quantize_xq(float4 v, int8_t* __restrict__ q, float* __restrict__ sx,
-                                                 uint32_t* __restrict__ pairs) {
+                                                 uint32_t* __restrict__ pairs, uint16_t* __restrict__ ms = nullptr) {
   const int lane = threadIdx.x & 63;
   const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   const float amax = wave_max(a);
@@ -46,6 +64,7 @@ __device__ __forceinline__ void wave_quantize_xq(float4 v, int8_t* __restrict__ 
   const int s32 = t16 + __builtin_amdgcn_update_dpp(0, t16, 0x141, 0xf, 0xf, false);  // lanes 8j..8j+7: S_j
   // (half-row mirror: the other quad of the 8-lane group, whose lanes all hold its sum)
   if (lane == 0) *sx = amax / 127.0f;
+  if (ms) min_split_record(s32, ms);
   if (!pairs) return;
   // pair dword j is built by lane j: sources are lanes holding the two sums
   int srcA, srcB;

@@ -12,7 +12,8 @@ What is modelled (per block of the launch the host code in launch_gemm would mak
   * the member tile: expert, first member, count, group base (find_tile, expert_tile,
     hit_expert_tile, find_wide_tile), and the member rows and output rows (member_rows,
     member_rows_list, the all-tokens form);
-  * every copy stream over all super-blocks: weight tile-blocks, activation chunks, scales (raw
+  * every copy stream over all super-blocks: weight tile-blocks, activation chunks, the Q4_K
+    min-term records (when the launch reads them), scales (raw
     global addresses for the plain forms, buffer-resource ranges for the buffer forms: a buffer
     access past its range reads zero, so for those the range itself must lie inside the buffer);
   * every output store.
@@ -30,6 +31,7 @@ TB = {Q4_K: 9216, Q6_K: 13440}  # bytes of one packed tile-block (64 rows x one 
 GATEUP, DOWN = 0, 1
 WIDE_LOG, WIDE_NB, WIDE_MIN_AVG = 4, 256, 192
 GU16_WAVES = 7
+GEMM_MS_MIN_AVG = 128
 MAX_ENTRIES = 64 * 8  # SEL_REGS * 512 of the in-block member lists (bb_members.h)
 
 
@@ -84,13 +86,18 @@ class Violations(list):
             self.append(what)
 
 
+def reads_ms(s):
+    """gemm_reads_ms: the caller carves the min-term records and the Q4_K GEMM reads them."""
+    return s.dt == Q4_K and s.n_ent >= GEMM_MS_MIN_AVG * s.E
+
+
 def launch_choice(s):
     """launch_gemm's choice: ('wide', n_mt) / ('gateup16', n_blocks) / ('gemm', mt, n_mt, buf)."""
     n_ent, E = s.n_ent, s.E
     if s.dt == Q6_K and s.kind == DOWN and n_ent >= WIDE_MIN_AVG * E and n_ent * s.n_in < (1 << 31):
         return ("wide", (n_ent // WIDE_NB + (WIDE_LOG + 1) * E + 7) // 8 * 8)
     mt = 8 if s.dt == Q6_K and n_ent >= 128 * E else (4 if n_ent >= 16 * E else 1)
-    if s.dt == Q4_K and mt == 4 and n_ent >= 48 * E:
+    if s.dt == Q4_K and mt == 4 and n_ent >= 48 * E and not reads_ms(s):
         mt = 5 if E > 1 or (n_ent + 79) // 80 * 5 < (n_ent + 63) // 64 * 4 else 4
     if (s.dt == Q4_K and s.kind == GATEUP and mt == 1 and s.T <= 16 and n_ent <= 64 and E <= 32
             and s.n_out % 32 == 0 and s.n_in in (2048, 512)):
@@ -120,6 +127,8 @@ def check_gemm(s, sel, v, written):
     E, K, bn, nb, tbytes = s.E, s.K, 16 * mt, s.nb, s.tile_bytes
     n_rt = s.n_t64 // 2
     w_size, xq_size, sx_size = E * s.stride, s.x_rows * s.n_in, s.x_rows * nb * 4
+    ms = mt == 4 and buf and reads_ms(s)  # the f16 min-term form (k_gemm<.., 4, true, true>)
+    ms_size = s.x_rows * nb * 32  # 16 halves per row and super-block
     out_size = s.n_ent * s.n_out * 4
     if mt == 1 and s.n_ent > MAX_ENTRIES:
         v.add(f"member lists hold {MAX_ENTRIES} entries, the call has {s.n_ent}")
@@ -188,8 +197,13 @@ def check_gemm(s, sel, v, written):
                 continue
             _check_range(v, f"block {lin}: activations of member {m}", r * s.n_in, r * s.n_in + s.n_in, xq_size)
             _check_range(v, f"block {lin}: scales of member {m}", 4 * r * nb, 4 * (r * nb + nb), sx_size)
+            if ms:
+                _check_range(v, f"block {lin}: min-term records of member {m}", 32 * r * nb, 32 * (r * nb + nb),
+                             ms_size)
         if buf:  # the buffer resources' ranges themselves
             _check_range(v, f"block {lin}: weight resource", w0, w0 + 2 * tbytes, w_size)
+        if ms:
+            _check_range(v, f"block {lin}: min-term resource", 0, s.x_rows * nb * 32, ms_size)
         # output stores: 2 packed tiles x 64 rows -> columns of this row tile
         for k64 in range(2):
             t64 = 2 * rtile + k64

@@ -66,6 +66,17 @@ def test_batched_one_dominant_expert_group(batched, oracle):
     assert sorted(np.nonzero(tr.counts)[0].tolist()) == [3, 9, 17, 30]
 
 
+@pytest.mark.parametrize("E,K,t,down", [(4, 2, 300, Q4_K), (4, 2, 256, Q4_K), (4, 1, 511, Q4_K), (4, 1, 512, Q4_K),
+                                        (8, 4, 256, Q6_K), (1, 1, 200, Q4_K), (2, 2, 129, Q4_K)])
+def test_batched_q4k_min_term_records(batched, oracle, E, K, t, down):
+    # groups of 128+ members on average: the Q4_K GEMMs take the min term from the split per-32
+    # activation sums through one f16 MFMA (both projections when down is Q4_K); 511 tokens of
+    # one pick among 4 experts stay just under the threshold, 512 meet it
+    w = synth.moe_weights(45, hidden=512, moe_ff=512, n_experts=E, n_used=K, down_dtype=down)
+    x = synth.hidden_states(46, t, hidden=512)
+    check_moe(batched, oracle, w, x, t, f"min-term records E={E} k={K} t={t}")
+
+
 def test_batched_zero_inputs(batched, oracle):
     w = synth.moe_weights(39, hidden=512, moe_ff=256, n_experts=8)
     x = synth.hidden_states(40, 40, hidden=512)
