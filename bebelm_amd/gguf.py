@@ -46,11 +46,27 @@ def _missing(rc):
     return False
 
 
+class _Mapping:
+    """Owner of a parsed file's native handle (its mapping or byte copy): closed when the last
+    reference goes, so the GgufFile and every zero-copy tensor view keep it alive."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def __del__(self):
+        h, self.handle = self.handle, None
+        if h:
+            try:
+                lib().bb_gguf_close(h)
+            except Exception:
+                pass
+
+
 class GgufFile:
     """A parsed GGUF file (gguf.rs:143-275): a read-only mapping of the file, or a copy of bytes."""
 
     def __init__(self, handle):
-        self.handle = handle
+        self._map = _Mapping(handle)
         v, a, d = ctypes.c_uint32(), ctypes.c_uint64(), ctypes.c_uint64()
         nt, nm = ctypes.c_size_t(), ctypes.c_size_t()
         check(lib().bb_gguf_header(handle, ctypes.byref(v), ctypes.byref(a), ctypes.byref(d), ctypes.byref(nt),
@@ -81,10 +97,15 @@ class GgufFile:
         check(lib().bb_gguf_open_bytes(buf, len(buf), ctypes.byref(h)))
         return cls(h)
 
+    @property
+    def handle(self):
+        m = getattr(self, "_map", None)
+        return m.handle if m is not None else None
+
     def close(self):
-        if getattr(self, "handle", None):
-            check(lib().bb_gguf_close(self.handle))
-            self.handle = None
+        """Ends this object's use of the file; the mapping itself is released once no tensor
+        view returned by tensor_data is alive any more."""
+        self._map = None
 
     def __enter__(self):
         return self
@@ -106,12 +127,16 @@ class GgufFile:
         return self.tensors[i.value]
 
     def tensor_data(self, t):
-        """tensor_data (gguf.rs:191-193): a zero-copy uint8 view, valid while the file is open."""
+        """tensor_data (gguf.rs:191-193): a zero-copy uint8 view of the tensor's bytes. The view
+        holds the file's mapping (as the reference's slice borrows the GgufFile), so it stays
+        valid after close() or after the GgufFile itself is gone."""
         p, n = ctypes.c_void_p(), ctypes.c_size_t()
         check(lib().bb_gguf_tensor_data(self.handle, t.index, ctypes.byref(p), ctypes.byref(n)))
         if n.value == 0:
             return np.zeros(0, np.uint8)
-        return np.ctypeslib.as_array((ctypes.c_uint8 * n.value).from_address(p.value))
+        buf = (ctypes.c_uint8 * n.value).from_address(p.value)
+        buf._owner = self._map  # the numpy array's base is buf
+        return np.ctypeslib.as_array(buf)
 
     def meta_type(self, key):
         """(value type, element type, items) of a key, or None when absent."""

@@ -168,6 +168,35 @@ def test_open_maps_a_file_and_reports_io_errors(tmp_path):
     assert e.value.code == _lib.BB_ERR_FORMAT
 
 
+def test_tensor_views_outlive_the_file_object(tmp_path):
+    # a zero-copy view holds the mapping: after close(), and after the GgufFile is collected, it
+    # still reads the tensor's bytes; the mapping goes with the last view
+    import gc
+    import weakref
+
+    p = tmp_path / "s.gguf"
+    p.write_bytes(build_sample())
+    g = gguf.GgufFile.open(p)
+    a = g.tensor_data(g.tensors[0])
+    g.close()
+    assert g.handle is None
+    with pytest.raises(BBError):
+        g.tensor_data(g.tensors[0])
+    assert a.view(np.float32).tolist() == [1.0, 2.0, 3.0, 4.0]
+    b = gguf.GgufFile.open(p).tensor_data(gguf.GgufFile.open(p).tensors[1])
+    gc.collect()
+    assert b.view(np.float32).tolist() == [10.0, 11.0, 12.0, 13.0, 14.0, 15.0]
+    g2 = gguf.GgufFile.from_bytes(build_sample())
+    owner = weakref.ref(g2._map)
+    c = g2.tensor_data(g2.tensors[1])[:8]
+    del g2
+    gc.collect()
+    assert owner() is not None and c.view(np.float32).tolist() == [10.0, 11.0]
+    del a, b, c
+    gc.collect()
+    assert owner() is None
+
+
 # ---- tensor.rs:135-167: block sizes and byte sizes, through the table ---------------------------
 
 @pytest.mark.parametrize("ty,n,nbytes", [(12, 2048 * 2048, 2_359_296), (14, 256, 210), (8, 32, 34), (0, 10, 40),
