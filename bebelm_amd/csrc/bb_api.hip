@@ -405,13 +405,17 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
     // fills the trace's counts, offsets and permutation
     if (bb::gemm_member_tiles((int)n_ent, m->E) > 1 || tr)
       launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
+    // (decode batches: the gate/up kernel also writes the act rows' Q8 when it can)
+    bool quantized = false;
     launch(c, bb::K_GEMM_GATEUP, [&] {
       return bb::launch_gemm_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
-                                    w.rb, bb::GemmX{w.xq.q, w.xq.sx, w.xq.ms}, w.act);
+                                    w.rb, bb::GemmX{w.xq.q, w.xq.sx, w.xq.ms}, w.act, w.aq_ms ? nullptr : w.aq,
+                                    w.aq_sx, &quantized);
     });
-    launch(c, bb::K_QUANT, [&] {
-      return bb::launch_quant_rows(c->stream, w.act, n_ent, m->F, w.aq, w.aq_sx, w.aq_ms);
-    });
+    if (!quantized)
+      launch(c, bb::K_QUANT, [&] {
+        return bb::launch_quant_rows(c->stream, w.act, n_ent, m->F, w.aq, w.aq_sx, w.aq_ms);
+      });
     launch(c, bb::K_GEMM_DOWN, [&] {
       return bb::launch_gemm_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->E, m->K,
                                   w.rb, bb::GemmX{w.aq, w.aq_sx, w.aq_ms}, w.slots);

@@ -192,8 +192,11 @@ constexpr int GEMM_MS_MIN_AVG = 128;
 inline bool gemm_reads_ms(int dtype, size_t n_ent, size_t E) {
   return dtype == BB_Q4_K && n_ent >= (size_t)GEMM_MS_MIN_AVG * E;
 }
+// With aq set, a launch that can also writes the Q8 of the act rows (aq, aq_sx: the
+// k_quant_rows output) and sets *quantized; otherwise the caller quantises them.
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
-                              int E, int K, const RouteBufs& rb, GemmX x, float* act);
+                              int E, int K, const RouteBufs& rb, GemmX x, float* act, int8_t* aq = nullptr,
+                              float* aq_sx = nullptr, bool* quantized = nullptr);
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
                             int K, const RouteBufs& rb, GemmX x, float* slots);
 

@@ -1090,23 +1090,25 @@ int gemm_member_tiles(int n_ent, int E) { return n_ent >= 16 * E ? 4 : 1; }
 // ---- Q4_K gate/up of decode batches (at most 16 tokens): weight rows straight into registers -------
 // Work unit = one expert x 16 outputs: the gate rows 16t.. and the up rows 32 + 16t.. of a 64-row
 // packed tile (t = 0, 1), so one wave holds both values of its outputs and applies SwiGLU itself.
-// Block = GU16_WAVES waves, each on its own unit (unit = block·GU16_WAVES + wave, expert-major):
-// E = 32 experts x 112 units of F = 1792 = 512 blocks of 7 waves, two on every CU, so each CU
-// runs the same number of units (blocks of one expert's 8 units left 448 blocks, and the CUs that
-// got two did twice the work of those that got one). The member tile is every token of the batch
-// (outputs of tokens that did not choose the expert are computed and dropped), so its
+// Block = GU16_WAVES = 16 waves on 16 consecutive units of one expert, i.e. the expert's outputs
+// 256j..256j+255 (unit = block·16 + wave, expert-major): E·F/256 blocks (224 for config 2's 32
+// experts and F = 1792), one per CU, each CU the same work. The member tile is every token of
+// the batch (outputs of tokens that did not choose the expert are computed and dropped), so its
 // activations do not depend on the selections: all NB super-blocks of the tokens' Q8 rows
 // (XOR-swizzled 16-byte chunks, as k_gemm stages them) and their scales are copied into LDS
 // once, at the block's start, and shared by its waves. No wave reads another wave's weight rows,
 // so a lane loads its 48 bytes per row and super-block (header and two qs words, the g-major
 // order of q4_block) straight into registers, two super-blocks ahead, through a buffer resource
 // on its packed tile (fixed per-lane offsets, the super-block's offset wave-uniform).
-// The unit's expert is known from the ids, so its first weights are requested before the
-// selections are read (a unit of an expert nobody chose wastes them and leaves). The integer
+// The block's expert is known from its id, so its first weights are requested before the
+// selections are read (a block of an expert nobody chose wastes them and leaves). The integer
 // sums and the f32 epilogue are q4_block's, in the same order; the sum over super-blocks starts
 // at +0.0 (-0.0 for an expert with one member).
+// The block then also writes the Q8 of its members' act rows at super-block j (quantize_q8,
+// model.rs:530-534, the k_quant_rows arithmetic) from its SwiGLU values gathered in LDS, so the
+// down GEMM's input needs no launch of its own.
 constexpr int GU16_SLOTS = 5;  // register slots of one row tile and super-block per lane
-constexpr int GU16_WAVES = 7;
+constexpr int GU16_WAVES = 16;
 
 // A lane's bytes of one row tile and super-block (header and its two qs words). The wave streams
 // its 2·NB (super-block, tile) halves through GU16_SLOTS register slots: half h is computed while
@@ -1152,7 +1154,8 @@ template <int NB>
 __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* __restrict__ wpk, size_t stride_e,
                                                                 int E, int K, int n_out, int n_tok,
                                                                 const int32_t* __restrict__ sel, GemmX x,
-                                                                float* __restrict__ out) {
+                                                                float* __restrict__ out, int8_t* __restrict__ aq,
+                                                                float* __restrict__ aq_sx) {
   constexpr int TB = (int)TB4;
   constexpr int XB = 16 * QK;  // one super-block of the 16 tokens' quants
   constexpr int NW = GU16_WAVES;
@@ -1161,6 +1164,7 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
   __shared__ __align__(16) float sxs[NW * 64];  // scales [b][16] (waves 0-1); the rest absorbs copies
   __shared__ uint64_t exptab[NW * 32];
   __shared__ int32_t selw[NW * 64];
+  __shared__ __align__(16) float actv[16 * QK];  // the block's 256 outputs of each token
   const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_ot = n_out / 16;                 // units per expert
@@ -1253,10 +1257,28 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[h & 1][i]));
     __builtin_amdgcn_sched_barrier(0);
   }
+  const int col = 32 * t64 + 16 * t16 + r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (orow[i] >= 0)
-      out[(size_t)orow[i] * n_out + 32 * t64 + 16 * t16 + r] = silu_tab(acc[0][i], exptab + 32 * w) * acc[1][i];
+  for (int i = 0; i < 4; ++i) {
+    if (orow[i] < 0) continue;
+    const float a = silu_tab(acc[0][i], exptab + 32 * w) * acc[1][i];
+    out[(size_t)orow[i] * n_out + col] = a;
+    actv[(4 * g + i) * QK + (col & (QK - 1))] = a;
+  }
+  // wave n quantises token n's 256 values when the token chose the expert (the block's outputs
+  // are super-block col / 256 of the expert's act rows)
+  lds_barrier();
+  const int n = w;
+  if (n < n_tok) {
+    const unsigned long long bits = (me >> (n * K)) & kmask;
+    if (bits) {
+      const int ii = n * K + __builtin_ctzll(bits);
+      const int row = base + __popcll(me & ((1ull << ii) - 1ull));
+      const int jb = col / QK;
+      const float4 v = *reinterpret_cast<const float4*>(actv + n * QK + 4 * lane);
+      wave_quantize_xq(v, aq + (size_t)row * n_out + jb * QK, aq_sx + (size_t)row * (n_out / QK) + jb, nullptr);
+    }
+  }
 }
 
 // Q6_K down GEMMs whose groups hold this many members on average take k_gemm_wide (blocks of up
@@ -1268,7 +1290,9 @@ constexpr int WIDE_MIN_AVG = 192;
 
 template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
-                              int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out) {
+                              int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out,
+                              int8_t* aq = nullptr, float* aq_sx = nullptr, bool* quantized = nullptr) {
+  if (quantized) *quantized = false;
   const int n_ent = T * K;
   if constexpr (DT == DT_Q6_K && KIND == GEMM_DOWN) {
     // (the kernel addresses x with 32-bit byte offsets)
@@ -1291,13 +1315,16 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   if (DT == DT_Q4_K && mt == 4 && n_ent >= 48 * E && !ms)
     mt = E > 1 || (n_ent + 79) / 80 * 5 < (n_ent + 63) / 64 * 4 ? 5 : 4;
   if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
-    // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048)
-    if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && E <= 32 && n_out % 32 == 0 && (n_in == 2048 || n_in == 512)) {
-      const dim3 grid((E * (n_out / 16) + GU16_WAVES - 1) / GU16_WAVES), block(64 * GU16_WAVES);
+    // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048), which also
+    // quantises the act rows into the caller's buffers
+    if (mt == 1 && rb.sel && aq && T <= 16 && n_ent <= 64 && E <= 32 && n_out % QK == 0 &&
+        (n_in == 2048 || n_in == 512)) {
+      const dim3 grid(E * (n_out / QK)), block(64 * GU16_WAVES);
       if (n_in == 2048)
-        BB_LAUNCH(k_gateup16<8>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out);
+        BB_LAUNCH(k_gateup16<8>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx);
       else
-        BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out);
+        BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx);
+      if (quantized) *quantized = true;
       return hipGetLastError();
     }
   }
@@ -1333,9 +1360,11 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
 }
 
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
-                              int E, int K, const RouteBufs& rb, GemmX x, float* act) {
-  if (dtype == DT_Q4_K) return launch_gemm<DT_Q4_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act);
-  return launch_gemm<DT_Q6_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act);
+                              int E, int K, const RouteBufs& rb, GemmX x, float* act, int8_t* aq, float* aq_sx,
+                              bool* quantized) {
+  if (dtype == DT_Q4_K)
+    return launch_gemm<DT_Q4_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act, aq, aq_sx, quantized);
+  return launch_gemm<DT_Q6_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act, aq, aq_sx, quantized);
 }
 
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
@@ -1371,20 +1400,7 @@ __global__ void __launch_bounds__(256) k_quant_rows(const float* __restrict__ x,
   const size_t wi = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wi >= n_rows * nbk) return;
   const float4 v = *reinterpret_cast<const float4*>(x + wi * QK + 4 * lane);
-  const float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  const float amax = wave_max(a);
-  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-  const int q0 = q8_round(v.x * inv), q1 = q8_round(v.y * inv), q2 = q8_round(v.z * inv), q3 = q8_round(v.w * inv);
-  reinterpret_cast<uint32_t*>(q + wi * QK)[lane] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
-                                                   ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
-  if (lane == 0) sx[wi] = amax / 127.0f;
-  if (ms) {
-    int t = q0 + q1 + q2 + q3;
-    t += __builtin_amdgcn_update_dpp(0, t, 0xB1, 0xf, 0xf, false);  // quad [1,0,3,2]
-    t += __builtin_amdgcn_update_dpp(0, t, 0x4E, 0xf, 0xf, false);  // quad [2,3,0,1]
-    t += __builtin_amdgcn_update_dpp(0, t, 0x141, 0xf, 0xf, false);  // row half-mirror: lanes 8j..8j+7 hold S_j
-    min_split_record(t, ms + wi * 16);
-  }
+  wave_quantize_xq(v, q + wi * QK, sx + wi, nullptr, ms ? ms + wi * 16 : nullptr);
 }
 
 hipError_t launch_quant_rows(hipStream_t s, const float* x, size_t n_rows, int n, int8_t* q, float* sx,

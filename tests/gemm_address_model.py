@@ -30,7 +30,7 @@ Q4_K, Q6_K = 12, 14
 TB = {Q4_K: 9216, Q6_K: 13440}  # bytes of one packed tile-block (64 rows x one super-block)
 GATEUP, DOWN = 0, 1
 WIDE_LOG, WIDE_NB, WIDE_MIN_AVG = 4, 256, 192
-GU16_WAVES = 7
+GU16_WAVES = 16
 GEMM_MS_MIN_AVG = 128
 MAX_ENTRIES = 64 * 8  # SEL_REGS * 512 of the in-block member lists (bb_members.h)
 
@@ -54,6 +54,7 @@ class Shape:
     n_out: int
     E: int
     K: int
+    quant: bool = True  # the MoE block's gate/up launch gets the act rows' Q8 buffers
 
     @property
     def n_ent(self):
@@ -99,9 +100,9 @@ def launch_choice(s):
     mt = 8 if s.dt == Q6_K and n_ent >= 128 * E else (4 if n_ent >= 16 * E else 1)
     if s.dt == Q4_K and mt == 4 and n_ent >= 48 * E and not reads_ms(s):
         mt = 5 if E > 1 or (n_ent + 79) // 80 * 5 < (n_ent + 63) // 64 * 4 else 4
-    if (s.dt == Q4_K and s.kind == GATEUP and mt == 1 and s.T <= 16 and n_ent <= 64 and E <= 32
-            and s.n_out % 32 == 0 and s.n_in in (2048, 512)):
-        return ("gateup16", (E * (s.n_out // 16) + GU16_WAVES - 1) // GU16_WAVES)
+    if (s.dt == Q4_K and s.kind == GATEUP and mt == 1 and s.quant and s.T <= 16 and n_ent <= 64 and E <= 32
+            and s.n_out % QK == 0 and s.n_in in (2048, 512)):
+        return ("gateup16", E * (s.n_out // QK))  # blocks of 16 waves over 256 outputs of one expert
     bn = 16 * mt
     n_mt = E * ((s.T + bn - 1) // bn) if mt == 1 else ((n_ent + bn - 1) // bn + E + 7) // 8 * 8
     buf = s.x_rows * s.n_in < (1 << 31) and 2 * s.tile_bytes < (1 << 31)
@@ -279,11 +280,16 @@ def check_gateup16(s, sel, v, written):
         v.add(f"gateup16 reads 64 selections from a carve of {sel_alloc} bytes")
     if s.n_ent > 64:
         v.add("gateup16 with more than 64 entries")
+    NW = GU16_WAVES
+    aq_size, aqs_size = s.n_ent * s.n_out, s.n_ent * (s.n_out // QK) * 4
+    qwritten = np.zeros((s.n_ent, s.n_out // QK), np.int32)
     for b in range(n_blocks):
-        for w in range(GU16_WAVES):
+        if (b * NW) // n_ot != (b * NW + NW - 1) // n_ot:
+            v.add(f"gateup16 block {b} spans two experts")
+        for w in range(NW):
             # activation and scale copies: rows clamped to the batch, super-blocks below NB
-            for t in range((4 * NB + GU16_WAVES - 1) // GU16_WAVES):
-                j = min(w + GU16_WAVES * t, 4 * NB - 1)
+            for t in range((4 * NB + NW - 1) // NW):
+                j = min(w + NW * t, 4 * NB - 1)
                 bb, mm = j >> 2, 4 * (j & 3) + 3
                 row = min(mm, s.T - 1)
                 _check_range(v, "gateup16 activation copy", row * NB * QK + bb * QK, row * NB * QK + bb * QK + QK,
@@ -291,7 +297,7 @@ def check_gateup16(s, sel, v, written):
             u = min(64 * w + 63, 16 * NB - 1)
             _check_range(v, "gateup16 scale copy", 4 * (min(u & 15, s.T - 1) * NB + (u >> 4)),
                          4 * (min(u & 15, s.T - 1) * NB + (u >> 4)) + 4, s.T * NB * 4)
-            unit = b * GU16_WAVES + w
+            unit = b * NW + w
             if unit >= E * n_ot:
                 continue  # its resource has range 0: every load reads zero
             e, o = unit // n_ot, unit % n_ot
@@ -311,6 +317,18 @@ def check_gateup16(s, sel, v, written):
                 _check_range(v, "gateup16 store", 4 * (orow * s.n_out + col0), 4 * (orow * s.n_out + col0 + 16),
                              out_size)
                 written[orow, col0:col0 + 16] += 1
+            # wave w quantises token w's 256 values at super-block col0 / 256
+            if w < s.T:
+                mine = [i for i in range(K) if w * K + i in lst]
+                if mine:
+                    orow, jb = base + lst.index(w * K + mine[0]), col0 // QK
+                    _check_range(v, "gateup16 act Q8 store", orow * s.n_out + jb * QK, orow * s.n_out + jb * QK + QK,
+                                 aq_size)
+                    _check_range(v, "gateup16 act scale store", 4 * (orow * (s.n_out // QK) + jb),
+                                 4 * (orow * (s.n_out // QK) + jb) + 4, aqs_size)
+                    qwritten[orow, jb] += 1
+    if not np.all(qwritten == 1):
+        v.add(f"gateup16 act Q8: {(qwritten != 1).sum()} (row, super-block) pairs not written exactly once")
 
 
 def check(s, sel):

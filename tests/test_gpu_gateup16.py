@@ -1,10 +1,11 @@
 """GPU parity of the Q4_K gate/up GEMM of decode batches (k_gateup16: at most 16 tokens, T*k <= 64,
 hidden 512 or 2048, member tiles of every token of the batch, weight rows streamed into registers,
-7-wave blocks of per-wave units, partial last block) on the grouped path, against the CPU
-restatement of Model::moe_ffn_batch (model.rs:286-371): routing, weights and block outputs
-bit-identical. The cases reach its edges: a single expert, experts nobody chose (their units leave
-early), one-member experts (sums started at -0.0), k = 8 with 8 tokens (64 entries), moe_ff not a
-multiple of 128 (the last block's units past the grid's end), zero and scaled input rows.
+16-wave blocks over 256 outputs of one expert that also write the act rows' Q8 for the down GEMM)
+on the grouped path, against the CPU restatement of Model::moe_ffn_batch (model.rs:286-371):
+routing, weights and block outputs bit-identical. The cases reach its edges: a single expert,
+experts nobody chose (their blocks leave early), one-member experts (sums started at -0.0), k = 8
+with 8 tokens (64 entries), k = E, moe_ff of 1, 4, 5 and 7 act super-blocks, zero and scaled
+input rows (a zero act block quantises to scale 0).
 """
 import numpy as np
 import pytest
@@ -28,12 +29,12 @@ def batched(gpu_ctx):
 # (seed, hidden, moe_ff, experts, k, tokens, down)
 CASES = [
     (1, 512, 512, 1, 1, 3, Q4_K),      # one expert: every token its member
-    (2, 512, 256, 32, 4, 1, Q4_K),     # 4 one-member experts, 28 nobody chose; 512 units
+    (2, 512, 256, 32, 4, 1, Q4_K),     # 4 one-member experts, 28 nobody chose; one block each
     (3, 512, 1792, 32, 4, 16, Q6_K),   # the decode-batch shape at hidden 512
     (4, 2048, 1792, 32, 8, 8, Q4_K),   # 64 entries, k = 8
-    (5, 2048, 1024, 13, 3, 11, Q4_K),   # 832 units: the last block partly past the grid's end
+    (5, 2048, 1024, 13, 3, 11, Q4_K),   # 13 experts x 4 blocks
     (6, 2048, 256, 5, 5, 12, Q6_K),    # k = E: every token chooses every expert
-    (7, 512, 1280, 7, 2, 16, Q4_K),    # moe_ff 1280: 80 units per expert, 40 packed tiles
+    (7, 512, 1280, 7, 2, 16, Q4_K),    # moe_ff 1280: 5 blocks per expert, 40 packed tiles
     (8, 2048, 1792, 32, 4, 2, Q6_K),
 ]
 
