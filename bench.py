@@ -152,6 +152,8 @@ def layer_work(w, counts, T, batched, prerouted=False):
         gate_b = u_hit * gu + w.router.nbytes + T * H * 4 + n_ent * F * 4
     else:
         gate_b = u_hit * gu + T * q8_bytes(H) + n_ent * F * 4
+        if T <= 16 and n_ent <= 64 and w.gate_dtype == synth.Q4_K and w.n_experts <= 32:
+            gate_b += n_ent * q8_bytes(F)  # k_gateup16 also writes the act rows' Q8
     # one token on its own (not in the stack): the down GEMV also combines, writing H outputs
     # instead of K slot rows
     combine_in_down = not batched and T == 1 and K <= 4 and not prerouted
