@@ -15,6 +15,9 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+#if defined(__AVX2__)
+#include <immintrin.h>
+#endif
 
 namespace {
 
@@ -256,10 +259,51 @@ float dot_variant(const float* a, const float* b, size_t n, int variant) {
   return sum;
 }
 
+// --- integer dots of unsigned weight bytes against Q8 activations -------------------------------
+// The reference computes its Q4_K / Q6_K block dots with AVX-512 VNNI byte dots on x86 builds
+// that have them (matmul.rs:262-289, :699-744) and with widening multiply-adds elsewhere. The
+// sums are exact integers (no overflow: |sd| < 2^25), so any grouping gives the same value;
+// the vector forms below only make the restatement run at a speed comparable to the
+// reference's, for the CPU baseline. Each has the scalar loop it must equal beside it
+// (tests/test_oracle_pins.py checks them against brute-force dequantised dots).
+#if defined(__AVX2__)
+// 32 bytes: u8 a[i]·s8 b[i] summed in groups of four, 8 i32 lanes (lane k: bytes 4k..4k+3).
+inline __m256i dot_u8s8(__m256i a, __m256i b) {
+#if defined(__AVX512VNNI__) && defined(__AVX512VL__)
+  return _mm256_dpbusd_epi32(_mm256_setzero_si256(), a, b);
+#else
+  // pairs of products in i16: a <= 63 and |b| <= 127, so a pair stays below 2^14 (no saturation)
+  return _mm256_madd_epi16(_mm256_maddubs_epi16(a, b), _mm256_set1_epi16(1));
+#endif
+}
+inline int32_t hsum8(__m256i v) {
+  __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4e));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xb1));
+  return _mm_cvtsi128_si32(s);
+}
+inline __m256i load32(const void* p) { return _mm256_loadu_si256(static_cast<const __m256i*>(p)); }
+// lanes 0-3 = a, lanes 4-7 = b (the scales of a 32-byte run's two 16-element sub-blocks)
+inline __m256i two_scales(int32_t a, int32_t b) { return _mm256_setr_epi32(a, a, a, a, b, b, b, b); }
+#endif
+
 // --- Q4_K x Q8 (matmul.rs:210-298) ---
 // Σ_j sc_j·<nib_j, qx_j>, exact i32 (q4k_block_sd_portable, :251-260; equal to the VNNI
-// and sdot variants by the reference's own tests :1456-1485).
+// and sdot variants by the reference's own tests :1456-1485): sub-block 2c is the low nibbles
+// of qs bytes 32c.., 2c+1 their high nibbles.
 int32_t q4k_sd(const uint8_t* qs, const int32_t sc[8], const int8_t* qx) {
+#if defined(__AVX2__)
+  const __m256i m4 = _mm256_set1_epi8(0x0f);
+  __m256i acc = _mm256_setzero_si256();
+  for (int c = 0; c < 4; ++c) {
+    const __m256i q = load32(qs + 32 * c);
+    const __m256i lo = _mm256_and_si256(q, m4), hi = _mm256_and_si256(_mm256_srli_epi16(q, 4), m4);
+    acc = _mm256_add_epi32(acc, _mm256_mullo_epi32(dot_u8s8(lo, load32(qx + 64 * c)), _mm256_set1_epi32(sc[2 * c])));
+    acc = _mm256_add_epi32(acc,
+                           _mm256_mullo_epi32(dot_u8s8(hi, load32(qx + 64 * c + 32)), _mm256_set1_epi32(sc[2 * c + 1])));
+  }
+  return hsum8(acc);
+#else
   int32_t sd = 0;
   for (int c = 0; c < 4; ++c) {
     int32_t lo = 0, hi = 0;
@@ -270,6 +314,7 @@ int32_t q4k_sd(const uint8_t* qs, const int32_t sc[8], const int8_t* qx) {
     sd += sc[2 * c] * lo + sc[2 * c + 1] * hi;
   }
   return sd;
+#endif
 }
 
 // matmul.rs:220-243.
@@ -322,8 +367,20 @@ void unpack_q6k(const uint8_t* block, int8_t wq[256], int32_t sc[16]) {
   }
 }
 
-// wsd_q6k (:559-572): Σ_s sc[s]·<wq_s, qx_s>, exact i32.
+// wsd_q6k (:559-572): Σ_s sc[s]·<wq_s, qx_s>, exact i32. Vector form: wq + 32 is the unsigned
+// quant q, and Σ sc·Σ wq·x = Σ sc·Σ q·x − 32·Σ sc·Σ x.
 int32_t wsd_q6k(const int8_t* wq, const int8_t* qx, const int32_t sc[16]) {
+#if defined(__AVX2__)
+  const __m256i off = _mm256_set1_epi8(32), ones = _mm256_set1_epi8(1);
+  __m256i aq = _mm256_setzero_si256(), ax = _mm256_setzero_si256();
+  for (int j = 0; j < 8; ++j) {
+    const __m256i q = _mm256_add_epi8(load32(wq + 32 * j), off), x = load32(qx + 32 * j);
+    const __m256i scv = two_scales(sc[2 * j], sc[2 * j + 1]);
+    aq = _mm256_add_epi32(aq, _mm256_mullo_epi32(dot_u8s8(q, x), scv));
+    ax = _mm256_add_epi32(ax, _mm256_mullo_epi32(dot_u8s8(ones, x), scv));
+  }
+  return hsum8(aq) - 32 * hsum8(ax);
+#else
   int32_t acc = 0;
   for (int s = 0; s < 16; ++s) {
     int32_t d = 0;
@@ -331,10 +388,32 @@ int32_t wsd_q6k(const int8_t* wq, const int8_t* qx, const int32_t sc[16]) {
     acc += d * sc[s];
   }
   return acc;
+#endif
 }
 
-// q6k_block_idot_portable (:650-682): the fused unpack, same exact integer.
+// q6k_block_idot_portable (:650-682): the fused unpack, same exact integer. Vector form: group g
+// of half n is 32 unsigned quants q = (ql nibble) | (2 qh bits << 4) of sub-blocks 2g, 2g+1,
+// and Σ sc·Σ (q − 32)·x = Σ sc·Σ q·x − 32·Σ sc·Σ x.
 int32_t q6k_idot_fused(const uint8_t* block, const int8_t* qx) {
+#if defined(__AVX2__)
+  const __m256i m4 = _mm256_set1_epi8(0x0f), m2 = _mm256_set1_epi8(0x03), ones = _mm256_set1_epi8(1);
+  __m256i aq = _mm256_setzero_si256(), ax = _mm256_setzero_si256();
+  for (int n = 0; n < 2; ++n) {
+    const __m256i qh = load32(block + 128 + 32 * n);
+    const int8_t* scn = reinterpret_cast<const int8_t*>(block + 192 + 8 * n);
+    for (int g = 0; g < 4; ++g) {
+      const __m256i ql = load32(block + 64 * n + 32 * (g & 1));
+      const __m256i nib = (g >> 1) ? _mm256_and_si256(_mm256_srli_epi16(ql, 4), m4) : _mm256_and_si256(ql, m4);
+      const __m256i h2 = _mm256_and_si256(_mm256_srl_epi16(qh, _mm_cvtsi32_si128(2 * g)), m2);
+      const __m256i q = _mm256_or_si256(nib, _mm256_slli_epi16(h2, 4));
+      const __m256i x = load32(qx + 128 * n + 32 * g);
+      const __m256i scv = two_scales(scn[2 * g], scn[2 * g + 1]);
+      aq = _mm256_add_epi32(aq, _mm256_mullo_epi32(dot_u8s8(q, x), scv));
+      ax = _mm256_add_epi32(ax, _mm256_mullo_epi32(dot_u8s8(ones, x), scv));
+    }
+  }
+  return hsum8(aq) - 32 * hsum8(ax);
+#else
   static const int GROUPS[4][3] = {{0, 0, 0}, {32, 0, 2}, {0, 1, 4}, {32, 1, 6}};
   int32_t acc = 0;
   for (int n = 0; n < 2; ++n) {
@@ -357,6 +436,7 @@ int32_t q6k_idot_fused(const uint8_t* block, const int8_t* qx) {
     }
   }
   return acc;
+#endif
 }
 
 // dot_q6k_block_q8 (:633-642).

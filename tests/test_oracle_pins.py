@@ -80,6 +80,27 @@ def test_q4k_integer_dot_brute_force(oracle, seed):
         assert abs(real - (d * sd - dmin * sm)) <= 1e-5 * max(abs(real), 1e-3) + 1e-6 * np.sum(np.abs(w * qx))
 
 
+@pytest.mark.parametrize("fill", [0xFF, 0x00, 0xF0, 0x0F])
+@pytest.mark.parametrize("xv", [127, -127])
+def test_integer_dots_at_extremes(oracle, fill, xv):
+    # every quant and scale at its largest (or smallest) value against activations all +-127
+    # (and alternating): the vector forms of the block dots must not saturate or wrap
+    for alt in (False, True):
+        qx = np.full(256, xv, np.int8)
+        if alt:
+            qx[1::2] = -xv
+        blk4 = np.full(144, fill, np.uint8)
+        _, _, sc, _, nib = np_unpack_q4k(blk4)
+        assert oracle.q4k_block_sd(blk4, qx) == int(np.sum(np.repeat(sc, 32) * nib * qx.astype(np.int64)))
+        for scale_byte in (0x7F, 0x80):
+            blk6 = np.full(210, fill, np.uint8)
+            blk6[192:208] = scale_byte
+            _, sc6, q6 = np_unpack_q6k(blk6)
+            want = int(np.sum(np.repeat(sc6, 16) * q6 * qx.astype(np.int64)))
+            assert oracle.q6k_block_idot(blk6, qx) == want
+            assert oracle.q6k_block_idot(blk6, qx, buffered=True) == want
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_q6k_integer_dot_brute_force(oracle, seed):
     g = np.random.default_rng(100 + seed)
