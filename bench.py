@@ -371,16 +371,15 @@ def run_config(args, ctx, config, steps, warmup, with_cpu, cpu_share=1.0):
             result["cpu_baseline"] = cpu_baseline(lambda i: bbo.ffn_stack(layers_o, x_host.reshape(-1), 1, 1e-5), T,
                                                   secs, "the 24-layer FFN stack (T=1)", args.cpu_reps)
         elif prefill:
-            # one call takes about 0.3 s (T = 512) or 2 s (T = 4096) on all cores: repetitions of
-            # one call each. Config 3: 20 of them, then 3 on one core (about 5 s each); config 4:
-            # 5 on all cores only (one call on one core takes about 30 s, beyond the bench's
-            # budget; config 3's one-core figure is the same kernels' per-token rate)
+            # one call takes about 0.3 s (T = 512) or 2-4 s (T = 4096) on all cores: repetitions
+            # of one call each. Config 3: 20 of them, then 3 on one core (about 1.2 s each);
+            # config 4: 5 on all cores, then one call on one core (about 13 s)
             sample = weights[: min(L, 4)]
             xs = x_host.reshape(-1)
             reps = 20 if config == 3 else 5
             result["cpu_baseline"] = cpu_baseline(lambda i: bbo.moe_ffn_batch(sample[i % len(sample)], xs, T), T,
                                                   1e-3 * reps, f"moe_ffn_batch (T={T}, {len(sample)} rotated layers)",
-                                                  reps, one_core=config == 3, reps_1core=3)
+                                                  reps, reps_1core=3 if config == 3 else 1)
         else:
             sample = weights[: min(L, 4)]
             xs = x_host.reshape(-1)
