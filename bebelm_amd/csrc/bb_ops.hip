@@ -254,7 +254,25 @@ __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, fl
 #pragma unroll 4
   for (int j = lane; j < n; j += 64) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
   __syncthreads();
-  if (lane == 0) {
+  // The reference's sum is one left-to-right chain of f64 adds (softmax.rs:14-17), but only
+  // inv = (float)(1 / sum) leaves it. Every summand is >= 0, so the chain's sum S_c and this
+  // wave's tree sum S_t (each lane's elements in order, then a butterfly) are both within
+  // (n + 5 + n/64)·u·S of the exact sum S (u = 2^-53, recursive summation bounds), and so
+  // within B = (n + 64)·2^-51·S_t of each other with room to spare for the rounding of B and of
+  // the interval's ends. (float)(1 / x) never increases as x grows: when the ends S_t − B and
+  // S_t + B give the same float, S_c gives it too. Otherwise (about one row in 10^4 at 16K
+  // positions, and rows holding NaN or infinities) lane 0 runs the chain itself.
+  // (IEEE addition commutes, so both lanes of every butterfly pair form the same sum and all 64
+  // lanes end with the same S_t.)
+  double st = 0.0;
+  for (int j = lane; j < n; j += 64) st += (double)r.ld(j);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) st += __shfl_xor(st, o);
+  const double bnd = (double)(n + 64) * 0x1p-51 * st;
+  const float f_lo = (float)(1.0 / (st - bnd)), f_hi = (float)(1.0 / (st + bnd));
+  if (f_lo == f_hi) {
+    if (lane == 0) *s_inv = f_lo;
+  } else if (lane == 0) {
     // left to right; the next 16 values are read while the adds of the current 16 run (the adds
     // are one dependent chain, the reads are not)
     constexpr int U = 16;

@@ -77,6 +77,36 @@ def test_softmax_matches_oracle(gpu_ctx, oracle, n):
     same(got, want, f"softmax n={n}")
 
 
+@pytest.mark.parametrize("n", [21324, 33825, 40880, 20000])
+def test_softmax_of_equal_scores(gpu_ctx, oracle, n):
+    # every exp is 1.0, so the sum is exactly n: at 21,324, 33,825 and 40,880 positions the
+    # interval test cannot settle (float)(1 / sum) and the kernel runs the reference's chain of
+    # adds (in LDS, and past the 40,000 positions LDS takes, in global memory); at 20,000 the
+    # interval settles it (tests/test_softmax_interval.py)
+    x = np.full(2 * n, 0.75, np.float32)
+    x[n:] = -3.5
+    got = x.copy()
+    K.softmax(gpu_ctx, got, 2)
+    want = np.concatenate([oracle.softmax(x[:n]), oracle.softmax(x[n:])])
+    same(got, want, f"softmax of equal scores n={n}")
+    assert np.all(got.view(np.uint32) == np.float32(1.0 / n).view(np.uint32))
+
+
+@pytest.mark.parametrize("n_ctx,G", [(21324, 4), (33825, 1), (40880, 2)])
+def test_attention_decode_equal_scores(gpu_ctx, oracle, n_ctx, G):
+    # identical key rows give every head a row of equal scores (the chain-of-adds case above),
+    # through the softmax and k_attn_pv_long
+    g = np.random.default_rng(n_ctx)
+    nkv, hd = 2, 64
+    nh = nkv * G
+    q = g.standard_normal(nh * hd).astype(np.float32)
+    k = np.tile(g.standard_normal(nkv * hd).astype(np.float32), n_ctx)
+    v = g.standard_normal(n_ctx * nkv * hd).astype(np.float32)
+    out = np.zeros(nh * hd, np.float32)
+    K.attention_decode(gpu_ctx, q, k, v, n_ctx, nh, nkv, hd, out)
+    same(out, oracle.attention_decode(q, k, v, n_ctx, nh, nkv, hd), f"attention of equal scores n_ctx={n_ctx}")
+
+
 @pytest.mark.parametrize("n_ctx,nh,nkv,hd", [(1, 1, 1, 2), (2, 1, 1, 2), (1, 2, 1, 2), (37, 8, 2, 64),
                                              (300, 32, 8, 64), (129, 4, 4, 40), (1000, 32, 8, 64), (16000, 8, 2, 64),
                                              (32769, 8, 2, 64), (41000, 4, 1, 64), (500, 4, 4, 64),
