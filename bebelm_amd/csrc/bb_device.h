@@ -55,6 +55,26 @@ __device__ __forceinline__ int q8_round(float y) {
   return (int)r;
 }
 
+// ---- buffer resources ------------------------------------------------------------------------
+// gfx9 raw buffers (base, byte size, word 3 = 0x00020000): loads through them take a 32-bit
+// per-lane offset and a wave-uniform one, so a lane keeps one register per stream instead of a
+// 64-bit address per load. An access at or past the size reads zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+// global_load_lds through a buffer: 16 (or 4) bytes a lane into dst + 16·lane (4·lane)
+__device__ __forceinline__ void buf_dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, (int)voff, (int)soff, 0,
+                                           0);
+}
+__device__ __forceinline__ void buf_dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint8_t* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, (int)voff, (int)soff, 0,
+                                           0);
+}
+
 // ---- block barrier for LDS traffic only ----------------------------------------------------
 // __syncthreads() also waits for every global load the wave has in flight (its release fence
 // waits on vmcnt, which counts loads and LDS-DMA copies alike). Where a barrier only orders LDS

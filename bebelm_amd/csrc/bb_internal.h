@@ -29,7 +29,9 @@ void free_owned(ModelOwned& o);
 void model_adopt(bb_model* m, ModelOwned&& o);
 
 // Profiling: when set, kernels are launched with hipExtLaunchKernelGGL, which has the kernel's
-// own dispatch stamp the two events (exact start and end, no queue gaps in between).
+// own dispatch stamp the events (exact start and end, no queue gaps in between). A launcher
+// that runs several kernels has the first stamp the start and each one the stop, so the pair
+// spans all of them.
 struct LaunchEvents {
   hipEvent_t start = nullptr, stop = nullptr;
 };
@@ -37,11 +39,13 @@ LaunchEvents& launch_events();  // per host thread
 
 #define BB_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                  \
   do {                                                                                                     \
-    const ::bb::LaunchEvents& bb_ev_ = ::bb::launch_events();                                              \
-    if (bb_ev_.start)                                                                                      \
+    ::bb::LaunchEvents& bb_ev_ = ::bb::launch_events();                                                    \
+    if (bb_ev_.stop) {                                                                                     \
       hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, bb_ev_.start, bb_ev_.stop, 0, __VA_ARGS__); \
-    else                                                                                                   \
+      bb_ev_.start = nullptr;                                                                              \
+    } else {                                                                                               \
       hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                                 \
+    }                                                                                                      \
   } while (0)
 
 // Device-side routing state for one forward call. All arrays live in the context workspace.

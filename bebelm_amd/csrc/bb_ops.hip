@@ -233,46 +233,66 @@ struct Row {
   }
 };
 
-// A score row of n floats into LDS by one wave: whole chunks of 64 by LDS DMA, all issued before
-// the one wait (a plain load-then-store loop waited for every load in turn: at 16K positions,
-// 256 round trips a row), the partial last chunk by plain loads.
+// A score row of n floats into LDS by the block's NW waves: whole chunks of 64 by LDS DMA (wave w
+// takes chunks w, w + NW, ...), all issued before the one wait (a plain load-then-store loop
+// waited for every load in turn: at 16K positions, 256 round trips a row), the partial last
+// chunk by plain loads. The caller's barrier publishes the row.
+template <int NW = 1>
 __device__ __forceinline__ void row_to_lds(const float* src, float* lrow, int n) {
-  const int lane = threadIdx.x & 63, nfull = n / 64;
-  for (int c = 0; c < nfull; ++c) __builtin_amdgcn_global_load_lds(src + 64 * c + lane, lrow + 64 * c, 4, 0, 0);
-  if (64 * nfull + lane < n) lrow[64 * nfull + lane] = src[64 * nfull + lane];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nfull = n / 64;
+  for (int c = w; c < nfull; c += NW) __builtin_amdgcn_global_load_lds(src + 64 * c + lane, lrow + 64 * c, 4, 0, 0);
+  if (w == 0 && 64 * nfull + lane < n) lrow[64 * nfull + lane] = src[64 * nfull + lane];
   __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0): the copies landed
 }
 
-// softmax.rs:9-22 on row r[0..n) by one wave (exps written back, then scaled).
-template <bool LDS>
-__device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, float* s_inv) {
-  const int lane = threadIdx.x;
+// softmax.rs:9-22 on row r[0..n) by the block's NW waves (exps written back, then scaled).
+template <bool LDS, int NW = 1>
+__device__ void row_softmax(const Row<LDS> r, int n, const uint64_t* exptab, float* s_inv) {
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   float m = -__builtin_inff();
 #pragma unroll 8
-  for (int j = lane; j < n; j += 64) m = fmaxf(m, r.ld(j));
+  for (int j = tid; j < n; j += NT) m = fmaxf(m, r.ld(j));
   m = wave_max(m);
+  if constexpr (NW > 1) {
+    __shared__ float wmax[NW];
+    if (lane == 0) wmax[w] = m;
+    __syncthreads();
+    m = wmax[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) m = fmaxf(m, wmax[i]);
+  }
 #pragma unroll 4
-  for (int j = lane; j < n; j += 64) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
+  for (int j = tid; j < n; j += NT) r.st(j, bb_expf_tab(r.ld(j) - m, exptab));
   __syncthreads();
   // The reference's sum is one left-to-right chain of f64 adds (softmax.rs:14-17), but only
   // inv = (float)(1 / sum) leaves it. Every summand is >= 0, so the chain's sum S_c and this
-  // wave's tree sum S_t (each lane's elements in order, then a butterfly) are both within
-  // (n + 5 + n/64)·u·S of the exact sum S (u = 2^-53, recursive summation bounds), and so
-  // within B = (n + 64)·2^-51·S_t of each other with room to spare for the rounding of B and of
-  // the interval's ends. (float)(1 / x) never increases as x grows: when the ends S_t − B and
-  // S_t + B give the same float, S_c gives it too. Otherwise (about one row in 10^4 at 16K
-  // positions, and rows holding NaN or infinities) lane 0 runs the chain itself.
-  // (IEEE addition commutes, so both lanes of every butterfly pair form the same sum and all 64
-  // lanes end with the same S_t.)
+  // block's tree sum S_t (each thread's elements in order, a butterfly over the wave, then the
+  // waves' sums in order) are both within (n + n/64 + 6 + NW)·u·S of the exact sum S (u = 2^-53,
+  // recursive summation bounds), and so within B = (n + 64)·2^-51·S_t of each other with room to
+  // spare for the rounding of B and of the interval's ends. (float)(1 / x) never increases as x
+  // grows: when the ends S_t − B and S_t + B give the same float, S_c gives it too. Otherwise
+  // (about one row in 10^4 at 16K positions, and rows holding NaN or infinities) thread 0 runs
+  // the chain itself.
+  // (IEEE addition commutes, so both lanes of every butterfly pair form the same sum, all 64
+  // lanes end with the same value, and every thread adds the waves' sums in the same order.)
   double st = 0.0;
-  for (int j = lane; j < n; j += 64) st += (double)r.ld(j);
+  for (int j = tid; j < n; j += NT) st += (double)r.ld(j);
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) st += __shfl_xor(st, o);
+  if constexpr (NW > 1) {
+    __shared__ double wsum[NW];
+    if (lane == 0) wsum[w] = st;
+    __syncthreads();
+    st = wsum[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) st += wsum[i];
+  }
   const double bnd = (double)(n + 64) * 0x1p-51 * st;
   const float f_lo = (float)(1.0 / (st - bnd)), f_hi = (float)(1.0 / (st + bnd));
   if (f_lo == f_hi) {
-    if (lane == 0) *s_inv = f_lo;
-  } else if (lane == 0) {
+    if (tid == 0) *s_inv = f_lo;
+  } else if (tid == 0) {
     // left to right; the next 16 values are read while the adds of the current 16 run (the adds
     // are one dependent chain, the reads are not)
     constexpr int U = 16;
@@ -302,7 +322,7 @@ __device__ void wave_softmax(const Row<LDS> r, int n, const uint64_t* exptab, fl
   __syncthreads();
   const float inv = *s_inv;
 #pragma unroll 8
-  for (int j = lane; j < n; j += 64) r.st(j, r.ld(j) * inv);
+  for (int j = tid; j < n; j += NT) r.st(j, r.ld(j) * inv);
   __syncthreads();
 }
 
@@ -322,7 +342,7 @@ __global__ void __launch_bounds__(64) k_attn_softmax_pv(float* sc, const float* 
     row_to_lds(s, lrow, n);
   __syncthreads();
   const Row<LDS> r{LDS ? lrow : s};
-  wave_softmax<LDS>(r, n, exptab, &s_inv);
+  row_softmax<LDS>(r, n, exptab, &s_inv);
   const int kv = h / (n_heads / n_kv);
   const size_t vs = (size_t)n_kv * hd;  // between consecutive positions of one value column
   for (int d = lane; d < hd; d += 64) {
@@ -433,22 +453,24 @@ __global__ void __launch_bounds__(256) k_attn_scores_tile(const float* __restric
   }
 }
 
-// softmax.rs:9-22 of every score row (t, h), each of its own length n0 + t + 1, in place.
+// softmax.rs:9-22 of every score row (t, h), each of its own length n0 + t + 1, in place, by
+// SM_WAVES waves per row.
+constexpr int SM_WAVES = 8;
 template <bool LDS>
-__global__ void __launch_bounds__(64) k_attn_softmax(float* sc, int n0, int n_heads, int ld) {
+__global__ void __launch_bounds__(64 * SM_WAVES) k_attn_softmax(float* sc, int n0, int n_heads, int ld) {
   extern __shared__ float lrow[];
   __shared__ uint64_t exptab[32];
   __shared__ float s_inv;
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  if (lane < 32) exptab[lane] = exp_table_entry();
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  if (tid < 32) exptab[tid] = exp_table_entry();
   const int n = n0 + t + 1;
   float* s = sc + ((size_t)t * n_heads + h) * ld;
   if constexpr (LDS)
-    row_to_lds(s, lrow, n);
+    row_to_lds<SM_WAVES>(s, lrow, n);
   __syncthreads();
-  wave_softmax<LDS>(Row<LDS>{LDS ? lrow : s}, n, exptab, &s_inv);
+  row_softmax<LDS, SM_WAVES>(Row<LDS>{LDS ? lrow : s}, n, exptab, &s_inv);
   if constexpr (LDS)
-    for (int j = lane; j < n; j += 64) s[j] = lrow[j];
+    for (int j = tid; j < n; j += 64 * SM_WAVES) s[j] = lrow[j];
 }
 
 // out[t][h][d] = Σ_j p[t][h][j]·v[j][g][d] for the block's items, position order from 0.0. Per
@@ -509,18 +531,23 @@ __global__ void __launch_bounds__(256) k_attn_pv_tile(const float* __restrict__ 
 }
 
 // P·V of a few tokens over long rows (after k_attn_softmax): out[t][h][d] = Σ_j p[t][h][j]·v[j][g][d]
-// in position order from 0.0 (attention.rs:46-54), the sums of k_attn_softmax_pv. The chains are
-// serial, so what bounds a long row is feeding them: one wave per head keeps too few value loads
-// in flight. Here block (kv head g, dim slice q, token t) is one wave whose lane (hh, d) is head
-// hh of the group and dim d of the slice (G heads x 64/G dims), so the slice's values of a
-// position (64/G floats, shared by the G heads) and the group's probabilities are fetched once,
-// by LDS DMA into a ring of PVL_R chunks of 64 positions, R-1 chunks ahead of the sums.
+// in position order from 0.0 (attention.rs:46-54), the sums of k_attn_softmax_pv. Each
+// (head, dim) is one serial chain of adds, so what bounds a long row is feeding the chains. Block
+// (kv head g, dim slice q, token t) is one wave whose lane (hh, d) is head hh of the group and
+// dim d of the slice (G heads x 64/G dims), so the slice's values of a position (64/G floats,
+// shared by the G heads) and the group's probabilities are fetched once: by LDS DMA through
+// buffer resources (positions past the row read zero and are never summed) into a ring of R
+// chunks of 64 positions, R-1 chunks ahead of the sums. A chunk's 16-byte reads of the probabilities and 4-byte reads of the values
+// all go out before its chain of adds, which then waits for the LDS latency once a chunk.
+// (Values held dim-major, so a lane read four positions at once, took 4-byte copies: 16 per chunk
+// for a 16-dim slice, which left room for only three chunks in flight, 180 against 140 µs at
+// 16,384 positions.)
 constexpr int PVL_CH = 64;
 template <int G>
 struct PvlCfg {
-  static constexpr int DS = 64 / G;                       // dims of a slice
-  static constexpr int NV = DS / 4;                       // 16-byte copies of a chunk's values (1 KB each)
-  static constexpr int NI = NV + G;                       // copies per chunk (G x 256-byte probability rows)
+  static constexpr int DS = 64 / G;                            // dims of a slice
+  static constexpr int NV = DS / 4;                            // 16-byte copies of a chunk's values (1 KB each)
+  static constexpr int NI = NV + G;                            // copies per chunk (G probability rows)
   static constexpr int R = 63 / NI + 1 < 8 ? 63 / NI + 1 : 8;  // ring slots ((R-1)·NI fits vmcnt)
 };
 
@@ -549,30 +576,75 @@ __global__ void __launch_bounds__(64) k_attn_pv_long(const float* __restrict__ p
   const int hh = lane / DS, dl = lane % DS;
   const int n = n0 + t + 1;
   const int nch = (n + PVL_CH - 1) / PVL_CH;
-  const float* prow = p + ((size_t)t * n_heads + (size_t)g * G) * ld;
-  // chunk c into slot S: value copy k of lane l = bytes 1024k + 16l of the chunk's [64][DS]
-  // floats (position (1024k + 16l) / (4 DS)); probability copy k = head k's 64 values. Positions
-  // past the row repeat its last one (read, never summed).
+  // values: the n rows of the cache; probabilities: the group's G rows of this token
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc, (uint32_t)n * (uint32_t)n_kv * 256u);
+  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p + ((size_t)t * n_heads + (size_t)g * G) * ld, (uint32_t)(G * ld) * 4u);
+  // value copy k of lane l = bytes 1024k + 16l of the chunk's [64][DS] floats: position
+  // (1024k + 16l) / (4 DS) of the chunk, byte (1024k + 16l) % (4 DS) of its slice
+  uint32_t vo[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int byte = 1024 * k + 16 * lane, r = byte / (4 * DS), off = byte % (4 * DS);
+    vo[k] = (uint32_t)((r * n_kv + g) * 256 + q * DS * 4 + off);
+  }
+  const uint32_t chunk_v = (uint32_t)PVL_CH * (uint32_t)n_kv * 256u;  // bytes of 64 cache rows
+  // (the chunk's advance goes into the per-lane offset: the buffer's range check, which turns the
+  // reads past the row into zeros, covers that offset and not the wave-uniform one)
   auto issue = [&](auto S, int c) {
     float* slot = pvl_slot<G, decltype(S)::value>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's earlier reads are done
+    const uint32_t cv = (uint32_t)c * chunk_v, cp = 4u * (uint32_t)(c * PVL_CH + lane);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int byte = 1024 * k + 16 * lane, r = byte / (4 * DS), off = byte % (4 * DS);
-      const int j = min(c * PVL_CH + r, n - 1);
-      const uint8_t* src = reinterpret_cast<const uint8_t*>(vc + ((size_t)j * n_kv + g) * 64 + q * DS) + off;
-      __builtin_amdgcn_global_load_lds(src, reinterpret_cast<uint8_t*>(slot) + 1024 * k, 16, 0, 0);
-    }
-    const int j = min(c * PVL_CH + lane, n - 1);
+    for (int k = 0; k < NV; ++k) buf_dma16(rv, vo[k] + cv, 0, reinterpret_cast<uint8_t*>(slot) + 1024 * k);
 #pragma unroll
     for (int k = 0; k < G; ++k)
-      __builtin_amdgcn_global_load_lds(prow + (size_t)k * ld + j, slot + PVL_CH * DS + k * PVL_CH, 4, 0, 0);
+      buf_dma4(rp, cp + (uint32_t)(k * ld) * 4u, 0, reinterpret_cast<uint8_t*>(slot + PVL_CH * DS + k * PVL_CH));
+  };
+  float o = 0.0f;
+  // the sums of the chunk in slot u over its jn positions
+  auto sum_chunk = [&](auto U, int jn) {
+    const float* slot = pvl_slot<G, decltype(U)::value>();
+    const float* sps = slot + PVL_CH * DS + hh * PVL_CH;
+    const float* svs = slot + dl;
+    if (jn == PVL_CH) {
+      float4 pw[PVL_CH / 4];
+      float vv[PVL_CH];
+#pragma unroll
+      for (int k = 0; k < PVL_CH / 4; ++k) {
+        pw[k] = *reinterpret_cast<const float4*>(sps + 4 * k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vv[4 * k + i] = svs[(4 * k + i) * DS];
+      }
+#pragma unroll
+      for (int k = 0; k < PVL_CH / 4; ++k) {
+        o += pw[k].x * vv[4 * k];
+        o += pw[k].y * vv[4 * k + 1];
+        o += pw[k].z * vv[4 * k + 2];
+        o += pw[k].w * vv[4 * k + 3];
+      }
+    } else {
+      for (int jj = 0; jj < jn; ++jj) o += sps[jj] * svs[jj * DS];
+    }
   };
   unroll_seq([&](auto S) { if (decltype(S)::value < nch) issue(S, decltype(S)::value); },
              std::make_integer_sequence<int, R - 1>{});
-  float o = 0.0f;
-  // chunk c0 + u sits in slot u (c0 a multiple of R): every read names its slot at compile time
-  for (int c0 = 0; c0 < nch; c0 += R) {
+  constexpr int WL = (R - 1) * NI;  // copies of the R-1 chunks after the current one
+  // chunk c0 + u sits in slot u (c0 a multiple of R): every read names its slot at compile time.
+  // The steady state (every chunk of the round full, with a chunk R-1 ahead to request) is kept
+  // apart from the last rounds, whose path waits for all copies: where both paths met, the
+  // compiler waited for all copies before the first slot's reads in every round.
+  int c0 = 0;
+  for (; c0 + 2 * R - 2 < nch; c0 += R) {
+    unroll_seq(
+        [&](auto U) {
+          constexpr int u = decltype(U)::value;
+          issue(std::integral_constant<int, (u + R - 1) % R>{}, c0 + u + R - 1);
+          __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
+          sum_chunk(U, PVL_CH);
+        },
+        std::make_integer_sequence<int, R>{});
+  }
+  for (; c0 < nch; c0 += R) {
     unroll_seq(
         [&](auto U) {
           constexpr int u = decltype(U)::value;
@@ -580,21 +652,11 @@ __global__ void __launch_bounds__(64) k_attn_pv_long(const float* __restrict__ p
           if (c >= nch) return;
           if (c + R - 1 < nch) {
             issue(std::integral_constant<int, (u + R - 1) % R>{}, c + R - 1);
-            constexpr int WL = (R - 1) * NI;  // copies of the chunks after c still in flight
             __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
           } else {
             __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
           }
-          const float* slot = pvl_slot<G, u>();
-          const float* svs = slot + dl;
-          const float* sps = slot + PVL_CH * DS + hh * PVL_CH;
-          const int jn = min(PVL_CH, n - c * PVL_CH);
-          if (jn == PVL_CH) {
-#pragma unroll
-            for (int jj = 0; jj < PVL_CH; ++jj) o += sps[jj] * svs[jj * DS];
-          } else {
-            for (int jj = 0; jj < jn; ++jj) o += sps[jj] * svs[jj * DS];
-          }
+          sum_chunk(U, min(PVL_CH, n - c * PVL_CH));
         },
         std::make_integer_sequence<int, R>{});
   }
@@ -625,9 +687,9 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
   if (T >= AT_PV_MIN_T && hd == AT_HD && n_heads / n_kv <= AT_PV_ITEMS) {
     // a batch: every row's softmax, then P·V in tiles of (tokens x heads of one kv head)
     if (ld <= OPS_ROW_LDS)
-      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, n0, n_heads, ld);
+      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64 * SM_WAVES), (size_t)ld * 4, s, scores, n0, n_heads, ld);
     else
-      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64), 0, s, scores, n0, n_heads, ld);
+      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64 * SM_WAVES), 0, s, scores, n0, n_heads, ld);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int TT = at_tokens(n_heads / n_kv, AT_PV_ITEMS);
@@ -639,9 +701,9 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
   if (hd == AT_HD && ld >= PVL_MIN_LD && (G == 1 || G == 2 || G == 4 || G == 8 || G == 16)) {
     // long rows: the softmax, then P·V with the values streamed through LDS (k_attn_pv_long)
     if (ld <= OPS_ROW_LDS)
-      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64), (size_t)ld * 4, s, scores, n0, n_heads, ld);
+      BB_LAUNCH(k_attn_softmax<true>, dim3(n_heads, T), dim3(64 * SM_WAVES), (size_t)ld * 4, s, scores, n0, n_heads, ld);
     else
-      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64), 0, s, scores, n0, n_heads, ld);
+      BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64 * SM_WAVES), 0, s, scores, n0, n_heads, ld);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid(n_kv, G, T);
@@ -662,27 +724,28 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
   return hipGetLastError();
 }
 
-// softmax of n_vec rows of n (kernels/softmax.rs:9-22), one wave per row (through LDS when the
-// row fits).
+// softmax of n_vec rows of n (kernels/softmax.rs:9-22), SM_WAVES waves per row (through LDS when
+// the row fits).
 template <bool LDS>
-__global__ void __launch_bounds__(64) k_softmax(float* x, int n) {
+__global__ void __launch_bounds__(64 * SM_WAVES) k_softmax(float* x, int n) {
   extern __shared__ float lrow[];
   __shared__ uint64_t exptab[32];
   __shared__ float s_inv;
   if (threadIdx.x < 32) exptab[threadIdx.x] = exp_table_entry();
   float* g = x + (size_t)blockIdx.x * n;
   if constexpr (LDS)
-    row_to_lds(g, lrow, n);
+    row_to_lds<SM_WAVES>(g, lrow, n);
   __syncthreads();
-  wave_softmax<LDS>(Row<LDS>{LDS ? lrow : g}, n, exptab, &s_inv);
+  row_softmax<LDS, SM_WAVES>(Row<LDS>{LDS ? lrow : g}, n, exptab, &s_inv);
   if constexpr (LDS)
-    for (int j = threadIdx.x; j < n; j += 64) g[j] = lrow[j];
+    for (int j = threadIdx.x; j < n; j += 64 * SM_WAVES) g[j] = lrow[j];
 }
 
 hipError_t launch_softmax(hipStream_t s, float* x, size_t n, size_t n_vec) {
   if (n == 0 || n_vec == 0) return hipSuccess;
-  if (n <= (size_t)OPS_ROW_LDS) BB_LAUNCH(k_softmax<true>, dim3((unsigned)n_vec), dim3(64), n * 4, s, x, (int)n);
-  else BB_LAUNCH(k_softmax<false>, dim3((unsigned)n_vec), dim3(64), 0, s, x, (int)n);
+  const dim3 block(64 * SM_WAVES);
+  if (n <= (size_t)OPS_ROW_LDS) BB_LAUNCH(k_softmax<true>, dim3((unsigned)n_vec), block, n * 4, s, x, (int)n);
+  else BB_LAUNCH(k_softmax<false>, dim3((unsigned)n_vec), block, 0, s, x, (int)n);
   return hipGetLastError();
 }
 
