@@ -889,7 +889,7 @@ void attn_forward_dev(bb_ctx* c, bb_attn_op* op, bb_kv_cache* kv, size_t pos0, c
     Carve cv{base};
     bb::Q8Bufs xq = carve_q8(cv, T, H);
     float* q = cv.take<float>(T * QD);
-    float* scores = cv.take<float>(T * NH * (n0 + T));
+    float* scores = cv.take<float>(T * NH * (n0 + T) + 4);  // (+ slack: launch_attn_pv reads one float past the rows)
     float* attn = cv.take<float>(T * QD);
     bb::Q8Bufs aq = carve_q8(cv, T, QD);
     int32_t* grp = cv.take<int32_t>(T + 8);
@@ -1624,7 +1624,8 @@ int bb_attention_decode(bb_ctx* c, const float* q, const float* k, const float* 
     const float scale = 1.0f / std::sqrt(float(head_dim));
     with_io(c, loc, {{q, QD * 4, true, false}, {k, KVB, true, false}, {v, KVB, true, false}, {out, QD * 4, false, true}},
             [&](std::vector<void*>& d) {
-              float* scores = reinterpret_cast<float*>(ensure_ws(c, n_heads * n_ctx * 4));
+              // (a float of slack after the rows: launch_attn_pv reads up to one past a row's end)
+              float* scores = reinterpret_cast<float*>(ensure_ws(c, n_heads * n_ctx * 4 + 16));
               const int n0 = (int)n_ctx - 1;
               launch(c, bb::K_ATTN_SCORES, [&] {
                 return bb::launch_attn_scores(c->stream, static_cast<const float*>(d[0]),

@@ -274,7 +274,8 @@ hipError_t launch_norm_rope(hipStream_t s, float* buf, int T, int n_heads, int h
 // scores [T][n_heads][n0+T]: token t's query against cached positions j < n0 + t + 1.
 hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
                               int hd, float scale, float* scores);
-// softmax of each score row (in place), then out [T][n_heads][hd] = Σ_j w_j·v_j.
+// softmax of each score row (in place), then out [T][n_heads][hd] = Σ_j w_j·v_j. scores needs one
+// float of slack after its last row (the long-row P·V reads a row's last position 8 bytes at a time).
 hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0, int T, int n_heads, int n_kv, int hd,
                           float* out);
 hipError_t launch_softmax(hipStream_t s, float* x, size_t n, size_t n_vec);

@@ -532,34 +532,42 @@ __global__ void __launch_bounds__(256) k_attn_pv_tile(const float* __restrict__ 
 
 // P·V of a few tokens over long rows (after k_attn_softmax): out[t][h][d] = Σ_j p[t][h][j]·v[j][g][d]
 // in position order from 0.0 (attention.rs:46-54), the sums of k_attn_softmax_pv. Each
-// (head, dim) is one serial chain of adds, so what bounds a long row is feeding the chains. Block
-// (kv head g, dim slice q, token t) is one wave whose lane (hh, d) is head hh of the group and
-// dim d of the slice (G heads x 64/G dims), so the slice's values of a position (64/G floats,
-// shared by the G heads) and the group's probabilities are fetched once: by LDS DMA through
-// buffer resources (positions past the row read zero and are never summed) into a ring of R
-// chunks of 64 positions, R-1 chunks ahead of the sums. A chunk's 16-byte reads of the probabilities and 4-byte reads of the values
-// all go out before its chain of adds, which then waits for the LDS latency once a chunk.
-// (Values held dim-major, so a lane read four positions at once, took 4-byte copies: 16 per chunk
-// for a 16-dim slice, which left room for only three chunks in flight, 180 against 140 µs at
-// 16,384 positions.)
-constexpr int PVL_CH = 64;
+// (head, dim) is one serial chain of adds, and a decode step has few of them (64 per head), so
+// what bounds a long row is how fast one wave can issue its chain: a wave issues one instruction
+// every four cycles, and a wave that also multiplied and read its operands spent about three of
+// them a position. Block (kv head g, dim slice q, token t) is three waves: wave 0 holds the 64
+// chains (lane L = head hh of the group x dim d of the slice, G heads x 64/G dims) and only adds;
+// waves 1 and 2 read the slice's values and the group's probabilities straight into registers
+// through buffer resources (positions past the row read zero), D chunks ahead, and write the
+// products of each chunk of 64 positions to a ring of PVL_NB chunks in LDS, one row of products per
+// chain. The chain wave reads a row 16 bytes (four positions) at a time, so a position costs it
+// one add and a quarter of a read. A block barrier a chunk hands the chunks over: in step k the
+// producers write chunk k and the chain wave sums chunk k-2 (reading ahead into chunk k-1). A
+// product past the row is p·v with p set to 0 and v read as 0, +0.0, and adding +0.0 leaves a
+// chain that starts at +0.0 unchanged, so every chunk is summed whole.
+constexpr int PVL_CH = 64;              // positions a chunk
+constexpr int PVL_ROW = PVL_CH + 4;     // floats a chain's row of products (the pad spreads rows over the banks)
+constexpr int PVL_NB = 3;               // chunks of products in the LDS ring
+constexpr int PVL_BUF = 64 * PVL_ROW;   // floats a chunk of products
 template <int G>
 struct PvlCfg {
-  static constexpr int DS = 64 / G;                            // dims of a slice
-  static constexpr int NV = DS / 4;                            // 16-byte copies of a chunk's values (1 KB each)
-  static constexpr int NI = NV + G;                            // copies per chunk (G probability rows)
-  static constexpr int R = 63 / NI + 1 < 8 ? 63 / NI + 1 : 8;  // ring slots ((R-1)·NI fits vmcnt)
+  static constexpr int DS = 64 / G;                  // dims of a slice
+  static constexpr int PC = DS / 4;                  // 16-byte pieces of a position's slice
+  static constexpr int PCL = PC < 4 ? PC : 4;        // pieces side by side in a load ...
+  static constexpr int PPL = 64 / PCL;               // ... over this many positions (lane = position x piece)
+  static constexpr bool SPLIT_HEADS = PCL == 1;      // a load covers the chunk: the producers split the heads
+  static constexpr int HP = SPLIT_HEADS ? G / 2 : G; // heads of a producer
+  static constexpr int NK = SPLIT_HEADS ? 1 : PCL / 2;  // adjacent positions of a lane (a producer: NK·PPL)
+  static constexpr int NQG = PC / PCL;               // piece groups (of PCL)
+  static constexpr int NL = NK * NQG;                // 16-byte value loads of a lane a chunk
+  static constexpr int HPL = (HP + PCL - 1) / PCL;   // probabilities a lane loads a position (the PCL
+                                                     // lanes of a position share theirs)
+  static constexpr int NV = NL * 4 + NK * HPL;       // registers of a chunk's loads
+  static constexpr int NLD = NL + HPL;               // loads a chunk (a lane's NK probabilities in one)
+  static constexpr int D0 = 176 / NV < 63 / NLD ? 176 / NV : 63 / NLD;
+  static constexpr int D = D0 < 12 ? D0 : 12;        // chunks of loads in flight (NLD·D fits vmcnt)
+  static_assert(NL * 4 * HP == 32, "a producer lane makes 32 products a chunk");
 };
-
-// Ring slot I of k_attn_pv_long<G>: a chunk's values [64][DS] then its probabilities [G][64].
-// Every slot is an LDS object of its own (a function-local array per instantiation), so the
-// compiler knows which copies in flight a read of one slot can be behind; with one array indexed
-// by slot it waited for every copy before every read.
-template <int G, int I>
-__device__ __forceinline__ float* pvl_slot() {
-  __shared__ __align__(16) float a[PVL_CH * PvlCfg<G>::DS + G * PVL_CH];
-  return a;
-}
 
 template <class F, int... I>
 __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I...>) {
@@ -567,100 +575,194 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
 }
 
 template <int G>
-__global__ void __launch_bounds__(64) k_attn_pv_long(const float* __restrict__ p, const float* __restrict__ vc,
-                                                    int n0, int n_heads, int n_kv, int ld, float* __restrict__ out) {
+__global__ void __launch_bounds__(192) k_attn_pv_long(const float* __restrict__ p, const float* __restrict__ vc,
+                                                     int n0, int n_heads, int n_kv, int ld, float* __restrict__ out) {
   using C = PvlCfg<G>;
-  constexpr int DS = C::DS, R = C::R, NV = C::NV, NI = C::NI;
-  static_assert(DS >= 4 && DS % 4 == 0, "slices of at least 4 dims");
-  const int g = blockIdx.x, q = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
-  const int hh = lane / DS, dl = lane % DS;
+  constexpr int DS = C::DS, PCL = C::PCL, PPL = C::PPL, HP = C::HP, NK = C::NK, NQG = C::NQG, NL = C::NL, D = C::D;
+  __shared__ __align__(16) float prod[PVL_NB * PVL_BUF];
+  const int g = blockIdx.x, q = blockIdx.y, t = blockIdx.z;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), lane = threadIdx.x % 64;
   const int n = n0 + t + 1;
   const int nch = (n + PVL_CH - 1) / PVL_CH;
-  // values: the n rows of the cache; probabilities: the group's G rows of this token
-  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc, (uint32_t)n * (uint32_t)n_kv * 256u);
-  const __amdgpu_buffer_rsrc_t rp = buf_rsrc(p + ((size_t)t * n_heads + (size_t)g * G) * ld, (uint32_t)(G * ld) * 4u);
-  // value copy k of lane l = bytes 1024k + 16l of the chunk's [64][DS] floats: position
-  // (1024k + 16l) / (4 DS) of the chunk, byte (1024k + 16l) % (4 DS) of its slice
-  uint32_t vo[NV];
+  const int nsteps = nch + 2;  // step k: chunk k made, chunk k-2 summed; a barrier after all but the last
+
+  if (w == 0) {
+    // the chains: lane L reads row L of each chunk, four positions a read
+    float o = 0.0f;
+    struct Half {
+      float4 v[8];
+    };
+    auto read_half = [&](const float* r, int h, Half& x) {
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int byte = 1024 * k + 16 * lane, r = byte / (4 * DS), off = byte % (4 * DS);
-    vo[k] = (uint32_t)((r * n_kv + g) * 256 + q * DS * 4 + off);
+      for (int m = 0; m < 8; ++m) x.v[m] = *reinterpret_cast<const float4*>(r + 32 * h + 4 * m);
+    };
+    auto add_half = [&](const Half& x) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        o += x.v[m].x;
+        o += x.v[m].y;
+        o += x.v[m].z;
+        o += x.v[m].w;
+      }
+    };
+    // (the chain wave loads nothing from memory; the wait tells the compiler so, which otherwise
+    // waits in the loop for the producers' loads on a path it cannot rule out)
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    asm volatile("" ::"s"(out));          // (the argument's load done before the loop, not in flight in it)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const float* const row = prod + lane * PVL_ROW;
+    int b = 0;  // ring slot of chunk s
+    Half x0, x1;
+    // each half's reads go out before the adds of the half before (the scheduling barriers keep
+    // the compiler from moving the next half's reads above the adds, which cost copies of x0)
+    read_half(row, 0, x0);
+    // one wait a half for its eight reads, issued a half of adds earlier, with the next half's
+    // eight still in flight
+    constexpr int LGKM8 = 0xc87f;  // lgkmcnt(8)
+    for (int s = 0; s < nch - 1; ++s) {
+      const int bn = b == PVL_NB - 1 ? 0 : b + 1;
+      read_half(row + b * PVL_BUF, 1, x1);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(LGKM8);
+      __builtin_amdgcn_sched_barrier(0);
+      add_half(x0);
+      __builtin_amdgcn_sched_barrier(0);
+      read_half(row + bn * PVL_BUF, 0, x0);  // chunk s+1
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(LGKM8);
+      __builtin_amdgcn_sched_barrier(0);
+      add_half(x1);
+      // no wait for the reads in flight: they are of a chunk the producers overwrite only after the
+      // barrier after next
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      b = bn;
+    }
+    read_half(row + b * PVL_BUF, 1, x1);
+    add_half(x0);
+    add_half(x1);
+    const int hh = lane / DS, dl = lane % DS;
+    out[((size_t)t * n_heads + (size_t)g * G + hh) * 64 + q * DS + dl] = o;
+    return;
   }
-  const uint32_t chunk_v = (uint32_t)PVL_CH * (uint32_t)n_kv * 256u;  // bytes of 64 cache rows
-  // (the chunk's advance goes into the per-lane offset: the buffer's range check, which turns the
-  // reads past the row into zeros, covers that offset and not the wave-uniform one)
-  auto issue = [&](auto S, int c) {
-    float* slot = pvl_slot<G, decltype(S)::value>();
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the slot's earlier reads are done
-    const uint32_t cv = (uint32_t)c * chunk_v, cp = 4u * (uint32_t)(c * PVL_CH + lane);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) buf_dma16(rv, vo[k] + cv, 0, reinterpret_cast<uint8_t*>(slot) + 1024 * k);
-#pragma unroll
-    for (int k = 0; k < G; ++k)
-      buf_dma4(rp, cp + (uint32_t)(k * ld) * 4u, 0, reinterpret_cast<uint8_t*>(slot + PVL_CH * DS + k * PVL_CH));
+
+  // producers: lane = (position lp of PPL, piece lc of PCL); producer pw takes positions
+  // [pw·NK·PPL, (pw+1)·NK·PPL) of a chunk (heads split instead when a load covers the chunk), a
+  // lane the NK adjacent positions pos0 + NK·lp + k
+  const int pw = w - 1;
+  const int lp = lane / PCL, lc = lane % PCL;
+  const int h0 = C::SPLIT_HEADS ? pw * HP : 0;
+  const int pos0 = (C::SPLIT_HEADS ? 0 : pw * NK * PPL) + NK * lp;
+  const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc, (uint32_t)n * (uint32_t)n_kv * 256u);
+  // (one float past the group's rows in range: a lane's two positions load as one 8-byte read, which
+  // at a row's last position takes the float after it; the caller leaves that float in its buffer)
+  const __amdgpu_buffer_rsrc_t rp =
+      buf_rsrc(p + ((size_t)t * n_heads + (size_t)g * G) * ld, (uint32_t)(G * ld + 1) * 4u);
+  const uint32_t row_b = (uint32_t)n_kv * 256u;  // bytes of a cache row
+  const uint32_t v_lane = (uint32_t)pos0 * row_b + (uint32_t)g * 256u + (uint32_t)(q * DS + lc * 4) * 4u;
+  const uint32_t p_lane = (uint32_t)(h0 * ld + pos0) * 4u;
+  const uint32_t chunk_v = (uint32_t)PVL_CH * row_b;
+  constexpr int HPL = C::HPL;
+  struct Set {
+    float4 v[NL];
+    float p[HPL][NK];  // head (j·PCL + lc) mod HP of the lane's positions
   };
-  float o = 0.0f;
-  // the sums of the chunk in slot u over its jn positions
-  auto sum_chunk = [&](auto U, int jn) {
-    const float* slot = pvl_slot<G, decltype(U)::value>();
-    const float* sps = slot + PVL_CH * DS + hh * PVL_CH;
-    const float* svs = slot + dl;
-    if (jn == PVL_CH) {
-      float4 pw[PVL_CH / 4];
-      float vv[PVL_CH];
+  auto load = [&](Set& x, int c) {
+    const uint32_t cv = (uint32_t)c * chunk_v, cp = (uint32_t)c * (PVL_CH * 4u);
 #pragma unroll
-      for (int k = 0; k < PVL_CH / 4; ++k) {
-        pw[k] = *reinterpret_cast<const float4*>(sps + 4 * k);
+    for (int k = 0; k < NK; ++k)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vv[4 * k + i] = svs[(4 * k + i) * DS];
+      for (int m = 0; m < NQG; ++m)
+        x.v[k * NQG + m] =
+            __builtin_bit_cast(float4, buf_load16(rv, v_lane + cv + (uint32_t)k * row_b + (uint32_t)(m * PCL * 16), 0));
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+      const uint32_t off = p_lane + cp + (uint32_t)(((j * PCL + lc) % HP) * ld) * 4u;
+      if constexpr (NK == 2) {
+        const float2 v2 = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rp, (int)off, 0, 0));
+        x.p[j][0] = v2.x;
+        x.p[j][1] = v2.y;
+      } else {
+        x.p[j][0] = buf_load4f(rp, off, 0);
       }
-#pragma unroll
-      for (int k = 0; k < PVL_CH / 4; ++k) {
-        o += pw[k].x * vv[4 * k];
-        o += pw[k].y * vv[4 * k + 1];
-        o += pw[k].z * vv[4 * k + 2];
-        o += pw[k].w * vv[4 * k + 3];
-      }
-    } else {
-      for (int jj = 0; jj < jn; ++jj) o += sps[jj] * svs[jj * DS];
     }
   };
-  unroll_seq([&](auto S) { if (decltype(S)::value < nch) issue(S, decltype(S)::value); },
-             std::make_integer_sequence<int, R - 1>{});
-  constexpr int WL = (R - 1) * NI;  // copies of the R-1 chunks after the current one
-  // chunk c0 + u sits in slot u (c0 a multiple of R): every read names its slot at compile time.
-  // The steady state (every chunk of the round full, with a chunk R-1 ahead to request) is kept
-  // apart from the last rounds, whose path waits for all copies: where both paths met, the
-  // compiler waited for all copies before the first slot's reads in every round.
-  int c0 = 0;
-  for (; c0 + 2 * R - 2 < nch; c0 += R) {
+  // probability of head H at the lane's position k: from the lane of its position that loaded it
+  auto prob = [&](const Set& x, auto H, int k) -> float {
+    constexpr int h = decltype(H)::value;
+    const float v = x.p[h / PCL][k];
+    if constexpr (PCL == 1) {
+      return v;
+    } else {
+      constexpr int s = h % PCL;  // quad lanes [s,s,s,s] (PCL 4) or [s,s,2+s,2+s] (PCL 2)
+      constexpr int ctrl = PCL == 4 ? s * 0x55 : (s | s << 2 | (2 + s) << 4 | (2 + s) << 6);
+      return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+    }
+  };
+  // product (k, m, i, h) goes to row (h0+h)·DS + (m·PCL + lc)·4 + i, column pos0 + k
+  float* const wbase = prod + (h0 * DS + lc * 4) * PVL_ROW + pos0;
+  auto make = [&](Set& x, int c) {
+    float* const dst = wbase + (c % PVL_NB) * PVL_BUF;
+    bool in[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) in[k] = c * PVL_CH + pos0 + k < n;
     unroll_seq(
-        [&](auto U) {
-          constexpr int u = decltype(U)::value;
-          issue(std::integral_constant<int, (u + R - 1) % R>{}, c0 + u + R - 1);
-          __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
-          sum_chunk(U, PVL_CH);
-        },
-        std::make_integer_sequence<int, R>{});
-  }
-  for (; c0 < nch; c0 += R) {
-    unroll_seq(
-        [&](auto U) {
-          constexpr int u = decltype(U)::value;
-          const int c = c0 + u;
-          if (c >= nch) return;
-          if (c + R - 1 < nch) {
-            issue(std::integral_constant<int, (u + R - 1) % R>{}, c + R - 1);
-            __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
-          } else {
-            __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+        [&](auto H) {
+          constexpr int h = decltype(H)::value;
+          float ph[NK];
+#pragma unroll
+          for (int k = 0; k < NK; ++k) {
+            const float pk = prob(x, H, k);  // (outside the select: the broadcast needs every lane)
+            ph[k] = in[k] ? pk : 0.0f;
           }
-          sum_chunk(U, min(PVL_CH, n - c * PVL_CH));
+#pragma unroll
+          for (int m = 0; m < NQG; ++m) {
+            float* d = dst + (h * DS + m * PCL * 4) * PVL_ROW;
+            if constexpr (NK == 2) {
+              const float4 v0 = x.v[m], v1 = x.v[NQG + m];
+              *reinterpret_cast<float2*>(d + 0 * PVL_ROW) = make_float2(ph[0] * v0.x, ph[1] * v1.x);
+              *reinterpret_cast<float2*>(d + 1 * PVL_ROW) = make_float2(ph[0] * v0.y, ph[1] * v1.y);
+              *reinterpret_cast<float2*>(d + 2 * PVL_ROW) = make_float2(ph[0] * v0.z, ph[1] * v1.z);
+              *reinterpret_cast<float2*>(d + 3 * PVL_ROW) = make_float2(ph[0] * v0.w, ph[1] * v1.w);
+            } else {
+              const float4 v0 = x.v[m];
+              d[0 * PVL_ROW] = ph[0] * v0.x;
+              d[1 * PVL_ROW] = ph[0] * v0.y;
+              d[2 * PVL_ROW] = ph[0] * v0.z;
+              d[3 * PVL_ROW] = ph[0] * v0.w;
+            }
+          }
         },
-        std::make_integer_sequence<int, R>{});
+        std::make_integer_sequence<int, HP>{});
+  };
+  // every step loads, also chunks past the row (through the buffers' range checks; never made):
+  // with a load skipped on some path the compiler could only wait for every load in flight
+  Set ring[D];
+  // (in ring order: the steady state's waits count on set u's loads being older than set u+1's)
+  // (the scheduling barriers keep each set's loads in ring order: empty asm statements do not
+  // order buffer loads)
+  unroll_seq(
+      [&](auto U) {
+        load(ring[decltype(U)::value], decltype(U)::value);
+        __builtin_amdgcn_sched_barrier(0);
+      },
+      std::make_integer_sequence<int, D>{});
+  for (int k0 = 0; k0 < nsteps - 1; k0 += D) {
+    unroll_seq(
+        [&](auto U) {
+          constexpr int u = decltype(U)::value;
+          const int k = k0 + u;
+          if (k < nch) make(ring[u], k);
+          __builtin_amdgcn_sched_barrier(0);
+          load(ring[u], k + D);
+          __builtin_amdgcn_sched_barrier(0);
+          if (k < nsteps - 1) lds_barrier();
+        },
+        std::make_integer_sequence<int, D>{});
   }
-  out[((size_t)t * n_heads + (size_t)g * G + hh) * 64 + q * DS + dl] = o;
 }
 
 hipError_t launch_attn_scores(hipStream_t s, const float* q, const float* kc, int n0, int T, int n_heads, int n_kv,
@@ -706,13 +808,13 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
       BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64 * SM_WAVES), 0, s, scores, n0, n_heads, ld);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid(n_kv, G, T);
+    const dim3 grid(n_kv, G, T), block(192);
     switch (G) {
-      case 1: BB_LAUNCH(k_attn_pv_long<1>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 2: BB_LAUNCH(k_attn_pv_long<2>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 4: BB_LAUNCH(k_attn_pv_long<4>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 8: BB_LAUNCH(k_attn_pv_long<8>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      default: BB_LAUNCH(k_attn_pv_long<16>, grid, dim3(64), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 1: BB_LAUNCH(k_attn_pv_long<1>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 2: BB_LAUNCH(k_attn_pv_long<2>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 4: BB_LAUNCH(k_attn_pv_long<4>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 8: BB_LAUNCH(k_attn_pv_long<8>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      default: BB_LAUNCH(k_attn_pv_long<16>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
     }
     return hipGetLastError();
   }
