@@ -351,8 +351,22 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
     sel = gsel;
   }
   if (publish && blockIdx.x == 0) publish_dispatch(sel, n_ent, E, rb);
+  // One token routed or gated in the block: its K entries are the members, one per selected
+  // expert, and its selections are in LDS, so every thread finds the block's experts and their
+  // entries from them directly (no member lists and none of their barriers).
+  const bool one = KIND == GEMV_GATEUP && RM != RM_NONE && T == 1;
+  auto entry_of = [&](int ex) {
+    int k0 = 0;
+    for (int k = 0; k < K; ++k) k0 = sel[k] == ex ? k : k0;
+    return k0;
+  };
   SelRegs sr;
-  const uint32_t mask = read_selection(sel, n_ent, sr, mem);
+  uint32_t mask = 0;
+  if (one) {
+    for (int k = 0; k < K; ++k) mask |= 1u << sel[k];
+  } else {
+    mask = read_selection(sel, n_ent, sr, mem);
+  }
   const int n_units = __popc(mask) * tiles;
   const int lo = (int)((long long)blockIdx.x * n_units / gridDim.x);
   const int hi = (int)((long long)(blockIdx.x + 1) * n_units / gridDim.x);
@@ -379,11 +393,19 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
 
   int u = lo / tiles, tile = lo % tiles;
   int e = nth_expert(mask, u);
-  int n_mem = member_list(sr, n_ent, e, mem);
+  int one_ent = 0;  // (one) the entry of expert e
+  int n_mem = 1;
+  if (one) {
+    one_ent = entry_of(e);
+  } else {
+    n_mem = member_list(sr, n_ent, e, mem);
+  }
   typename R::Loaded L;
   if (has_blk) R::load(L, tile_addr(e, tile));
-  if (n_mem <= MST) stage(0, n_mem);
-  lds_barrier();
+  if (!one) {
+    if (n_mem <= MST) stage(0, n_mem);
+    lds_barrier();
+  }
   for (int unit = lo; unit < hi; ++unit) {
     typename R::Blk B;
     if (has_blk) R::prep(B, L);
@@ -406,7 +428,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
       if (has_blk) {
         if constexpr (KIND == GEMV_GATEUP) {
           for (int m = 0; m < cnt; ++m) {
-            const int tok = __builtin_amdgcn_readfirstlane(mem.list[c0 + m] / K);
+            const int tok = one ? 0 : __builtin_amdgcn_readfirstlane(mem.list[c0 + m] / K);
             if constexpr (ROUTE) {
               tv.v[m][w][lane] = R::value(B, rt.q[tok] + w * QK, rt.pairs[tok][w], rt.sx[tok][w]);
             } else {
@@ -423,7 +445,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
       for (int m = w; m < cnt; m += 8) {
         float acc = start;
         for (int b = 0; b < nb; ++b) acc += tv.v[m][b][lane];
-        const int ent = mem.list[c0 + m];
+        const int ent = one ? one_ent : mem.list[c0 + m];
         if constexpr (KIND == GEMV_GATEUP) {
           const float upv = __shfl(acc, (lane + 32) & 63);
           if (lane < 32) out[(size_t)ent * out_w + tile * 32 + lane] = silu_tab(acc, exptab) * upv;
@@ -435,9 +457,13 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
     }
     if (more && u_n != u) {
       e = e_n;
-      n_mem = member_list(sr, n_ent, e, mem);
-      if (n_mem <= MST) stage(0, n_mem);
-      lds_barrier();
+      if (one) {
+        one_ent = entry_of(e);
+      } else {
+        n_mem = member_list(sr, n_ent, e, mem);
+        if (n_mem <= MST) stage(0, n_mem);
+        lds_barrier();
+      }
     }
     u = u_n;
     tile = tile_n;
@@ -527,17 +553,26 @@ __global__ void __launch_bounds__(512) k_down_combine1(const uint8_t* __restrict
   const int k = min(lane >> 4, K - 1), r = lane & 15;
   const int nb = F / QK;
   const int orow = 16 * blockIdx.x + r;
+  // the act rows of the K entries, one wave per 256-block (at most 4 a wave), read first: they
+  // do not wait for the selections, which the weight reads do
+  constexpr int NTASK = 4 * 8 / 8;
+  float4 av[NTASK];
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int task = min(w + 8 * i, K * nb - 1), m = task / nb, b = task % nb;
+    av[i] = *reinterpret_cast<const float4*>(act + (size_t)m * F + b * QK + 4 * lane);
+  }
   const int e = rb.sel[k];  // T = 1: entry k is slot k
   const size_t tile_bytes = (size_t)nb * R::TB_BYTES;
   const bool has_blk = w < nb;
   typename R::Loaded L;
   if (has_blk) R::load(L, wpk + (size_t)e * stride_e + (size_t)(orow / 64) * tile_bytes + (size_t)w * R::TB_BYTES,
                        orow % 64);
-  // the act rows of the K entries, one wave per 256-block
-  for (int task = w; task < K * nb; task += 8) {
-    const int m = task / nb, b = task % nb;
-    const float4 v = *reinterpret_cast<const float4*>(act + (size_t)m * F + b * QK + 4 * lane);
-    wave_quantize_xq(v, xq[m] + b * QK, &sxs[m][b], pairs[m][b]);
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int task = w + 8 * i;
+    if (task < K * nb)
+      wave_quantize_xq(av[i], xq[task / nb] + (task % nb) * QK, &sxs[task / nb][task % nb], pairs[task / nb][task % nb]);
   }
   lds_barrier();
   float v = 0.0f;
