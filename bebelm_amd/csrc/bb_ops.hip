@@ -535,10 +535,11 @@ __global__ void __launch_bounds__(256) k_attn_pv_tile(const float* __restrict__ 
 // (head, dim) is one serial chain of adds, and a decode step has few of them (64 per head), so
 // what bounds a long row is how fast one wave can issue its chain: a wave issues one instruction
 // every four cycles, and a wave that also multiplied and read its operands spent about three of
-// them a position. Block (kv head g, dim slice q, token t) is three waves: wave 0 holds the 64
+// them a position. Block (kv head g, dim slice q, token t) is 1 + NP waves: wave 0 holds the 64
 // chains (lane L = head hh of the group x dim d of the slice, G heads x 64/G dims) and only adds;
-// waves 1 and 2 read the slice's values and the group's probabilities straight into registers
-// through buffer resources (positions past the row read zero), D chunks ahead, and write the
+// the NP producer waves (four for slices of 16 or more dims, else two) read the slice's values
+// and the group's probabilities straight into registers through buffer resources (positions
+// past the row read zero), D chunks ahead, and write the
 // products of each chunk of 64 positions to a ring of PVL_NB chunks in LDS, one row of products per
 // chain. The chain wave reads a row 16 bytes (four positions) at a time, so a position costs it
 // one add and a quarter of a read. A block barrier a chunk hands the chunks over: in step k the
@@ -556,8 +557,9 @@ struct PvlCfg {
   static constexpr int PCL = PC < 4 ? PC : 4;        // pieces side by side in a load ...
   static constexpr int PPL = 64 / PCL;               // ... over this many positions (lane = position x piece)
   static constexpr bool SPLIT_HEADS = PCL == 1;      // a load covers the chunk: the producers split the heads
+  static constexpr int NP = PCL == 4 ? 4 : 2;        // producer waves
   static constexpr int HP = SPLIT_HEADS ? G / 2 : G; // heads of a producer
-  static constexpr int NK = SPLIT_HEADS ? 1 : PCL / 2;  // adjacent positions of a lane (a producer: NK·PPL)
+  static constexpr int NK = SPLIT_HEADS ? 1 : PCL / NP;  // adjacent positions of a lane (a producer: NK·PPL)
   static constexpr int NQG = PC / PCL;               // piece groups (of PCL)
   static constexpr int NL = NK * NQG;                // 16-byte value loads of a lane a chunk
   static constexpr int HPL = (HP + PCL - 1) / PCL;   // probabilities a lane loads a position (the PCL
@@ -566,7 +568,7 @@ struct PvlCfg {
   static constexpr int NLD = NL + HPL;               // loads a chunk (a lane's NK probabilities in one)
   static constexpr int D0 = 176 / NV < 63 / NLD ? 176 / NV : 63 / NLD;
   static constexpr int D = D0 < 12 ? D0 : 12;        // chunks of loads in flight (NLD·D fits vmcnt)
-  static_assert(NL * 4 * HP == 32, "a producer lane makes 32 products a chunk");
+  static_assert(NL * 4 * HP * NP == 64, "the producers' lanes make the chunk's 64 x 64 products");
 };
 
 template <class F, int... I>
@@ -575,7 +577,7 @@ __device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, I..
 }
 
 template <int G>
-__global__ void __launch_bounds__(192) k_attn_pv_long(const float* __restrict__ p, const float* __restrict__ vc,
+__global__ void __launch_bounds__(320) k_attn_pv_long(const float* __restrict__ p, const float* __restrict__ vc,
                                                      int n0, int n_heads, int n_kv, int ld, float* __restrict__ out) {
   using C = PvlCfg<G>;
   constexpr int DS = C::DS, PCL = C::PCL, PPL = C::PPL, HP = C::HP, NK = C::NK, NQG = C::NQG, NL = C::NL, D = C::D;
@@ -808,13 +810,16 @@ hipError_t launch_attn_pv(hipStream_t s, float* scores, const float* vc, int n0,
       BB_LAUNCH(k_attn_softmax<false>, dim3(n_heads, T), dim3(64 * SM_WAVES), 0, s, scores, n0, n_heads, ld);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid(n_kv, G, T), block(192);
+    const dim3 grid(n_kv, G, T);
+    auto blk = [](int np) { return dim3(64 * (1 + np)); };  // the chain wave and the producers
     switch (G) {
-      case 1: BB_LAUNCH(k_attn_pv_long<1>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 2: BB_LAUNCH(k_attn_pv_long<2>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 4: BB_LAUNCH(k_attn_pv_long<4>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      case 8: BB_LAUNCH(k_attn_pv_long<8>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
-      default: BB_LAUNCH(k_attn_pv_long<16>, grid, block, 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 1: BB_LAUNCH(k_attn_pv_long<1>, grid, blk(PvlCfg<1>::NP), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 2: BB_LAUNCH(k_attn_pv_long<2>, grid, blk(PvlCfg<2>::NP), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 4: BB_LAUNCH(k_attn_pv_long<4>, grid, blk(PvlCfg<4>::NP), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      case 8: BB_LAUNCH(k_attn_pv_long<8>, grid, blk(PvlCfg<8>::NP), 0, s, scores, vc, n0, n_heads, n_kv, ld, out); break;
+      default:
+        BB_LAUNCH(k_attn_pv_long<16>, grid, blk(PvlCfg<16>::NP), 0, s, scores, vc, n0, n_heads, n_kv, ld, out);
+        break;
     }
     return hipGetLastError();
   }
