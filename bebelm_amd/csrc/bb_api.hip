@@ -797,6 +797,10 @@ struct bb_model {
   std::vector<Layer> layers;
   float *h = nullptr, *normed = nullptr, *tmp = nullptr;
   bb::Q8Bufs nq{};          // Q8 of normed, written with it for the conv / attention / dense layers
+  // a boundary before an MoE layer of a few tokens also takes its router logits and XQ records
+  // (the residual then goes to h2, which becomes h)
+  float *h2 = nullptr, *logits = nullptr;
+  bb::XQBufs xq{};
   uint32_t* tok = nullptr;  // token ids of the current call
   size_t cap_T = 0, tok_cap = 0;
   bb::ModelOwned owned;  // set by bb_model_load
@@ -1930,7 +1934,8 @@ void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
   if (T <= m->cap_T) return;
   check_hip(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   for (void** p : {(void**)&m->h, (void**)&m->normed, (void**)&m->tmp, (void**)&m->nq.q, (void**)&m->nq.scales,
-                   (void**)&m->nq.sums}) {
+                   (void**)&m->nq.sums, (void**)&m->h2, (void**)&m->logits, (void**)&m->xq.q, (void**)&m->xq.sx,
+                   (void**)&m->xq.pairs}) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
   }
@@ -1943,6 +1948,16 @@ void model_buffers(bb_ctx* c, bb_model* m, size_t T) {
     m->nq.q = static_cast<int8_t*>(dev_alloc(T * H));
     m->nq.scales = static_cast<float*>(dev_alloc(T * H / 256 * 4));
     m->nq.sums = static_cast<int32_t*>(dev_alloc(T * H / 32 * 4));
+  }
+  if (H % 256 == 0) {
+    // (h2 as large as h: the two trade places at a routing boundary; the logits and XQ records
+    // serve calls of at most ROUTE_IN_GATEUP_MAX_T tokens)
+    constexpr size_t TR = bb::ROUTE_IN_GATEUP_MAX_T;
+    m->h2 = static_cast<float*>(dev_alloc(T * H * 4));
+    m->logits = static_cast<float*>(dev_alloc(TR * 32 * 4));
+    m->xq.q = static_cast<int8_t*>(dev_alloc(TR * H));
+    m->xq.sx = static_cast<float*>(dev_alloc(TR * (H / 256) * 4));
+    m->xq.pairs = static_cast<uint32_t*>(dev_alloc(TR * (H / 256) * 12 * 4));
   }
   m->cap_T = T;
 }
@@ -2007,9 +2022,25 @@ void model_run_dev(bb_ctx* c, bb_model* m, bb_cache* k, const uint32_t* tokens, 
     auto& L = m->layers[i];
     if (L.conv) conv_forward_dev(c, L.conv, k->conv[i], m->normed, T, m->tmp, nq);
     else attn_forward_dev(c, L.attn, k->kv[i], k->pos, m->normed, T, m->tmp, nq);
-    boundary(L.ffn_norm, L.dense != nullptr);
-    if (L.moe) moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr);
-    else dense_forward_dev(c, L.dense, m->normed, T, m->tmp, nq);
+    // before an MoE layer of a few tokens on the GEMV path the boundary also takes the layer's
+    // router logits and its input's XQ records, and the gate/up GEMV only gates
+    const bb_moe* mo = L.moe;
+    const bool route_here = fused && mo && m->h2 && T <= (size_t)bb::ROUTE_IN_GATEUP_MAX_T &&
+                            T * (size_t)mo->K < c->batched_min_entries && H % 128 == 0 && mo->E <= 32 &&
+                            mo->K <= 8;
+    if (route_here) {
+      launch(c, bb::K_RESIDUAL_ROUTE, [&] {
+        return bb::launch_residual_norm_route(c->stream, m->h, m->h2, nullptr, nullptr, 0, m->tmp, L.ffn_norm, m->eps,
+                                              (int)H, (int)T, m->normed, mo->router_cm, mo->E, m->logits, m->xq);
+      });
+      std::swap(m->h, m->h2);
+      const PreRoute pre{m->logits, m->xq};
+      moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr, true, &pre);
+    } else {
+      boundary(L.ffn_norm, L.dense != nullptr);
+      if (L.moe) moe_forward_dev(c, L.moe, m->normed, T, m->tmp, nullptr);
+      else dense_forward_dev(c, L.dense, m->normed, T, m->tmp, nq);
+    }
     boundary(i + 1 < n_layers ? m->layers[i + 1].attn_norm : nullptr, true);
   }
   k->pos += T;
@@ -2131,7 +2162,8 @@ int bb_model_destroy(bb_model* m) {
       if (L.ffn_norm) (void)hipFree(L.ffn_norm);
     }
     for (void* p : {(void*)m->final_norm, (void*)m->h, (void*)m->normed, (void*)m->tmp, (void*)m->tok,
-                    (void*)m->nq.q, (void*)m->nq.scales, (void*)m->nq.sums})
+                    (void*)m->nq.q, (void*)m->nq.scales, (void*)m->nq.sums, (void*)m->h2, (void*)m->logits,
+                    (void*)m->xq.q, (void*)m->xq.sx, (void*)m->xq.pairs})
       if (p) (void)hipFree(p);
     bb::free_owned(m->owned);
     delete m;
