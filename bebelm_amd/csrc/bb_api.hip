@@ -1993,7 +1993,9 @@ void model_run_dev(bb_ctx* c, bb_model* m, bb_cache* k, const uint32_t* tokens, 
   });
   // Each layer boundary (h += sub-layer output, then the next rmsnorm) is one launch of
   // k_residual_norm, which also writes the normed rows' Q8 when the next sub-layer projects
-  // them (conv, attention, dense FFN; the MoE route quantises its input itself).
+  // them (conv, attention, dense FFN; the MoE route quantises its input itself), or, before an
+  // MoE layer of a few tokens, of k_residual_norm_route, which also takes the layer's router
+  // logits and XQ records.
   const bool fused = H <= (size_t)bb::GU_H_MAX && m->nq.q;
   auto boundary = [&](const float* gain, bool q8) {
     if (fused) {
