@@ -1188,12 +1188,13 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
   constexpr int NH = 2 * NB, AHEAD = GU16_SLOTS - 1;
   auto half_load = [&](Gu16H& v, int h) { gu16_load(v, rsrc, og + 512u * (uint32_t)(h & 1), oq, (uint32_t)((h >> 1) * TB)); };
   Gu16H wr[GU16_SLOTS];
-#pragma unroll
-  for (int h = 0; h < AHEAD; ++h)
-    if (h < NH) half_load(wr[h], h);
+  // the first half goes out before the selections are known, the rest of the halves in flight
+  // only once the expert is known to have members (an expert nobody chose then wastes one half
+  // a wave instead of AHEAD)
+  half_load(wr[0], 0);
   __builtin_amdgcn_sched_barrier(0);
   // this wave's copies landed (the weight loads issued after them may still be in flight)
-  constexpr int WL = 3 * (AHEAD < NH ? AHEAD : NH);
+  constexpr int WL = 3;
   __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
   lds_barrier();
   // the expert's entries (entry i = token·K + slot on lane i), the entries of smaller expert ids
@@ -1205,6 +1206,10 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
     return;
   }
+#pragma unroll
+  for (int h = 1; h < AHEAD; ++h)
+    if (h < NH) half_load(wr[h], h);
+  __builtin_amdgcn_sched_barrier(0);
   const int base = __popcll(__ballot(sv >= 0 && sv < e));
   const unsigned long long kmask = K >= 64 ? ~0ull : (1ull << K) - 1ull;
   int orow[4];
