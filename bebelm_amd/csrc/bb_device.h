@@ -65,6 +65,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
+// Cache policy of the loads that stream expert weights read once per call (the decode paths):
+// non-temporal ("nt"), so a layer's weights pass through L2 without displacing the data that
+// the next kernels read again (the router, the tokens' rows and Q8 records, the selections).
+constexpr int CPOL_NT = 2;
+__device__ __forceinline__ uint4 buf_load16nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, CPOL_NT));
+}
+// A 16-byte global load with the same policy.
+__device__ __forceinline__ uint4 ld16_nt(const uint8_t* p) {
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p)));
+}
 __device__ __forceinline__ float buf_load4f(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }

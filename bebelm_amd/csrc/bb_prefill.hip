@@ -309,8 +309,9 @@ __device__ __forceinline__ void gemm_issue(const uint8_t* w0, size_t tile_bytes,
         const int u = j * 64 + lane;
         if (u < C::W_UNITS) {
           const int k = u / (TB / 16), o = u % (TB / 16);
+          // a decode batch's weight tiles are read once (one member tile per expert): streamed
           __builtin_amdgcn_global_load_lds(w0 + (size_t)k * tile_bytes + (size_t)b * TB + 16 * o, wb + j * 1024, 16,
-                                           0, 0);
+                                           0, MT == 1 ? CPOL_NT : 0);
         }
       }
     } else if (PARTS & ISSUE_X) {
@@ -1100,9 +1101,9 @@ struct Gu16H {
 };
 
 __device__ __forceinline__ void gu16_load(Gu16H& v, __amdgpu_buffer_rsrc_t r, uint32_t orow, uint32_t oq, uint32_t sb) {
-  v.h = buf_load16(r, orow, sb);
-  v.q0 = buf_load16(r, orow + oq, sb);
-  v.q1 = buf_load16(r, orow + oq + 1024u, sb);
+  v.h = buf_load16nt(r, orow, sb);
+  v.q0 = buf_load16nt(r, orow + oq, sb);
+  v.q1 = buf_load16nt(r, orow + oq + 1024u, sb);
 }
 
 // One super-block of one of the wave's row tiles (header h, qs words q0 and q1) against the 16

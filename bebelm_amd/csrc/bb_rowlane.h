@@ -93,10 +93,11 @@ struct Q4Blk {
 };
 
 // tb: the tile-block (tile-packed layout); chunk k of row j's block is at tb + 1024k + 16j.
-// Row = lane: each load of the wave reads 1 KB of contiguous memory.
+// Row = lane: each load of the wave reads 1 KB of contiguous memory. The GEMVs read each weight
+// once per call, so the loads stream (non-temporal).
 __device__ __forceinline__ void q4_load(uint4 (&w)[9], const uint8_t* __restrict__ tb, int row) {
 #pragma unroll
-  for (int k = 0; k < 9; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * row);
+  for (int k = 0; k < 9; ++k) w[k] = ld16_nt(tb + 1024 * k + 16 * row);
 }
 
 // get_scale_min_k4 (dequant.rs:64-72) on four bytes at a time, then the nibble unpack
@@ -171,7 +172,7 @@ struct Q6Blk {
 // Bytes 0..207 of the block (ql, qh, scales) in 13 chunks, then the f16 d from the tail.
 __device__ __forceinline__ void q6_load(uint4 (&w)[13], uint32_t& dbits, const uint8_t* __restrict__ tb, int row) {
 #pragma unroll
-  for (int k = 0; k < 13; ++k) w[k] = *reinterpret_cast<const uint4*>(tb + 1024 * k + 16 * row);
+  for (int k = 0; k < 13; ++k) w[k] = ld16_nt(tb + 1024 * k + 16 * row);
   dbits = *reinterpret_cast<const uint16_t*>(tb + 13 * 1024 + 2 * row);
 }
 
