@@ -814,26 +814,47 @@ hipError_t launch_residual_norm_route(hipStream_t s, const float* h_in, float* h
 
 // ---- combine -----------------------------------------------------------------------------------
 // out[t][o] = Σ_k w[t,k]·slots[t*K+k][o], k ascending from +0.0 (add_scaled, elementwise.rs:12).
+// KT > 0: K = KT known at compile time, every slot's loads issued before the first add (one
+// memory round trip instead of one per slot); KT = 0: any K, one slot after the other.
+template <int KT>
 __global__ void __launch_bounds__(256) k_combine(const float* __restrict__ slots, const float* __restrict__ wts, int T,
                                                  int H, int K, float* __restrict__ out) {
   // block (x, t): outputs 4·(256x + thread) .. +3 of token t
   const int t = blockIdx.y, o4 = blockIdx.x * 256 + threadIdx.x;
   if (o4 * 4 >= H) return;
+  if constexpr (KT > 0) K = KT;
   const float4* s4 = reinterpret_cast<const float4*>(slots);
   float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int k = 0; k < K; ++k) {
-    const float wk = wts[(size_t)t * K + k];
-    const float4 v = s4[((size_t)t * K + k) * (H / 4) + o4];
-    acc.x = acc.x + wk * v.x;
-    acc.y = acc.y + wk * v.y;
-    acc.z = acc.z + wk * v.z;
-    acc.w = acc.w + wk * v.w;
+  constexpr int NR = KT > 0 ? KT : 1;
+  float wk[NR];
+  float4 v[NR];
+  for (int k0 = 0; k0 < K; k0 += NR) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      wk[i] = wts[(size_t)t * K + k0 + i];
+      v[i] = s4[((size_t)t * K + k0 + i) * (H / 4) + o4];
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      acc.x = acc.x + wk[i] * v[i].x;
+      acc.y = acc.y + wk[i] * v[i].y;
+      acc.z = acc.z + wk[i] * v[i].z;
+      acc.w = acc.w + wk[i] * v[i].w;
+    }
   }
   reinterpret_cast<float4*>(out)[(size_t)t * (H / 4) + o4] = acc;
 }
 
 hipError_t launch_combine(hipStream_t s, const float* slots, const float* wts, int T, int H, int K, float* out) {
-  BB_LAUNCH(k_combine, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, s, slots, wts, T, H, K, out);
+  const dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)T);
+  switch (K) {
+#define BB_COMBINE_K(k) \
+  case k: BB_LAUNCH(k_combine<k>, grid, dim3(256), 0, s, slots, wts, T, H, K, out); break;
+    BB_COMBINE_K(1) BB_COMBINE_K(2) BB_COMBINE_K(3) BB_COMBINE_K(4)
+    BB_COMBINE_K(5) BB_COMBINE_K(6) BB_COMBINE_K(7) BB_COMBINE_K(8)
+#undef BB_COMBINE_K
+    default: BB_LAUNCH(k_combine<0>, grid, dim3(256), 0, s, slots, wts, T, H, K, out);
+  }
   return hipGetLastError();
 }
 
