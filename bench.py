@@ -454,8 +454,9 @@ def decoder_bench(args, ctx, with_cpu):
             m.forward_step(int(t), cache)
         return (time.perf_counter() - t0) / n_dec
 
-    # decode at a 512-token context
-    dec = decode_rate(32)
+    # decode at a 512-token context: the median of three runs of 32 steps (the host's share of a
+    # step varies from run to run)
+    dec = sorted(decode_rate(32) for _ in range(3))[1]
     # per-kernel times of decode steps (events stamped by each dispatch)
     ctx.reset_stats()
     ctx.profile(True)
@@ -474,7 +475,7 @@ def decoder_bench(args, ctx, with_cpu):
         t0 = time.perf_counter()
         m.absorb(cache, rng_dec.integers(0, mw.vocab, more).astype(np.uint32), 32768)
         ab = time.perf_counter() - t0
-        d = decode_rate(16)
+        d = sorted(decode_rate(16) for _ in range(3))[1]
         ctx.reset_stats()
         ctx.profile(True)
         for t in rng_dec.integers(0, mw.vocab, 4):
