@@ -540,8 +540,11 @@ def main():
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
 
     def defaults(config):
-        steps = args.steps if args.steps is not None else (20 if config == 4 else 50 if config == 3 else 200)
-        warmup = args.warmup if args.warmup is not None else (3 if config == 4 else 20)
+        # timed steps: 0.04-0.11 s of GPU work each, so that the fixed cost of a timed region (the
+        # launch queue filling behind the first step, the final synchronisation) is a small share
+        # of a step (config 2: 53.3 µs a step over 200 steps, 49.5-49.7 µs over 2000)
+        steps = args.steps if args.steps is not None else {1: 2000, 2: 2000, 3: 500, 4: 100, 5: 200}[config]
+        warmup = args.warmup if args.warmup is not None else {1: 200, 2: 200, 3: 50, 4: 10, 5: 20}[config]
         return steps, warmup
 
     steps, warmup = defaults(args.config)
