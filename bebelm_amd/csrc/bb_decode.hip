@@ -563,6 +563,10 @@ __global__ void __launch_bounds__(512) k_down_combine1(const uint8_t* __restrict
     av[i] = *reinterpret_cast<const float4*>(act + (size_t)m * F + b * QK + 4 * lane);
   }
   const int e = rb.sel[k];  // T = 1: entry k is slot k
+  // the combine weights as well, here rather than after the barriers (another kernel wrote them)
+  float wk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) wk[j] = rb.wts[min(j, K - 1)];
   const size_t tile_bytes = (size_t)nb * R::TB_BYTES;
   const bool has_blk = w < nb;
   typename R::Loaded L;
@@ -591,7 +595,9 @@ __global__ void __launch_bounds__(512) k_down_combine1(const uint8_t* __restrict
   lds_barrier();
   if (tid < 16) {
     float y = 0.0f;
-    for (int j = 0; j < K; ++j) y = y + rb.wts[j] * slot[j][tid];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < K) y = y + wk[j] * slot[j][tid];
     out[16 * blockIdx.x + tid] = y;
   }
 }
