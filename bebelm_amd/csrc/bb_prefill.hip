@@ -1269,6 +1269,111 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
   }
 }
 
+// ---- Q4_K down of decode batches (at most 16 members per expert): weight rows into registers ------
+// k_gateup16's form for the down GEMM. Work unit = one expert x 16 output rows (a quarter of a
+// 64-row packed tile); block = GU16_WAVES waves on the expert's rows 256j..256j+255, H/256 blocks
+// per expert, expert-major. A token chooses an expert at most once, so an expert of a batch of at
+// most 16 tokens has at most 16 members: its entries in ascending order, whose Q8 act rows are the
+// group positions base..base+cnt-1 (the order k_gateup16 and k_quant_rows write them in). The
+// block requests its first weights from its id, reads the selections, copies its members' act
+// rows (all NB super-blocks, XOR-swizzled chunks as k_gemm stages them) and their scales into LDS,
+// and streams the rest of its weights through the register ring while it computes. The integer
+// sums and the f32 epilogue are q4_block's (gu16_tile), from +0.0 (-0.0 for an expert with one
+// member, as k_gemm); member m's outputs go to the slot row of its entry.
+template <int NB>
+__global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __restrict__ wpk, size_t stride_e,
+                                                              int n_out, int n_ent,
+                                                              const int32_t* __restrict__ sel, GemmX x,
+                                                              float* __restrict__ out) {
+  constexpr int TB = (int)TB4;
+  constexpr int XB = 16 * QK;  // one super-block of 16 members' quants
+  constexpr int NW = GU16_WAVES;
+  constexpr int NC = (4 * NB + NW - 1) / NW;  // activation copies per wave
+  __shared__ __align__(16) uint8_t xs[NB * XB];
+  __shared__ __align__(16) float sxs[NW * 64];  // scales [b][16] (waves 0-1); the rest absorbs copies
+  __shared__ int32_t selw[NW * 64];
+  const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bpe = n_out / (16 * NW);          // blocks per expert
+  const int e = blockIdx.x / bpe;
+  const int o = (blockIdx.x % bpe) * NW + w;  // the wave's 16-row group of the expert
+  const int t64 = o >> 2, t16 = o & 3;
+  // the selections (T*K <= 64 entries; their workspace slot holds 64) into the wave's own slots
+  lds_dma4(reinterpret_cast<const uint8_t*>(sel + lane), reinterpret_cast<uint8_t*>(selw + 64 * w));
+  const size_t tile_bytes = (size_t)NB * TB;
+  const __amdgpu_buffer_rsrc_t rsrc = buf_rsrc(wpk + (size_t)e * stride_e + (size_t)t64 * tile_bytes,
+                                               (uint32_t)tile_bytes);
+  // half h = super-block h of the wave's 16 rows
+  const uint32_t og = 16u * (uint32_t)(16 * t16 + r), oq = 1024u * (uint32_t)(1 + 2 * g);
+  constexpr int AHEAD = GU16_SLOTS - 1;
+  auto half_load = [&](Gu16H& v, int h) { gu16_load(v, rsrc, og, oq, (uint32_t)(h * TB)); };
+  Gu16H wr[GU16_SLOTS];
+  half_load(wr[0], 0);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wave's selection copy landed (the weight loads issued after it may still be in flight)
+  constexpr int WS = 3;
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (WS & 15) | ((WS >> 4) << 14));
+  // the expert's entries (entry i on lane i) and the entries of smaller expert ids (the first
+  // group position of its members)
+  const int sv = lane < n_ent ? selw[64 * w + lane] : -1;
+  const unsigned long long me = __ballot(sv == e);
+  const int cnt = __popcll(me);  // the same in every wave of the block
+  if (cnt == 0) {
+    __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
+    return;
+  }
+  const int base = __popcll(__ballot(sv >= 0 && sv < e));
+  {
+    // act copies: NB super-blocks x 4 KB as 4·NB wave copies of 1 KB, copy j = super-block j/4,
+    // members 4(j%4)..+3 (members past cnt repeat the last one's row); wave w issues copies w,
+    // w+NW, ... (repeats of the last copy rewrite the same bytes)
+    const int m = lane >> 4, p = lane & 15;
+#pragma unroll
+    for (int t = 0; t < NC; ++t) {
+      const int j = min(w + NW * t, 4 * NB - 1);
+      const int b = j >> 2, mm = 4 * (j & 3) + m;
+      const int row = base + min(mm, cnt - 1);
+      lds_dma16(reinterpret_cast<const uint8_t*>(x.q) + (size_t)row * (NB * QK) + b * QK + 16 * (p ^ mm),
+                xs + j * 1024);
+    }
+    // scales: wave w < 2 copies entries 64w.. of [b][16]; the others copy into spare space
+    const int u = min(64 * w + lane, 16 * NB - 1);
+    const int row = base + min(u & 15, cnt - 1);
+    lds_dma4(reinterpret_cast<const uint8_t*>(x.sx + (size_t)row * NB + (u >> 4)),
+             reinterpret_cast<uint8_t*>(sxs + 64 * w));
+  }
+  constexpr int NL = AHEAD - 1 < NB - 1 ? AHEAD - 1 : NB - 1;  // halves requested after the copies
+#pragma unroll
+  for (int h = 1; h <= NL; ++h) half_load(wr[h], h);
+  __builtin_amdgcn_sched_barrier(0);
+  // this wave's copies landed (the weight loads issued after them may still be in flight)
+  constexpr int WL = 3 * NL;
+  __builtin_amdgcn_s_waitcnt(0x3f70 | (WL & 15) | ((WL >> 4) << 14));
+  lds_barrier();
+  const float start = cnt > 1 ? 0.0f : -0.0f;
+  float acc[4] = {start, start, start, start};
+#pragma unroll
+  for (int h = 0; h < NB; ++h) {
+    // the slot half h-1 used takes half h+AHEAD
+    if (h + AHEAD < NB) half_load(wr[(h + AHEAD) % GU16_SLOTS], h + AHEAD);
+    __builtin_amdgcn_sched_barrier(0);
+    const Gu16H& cur = wr[h % GU16_SLOTS];
+    gu16_tile(cur.h, cur.q0, cur.q1, xs + h * XB, sxs + 16 * h, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i]));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const int col = 64 * t64 + 16 * t16 + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = 4 * g + i;  // member n: the n-th entry of the expert
+    if (n >= cnt) continue;
+    unsigned long long rest = me;
+    for (int k = 0; k < n; ++k) rest &= rest - 1ull;
+    out[(size_t)__builtin_ctzll(rest) * n_out + col] = acc[i];
+  }
+}
+
 // Q6_K down GEMMs whose groups hold this many members on average take k_gemm_wide (blocks of up
 // to 256 members). For config 4 (4096 tokens, Zipf-skewed groups) it runs the Q6_K down GEMM in
 // 228 µs against k_gemm's 274; the Q4_K gate/up GEMM, whose 3-pass epilogue and operand build
@@ -1313,6 +1418,20 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
       else
         BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx);
       if (quantized) *quantized = true;
+      return hipGetLastError();
+    }
+  }
+  if constexpr (DT == DT_Q4_K && KIND == GEMM_DOWN) {
+    // decode batches of at most 16 tokens (an expert then has at most 16 members): k_down16
+    if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && n_out % 256 == 0 && n_in % QK == 0 && n_in / QK >= 1 &&
+        n_in / QK <= 8) {
+      const dim3 grid(E * (n_out / 256)), block(64 * GU16_WAVES);
+      switch (n_in / QK) {
+#define BB_DOWN16(nb) \
+  case nb: BB_LAUNCH(k_down16<nb>, grid, block, 0, s, w, stride_e, n_out, n_ent, rb.sel, x, out); break;
+        BB_DOWN16(1) BB_DOWN16(2) BB_DOWN16(3) BB_DOWN16(4) BB_DOWN16(5) BB_DOWN16(6) BB_DOWN16(7) BB_DOWN16(8)
+#undef BB_DOWN16
+      }
       return hipGetLastError();
     }
   }
