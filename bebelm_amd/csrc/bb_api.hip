@@ -332,6 +332,15 @@ struct WsRegion {
   size_t cap = 0;
 };
 
+// Decode batches whose gate/up and down GEMMs both run as the kernels of at most 16 members
+// (k_gateup16, k_down16): the Q8 act rows of expert e's member m go to row 16e + m (E·16 rows).
+bool moe_act_pad(const bb_moe* m, size_t T) {
+  const int n_ent = (int)(T * m->K);
+  return bb::gateup16_applies((int)m->gu_dtype, (int)T, (int)m->H, (int)m->F, (int)m->E, (int)m->K,
+                              !bb::gemm_reads_ms((int)m->dn_dtype, n_ent, (int)m->E)) &&
+         bb::down16_applies((int)m->dn_dtype, (int)T, (int)m->H, (int)m->F, (int)m->E, (int)m->K);
+}
+
 MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegion* fixed = nullptr) {
   const size_t H = m->H, F = m->F, E = m->E, K = m->K;
   for (int pass = 0; pass < 2; ++pass) {
@@ -353,8 +362,9 @@ MoeWs carve_moe(bb_ctx* c, const bb_moe* m, size_t T, bool batched, const WsRegi
     w.act = cv.take<float>(T * K * F);
     w.slots = cv.take<float>(T * K * H);
     if (batched) {
-      w.aq = cv.take<int8_t>(T * K * F);
-      w.aq_sx = cv.take<float>(T * K * F / 256);
+      const size_t aq_rows = moe_act_pad(m, T) ? std::max(T * K, 16 * E) : T * K;
+      w.aq = cv.take<int8_t>(aq_rows * F);
+      w.aq_sx = cv.take<float>(aq_rows * F / 256);
       w.aq_ms = bb::gemm_reads_ms(m->dn_dtype, T * K, E) ? cv.take<uint16_t>(T * K * F / 256 * 16) : nullptr;
     }
     if (pass == 0) {
@@ -407,10 +417,11 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
       launch(c, bb::K_DISPATCH, [&] { return bb::launch_dispatch(c->stream, (int)n_ent, m->E, w.rb); });
     // (decode batches: the gate/up kernel also writes the act rows' Q8 when it can)
     bool quantized = false;
+    const bool act_pad = moe_act_pad(m, T);
     launch(c, bb::K_GEMM_GATEUP, [&] {
       return bb::launch_gemm_gateup(c->stream, m->gu_dtype, m->gu_packed, m->stride_gu, (int)T, m->H, m->F, m->E, m->K,
                                     w.rb, bb::GemmX{w.xq.q, w.xq.sx, w.xq.ms}, w.act, w.aq_ms ? nullptr : w.aq,
-                                    w.aq_sx, &quantized);
+                                    w.aq_sx, &quantized, act_pad);
     });
     if (!quantized)
       launch(c, bb::K_QUANT, [&] {
@@ -418,7 +429,7 @@ MoeWs moe_forward_dev(bb_ctx* c, bb_moe* m, const float* x, size_t T, float* out
       });
     launch(c, bb::K_GEMM_DOWN, [&] {
       return bb::launch_gemm_down(c->stream, m->dn_dtype, m->dn_packed, m->stride_dn, (int)T, m->H, m->F, m->E, m->K,
-                                  w.rb, bb::GemmX{w.aq, w.aq_sx, w.aq_ms}, w.slots);
+                                  w.rb, bb::GemmX{w.aq, w.aq_sx, w.aq_ms}, w.slots, act_pad);
     });
   } else {
     const int batch_mode = T > 1;

@@ -178,6 +178,9 @@ hipError_t launch_dispatch(hipStream_t s, int n_ent, int E, const RouteBufs& rb)
 // Member tile of the grouped GEMMs in units of 16 members; 1 means the GEMMs derive the
 // grouping from rb.sel themselves and need no dispatch kernel before them.
 int gemm_member_tiles(int n_ent, int E);
+// Whether launch_gemm_gateup runs the gate/up GEMM of this call as k_gateup16 (decode batches of
+// Q4_K experts, the act Q8 written by the kernel: act_q8).
+bool gateup16_applies(int dtype, int T, int H, int F, int E, int K, bool act_q8);
 
 // Grouped expert GEMM over the members of each expert (int8 MFMA with exact integer
 // sub-dots and the reference's f32 per-block epilogue).
@@ -198,11 +201,18 @@ inline bool gemm_reads_ms(int dtype, size_t n_ent, size_t E) {
 }
 // With aq set, a launch that can also writes the Q8 of the act rows (aq, aq_sx: the
 // k_quant_rows output) and sets *quantized; otherwise the caller quantises them.
+// act_pad (decode batches whose gate/up runs as k_gateup16 and whose down runs as k_down16:
+// gateup16_applies and down16_applies): the Q8 act rows of expert e's member m are row 16e + m of
+// aq (E·16 rows) instead of its group position, so the down GEMM copies them without reading the
+// selections first.
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
                               int E, int K, const RouteBufs& rb, GemmX x, float* act, int8_t* aq = nullptr,
-                              float* aq_sx = nullptr, bool* quantized = nullptr);
+                              float* aq_sx = nullptr, bool* quantized = nullptr, bool act_pad = false);
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
-                            int K, const RouteBufs& rb, GemmX x, float* slots);
+                            int K, const RouteBufs& rb, GemmX x, float* slots, bool act_pad = false);
+// Whether launch_gemm_down runs the down GEMM of this call as k_down16 (decode batches of Q4_K
+// experts, at most 16 members per expert).
+bool down16_applies(int dtype, int T, int H, int F, int E, int K);
 
 // A Q4_K / Q6_K weight matrix in the grouped GEMM's packed tile layout as a single expert: plain
 // 64-row tiles (GEMM_DOWN form, n_out % 128 == 0) or gate and up interleaved (GEMM_GATEUP form,

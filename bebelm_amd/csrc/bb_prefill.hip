@@ -1070,6 +1070,18 @@ __global__ void __launch_bounds__(64 * WIDE_WAVES, 2) k_gemm_wide(const uint8_t*
 // still fills a CU's LDS alone.)
 int gemm_member_tiles(int n_ent, int E) { return n_ent >= 16 * E ? 4 : 1; }
 
+bool gateup16_applies(int dtype, int T, int H, int F, int E, int K, bool act_q8) {
+  const int n_ent = T * K;
+  return dtype == DT_Q4_K && act_q8 && gemm_member_tiles(n_ent, E) == 1 && T <= 16 && n_ent <= 64 && E <= 32 &&
+         F % QK == 0 && (H == 2048 || H == 512);
+}
+
+bool down16_applies(int dtype, int T, int H, int F, int E, int K) {
+  const int n_ent = T * K;
+  return dtype == DT_Q4_K && gemm_member_tiles(n_ent, E) == 1 && T <= 16 && n_ent <= 64 && H % 256 == 0 &&
+         F % QK == 0 && F / QK >= 1 && F / QK <= 8;
+}
+
 // ---- Q4_K gate/up of decode batches (at most 16 tokens): weight rows straight into registers -------
 // Work unit = one expert x 16 outputs: the gate rows 16t.. and the up rows 32 + 16t.. of a 64-row
 // packed tile (t = 0, 1), so one wave holds both values of its outputs and applies SwiGLU itself.
@@ -1138,7 +1150,7 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
                                                                 int E, int K, int n_out, int n_tok,
                                                                 const int32_t* __restrict__ sel, GemmX x,
                                                                 float* __restrict__ out, int8_t* __restrict__ aq,
-                                                                float* __restrict__ aq_sx) {
+                                                                float* __restrict__ aq_sx, int act_pad) {
   constexpr int TB = (int)TB4;
   constexpr int XB = 16 * QK;  // one super-block of the 16 tokens' quants
   constexpr int NW = GU16_WAVES;
@@ -1261,7 +1273,8 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_gateup16(const uint8_t* 
     const unsigned long long bits = (me >> (n * K)) & kmask;
     if (bits) {
       const int ii = n * K + __builtin_ctzll(bits);
-      const int row = base + __popcll(me & ((1ull << ii) - 1ull));
+      const int mi = __popcll(me & ((1ull << ii) - 1ull));  // the entry's rank among the expert's
+      const int row = act_pad ? 16 * e + mi : base + mi;
       const int jb = col / QK;
       const float4 v = *reinterpret_cast<const float4*>(actv + n * QK + 4 * lane);
       wave_quantize_xq(v, aq + (size_t)row * n_out + jb * QK, aq_sx + (size_t)row * (n_out / QK) + jb, nullptr);
@@ -1284,7 +1297,7 @@ template <int NB>
 __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __restrict__ wpk, size_t stride_e,
                                                               int n_out, int n_ent,
                                                               const int32_t* __restrict__ sel, GemmX x,
-                                                              float* __restrict__ out) {
+                                                              float* __restrict__ out, int act_pad) {
   constexpr int TB = (int)TB4;
   constexpr int XB = 16 * QK;  // one super-block of 16 members' quants
   constexpr int NW = GU16_WAVES;
@@ -1300,6 +1313,28 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __
   const int t64 = o >> 2, t16 = o & 3;
   // the selections (T*K <= 64 entries; their workspace slot holds 64) into the wave's own slots
   lds_dma4(reinterpret_cast<const uint8_t*>(sel + lane), reinterpret_cast<uint8_t*>(selw + 64 * w));
+  // act copies: NB super-blocks x 4 KB as 4·NB wave copies of 1 KB, copy j = super-block j/4,
+  // members 4(j%4)..+3; wave w issues copies w, w+NW, ... (repeats of the last copy rewrite the
+  // same bytes). Member m's row: 16e + m with act_pad (rows past the expert's members hold
+  // whatever was there; their outputs are not stored), else group position first + m (members
+  // past the last repeat its row).
+  auto act_copies = [&](int first, int cnt) {
+    const int m = lane >> 4, p = lane & 15;
+#pragma unroll
+    for (int t = 0; t < NC; ++t) {
+      const int j = min(w + NW * t, 4 * NB - 1);
+      const int b = j >> 2, mm = 4 * (j & 3) + m;
+      const int row = first + min(mm, cnt - 1);
+      lds_dma16(reinterpret_cast<const uint8_t*>(x.q) + (size_t)row * (NB * QK) + b * QK + 16 * (p ^ mm),
+                xs + j * 1024);
+    }
+    // scales: wave w < 2 copies entries 64w.. of [b][16]; the others copy into spare space
+    const int u = min(64 * w + lane, 16 * NB - 1);
+    const int row = first + min(u & 15, cnt - 1);
+    lds_dma4(reinterpret_cast<const uint8_t*>(x.sx + (size_t)row * NB + (u >> 4)),
+             reinterpret_cast<uint8_t*>(sxs + 64 * w));
+  };
+  if (act_pad) act_copies(16 * e, 16);
   const size_t tile_bytes = (size_t)NB * TB;
   const __amdgpu_buffer_rsrc_t rsrc = buf_rsrc(wpk + (size_t)e * stride_e + (size_t)t64 * tile_bytes,
                                                (uint32_t)tile_bytes);
@@ -1310,7 +1345,8 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __
   Gu16H wr[GU16_SLOTS];
   half_load(wr[0], 0);
   __builtin_amdgcn_sched_barrier(0);
-  // this wave's selection copy landed (the weight loads issued after it may still be in flight)
+  // this wave's selection copy (and act copies) landed (the weight loads issued after them may
+  // still be in flight)
   constexpr int WS = 3;
   __builtin_amdgcn_s_waitcnt(0x3f70 | (WS & 15) | ((WS >> 4) << 14));
   // the expert's entries (entry i on lane i) and the entries of smaller expert ids (the first
@@ -1322,26 +1358,7 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __
     __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
     return;
   }
-  const int base = __popcll(__ballot(sv >= 0 && sv < e));
-  {
-    // act copies: NB super-blocks x 4 KB as 4·NB wave copies of 1 KB, copy j = super-block j/4,
-    // members 4(j%4)..+3 (members past cnt repeat the last one's row); wave w issues copies w,
-    // w+NW, ... (repeats of the last copy rewrite the same bytes)
-    const int m = lane >> 4, p = lane & 15;
-#pragma unroll
-    for (int t = 0; t < NC; ++t) {
-      const int j = min(w + NW * t, 4 * NB - 1);
-      const int b = j >> 2, mm = 4 * (j & 3) + m;
-      const int row = base + min(mm, cnt - 1);
-      lds_dma16(reinterpret_cast<const uint8_t*>(x.q) + (size_t)row * (NB * QK) + b * QK + 16 * (p ^ mm),
-                xs + j * 1024);
-    }
-    // scales: wave w < 2 copies entries 64w.. of [b][16]; the others copy into spare space
-    const int u = min(64 * w + lane, 16 * NB - 1);
-    const int row = base + min(u & 15, cnt - 1);
-    lds_dma4(reinterpret_cast<const uint8_t*>(x.sx + (size_t)row * NB + (u >> 4)),
-             reinterpret_cast<uint8_t*>(sxs + 64 * w));
-  }
+  if (!act_pad) act_copies(__popcll(__ballot(sv >= 0 && sv < e)), cnt);
   constexpr int NL = AHEAD - 1 < NB - 1 ? AHEAD - 1 : NB - 1;  // halves requested after the copies
 #pragma unroll
   for (int h = 1; h <= NL; ++h) half_load(wr[h], h);
@@ -1384,7 +1401,8 @@ constexpr int WIDE_MIN_AVG = 192;
 template <int DT, int KIND>
 static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, int T, int n_in, int n_out,
                               int n_t64, int E, int K, const RouteBufs& rb, GemmX x, float* out,
-                              int8_t* aq = nullptr, float* aq_sx = nullptr, bool* quantized = nullptr) {
+                              int8_t* aq = nullptr, float* aq_sx = nullptr, bool* quantized = nullptr,
+                              bool act_pad = false) {
   if (quantized) *quantized = false;
   const int n_ent = T * K;
   if constexpr (DT == DT_Q6_K && KIND == GEMM_DOWN) {
@@ -1410,25 +1428,25 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
   if constexpr (DT == DT_Q4_K && KIND == GEMM_GATEUP) {
     // decode batches of at most 16 tokens: k_gateup16 (input rows of 512 or 2048), which also
     // quantises the act rows into the caller's buffers
-    if (mt == 1 && rb.sel && aq && T <= 16 && n_ent <= 64 && E <= 32 && n_out % QK == 0 &&
-        (n_in == 2048 || n_in == 512)) {
+    if (rb.sel && gateup16_applies(DT, T, n_in, n_out, E, K, aq != nullptr)) {
       const dim3 grid(E * (n_out / QK)), block(64 * GU16_WAVES);
       if (n_in == 2048)
-        BB_LAUNCH(k_gateup16<8>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx);
+        BB_LAUNCH(k_gateup16<8>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx,
+                  (int)act_pad);
       else
-        BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx);
+        BB_LAUNCH(k_gateup16<2>, grid, block, 0, s, w, stride_e, E, K, n_out, T, rb.sel, x, out, aq, aq_sx,
+                  (int)act_pad);
       if (quantized) *quantized = true;
       return hipGetLastError();
     }
   }
   if constexpr (DT == DT_Q4_K && KIND == GEMM_DOWN) {
     // decode batches of at most 16 tokens (an expert then has at most 16 members): k_down16
-    if (mt == 1 && rb.sel && T <= 16 && n_ent <= 64 && n_out % 256 == 0 && n_in % QK == 0 && n_in / QK >= 1 &&
-        n_in / QK <= 8) {
+    if (rb.sel && down16_applies(DT, T, n_out, n_in, E, K)) {
       const dim3 grid(E * (n_out / 256)), block(64 * GU16_WAVES);
       switch (n_in / QK) {
 #define BB_DOWN16(nb) \
-  case nb: BB_LAUNCH(k_down16<nb>, grid, block, 0, s, w, stride_e, n_out, n_ent, rb.sel, x, out); break;
+  case nb: BB_LAUNCH(k_down16<nb>, grid, block, 0, s, w, stride_e, n_out, n_ent, rb.sel, x, out, (int)act_pad); break;
         BB_DOWN16(1) BB_DOWN16(2) BB_DOWN16(3) BB_DOWN16(4) BB_DOWN16(5) BB_DOWN16(6) BB_DOWN16(7) BB_DOWN16(8)
 #undef BB_DOWN16
       }
@@ -1468,15 +1486,21 @@ static hipError_t launch_gemm(hipStream_t s, const uint8_t* w, size_t stride_e, 
 
 hipError_t launch_gemm_gateup(hipStream_t s, int dtype, const uint8_t* gu, size_t stride_gu, int T, int H, int F,
                               int E, int K, const RouteBufs& rb, GemmX x, float* act, int8_t* aq, float* aq_sx,
-                              bool* quantized) {
+                              bool* quantized, bool act_pad) {
+  // act_pad: only where k_gateup16 and k_down16 both run (the act rows' layout is theirs)
+  if (act_pad && !(gateup16_applies(dtype, T, H, F, E, K, aq != nullptr) && rb.sel)) return hipErrorInvalidValue;
   if (dtype == DT_Q4_K)
-    return launch_gemm<DT_Q4_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act, aq, aq_sx, quantized);
+    return launch_gemm<DT_Q4_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act, aq, aq_sx, quantized,
+                                             act_pad);
   return launch_gemm<DT_Q6_K, GEMM_GATEUP>(s, gu, stride_gu, T, H, F, F / 32, E, K, rb, x, act, aq, aq_sx, quantized);
 }
 
 hipError_t launch_gemm_down(hipStream_t s, int dtype, const uint8_t* dn, size_t stride_dn, int T, int H, int F, int E,
-                            int K, const RouteBufs& rb, GemmX x, float* slots) {
-  if (dtype == DT_Q4_K) return launch_gemm<DT_Q4_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots);
+                            int K, const RouteBufs& rb, GemmX x, float* slots, bool act_pad) {
+  if (act_pad && !(down16_applies(dtype, T, H, F, E, K) && rb.sel)) return hipErrorInvalidValue;
+  if (dtype == DT_Q4_K)
+    return launch_gemm<DT_Q4_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots, nullptr, nullptr,
+                                           nullptr, act_pad);
   return launch_gemm<DT_Q6_K, GEMM_DOWN>(s, dn, stride_dn, T, F, H, H / 64, E, K, rb, x, slots);
 }
 
