@@ -1093,7 +1093,7 @@ bool down16_applies(int dtype, int T, int H, int F, int E, int K) {
 // (XOR-swizzled 16-byte chunks, as k_gemm stages them) and their scales are copied into LDS
 // once, at the block's start, and shared by its waves. No wave reads another wave's weight rows,
 // so a lane loads its 48 bytes per row and super-block (header and two qs words, the g-major
-// order of q4_block) straight into registers, two super-blocks ahead, through a buffer resource
+// order of q4_block) straight into registers, a super-block ahead, through a buffer resource
 // on its packed tile (fixed per-lane offsets, the super-block's offset wave-uniform).
 // The block's expert is known from its id, so its first weights are requested before the
 // selections are read (a block of an expert nobody chose wastes them and leaves). The integer
@@ -1102,12 +1102,18 @@ bool down16_applies(int dtype, int T, int H, int F, int E, int K) {
 // The block then also writes the Q8 of its members' act rows at super-block j (quantize_q8,
 // model.rs:530-534, the k_quant_rows arithmetic) from its SwiGLU values gathered in LDS, so the
 // down GEMM's input needs no launch of its own.
-constexpr int GU16_SLOTS = 5;  // register slots of one row tile and super-block per lane
+// Register slots of one row tile and super-block per lane: gate/up 3 (a super-block in flight
+// while one half is computed), down 2 (k_down16: one half ahead). Deeper rings measured slower
+// (config 2, same box, gate/up and down slots 5/5: 49.2 µs a step, 3/4: 48.2, 5/2: 48.3, 2/2:
+// 47.4, 3/2: 46.85): the 224-256 blocks' first requests all go out at once, and the deeper the
+// ring the longer the burst that delays the selection and activation reads behind it.
+constexpr int GU16_SLOTS = 3;
+constexpr int DN16_SLOTS = 2;
 constexpr int GU16_WAVES = 16;
 
 // A lane's bytes of one row tile and super-block (header and its two qs words). The wave streams
 // its 2·NB (super-block, tile) halves through GU16_SLOTS register slots: half h is computed while
-// halves h+1 .. h+GU16_SLOTS-1 (two super-blocks) are in flight.
+// halves h+1 .. h+GU16_SLOTS-1 are in flight.
 struct Gu16H {
   uint4 h, q0, q1;
 };
@@ -1340,9 +1346,9 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __
                                                (uint32_t)tile_bytes);
   // half h = super-block h of the wave's 16 rows
   const uint32_t og = 16u * (uint32_t)(16 * t16 + r), oq = 1024u * (uint32_t)(1 + 2 * g);
-  constexpr int AHEAD = GU16_SLOTS - 1;
+  constexpr int AHEAD = DN16_SLOTS - 1;
   auto half_load = [&](Gu16H& v, int h) { gu16_load(v, rsrc, og, oq, (uint32_t)(h * TB)); };
-  Gu16H wr[GU16_SLOTS];
+  Gu16H wr[DN16_SLOTS];
   half_load(wr[0], 0);
   __builtin_amdgcn_sched_barrier(0);
   // this wave's selection copy (and act copies) landed (the weight loads issued after them may
@@ -1372,9 +1378,9 @@ __global__ void __launch_bounds__(64 * GU16_WAVES, 4) k_down16(const uint8_t* __
 #pragma unroll
   for (int h = 0; h < NB; ++h) {
     // the slot half h-1 used takes half h+AHEAD
-    if (h + AHEAD < NB) half_load(wr[(h + AHEAD) % GU16_SLOTS], h + AHEAD);
+    if (h + AHEAD < NB) half_load(wr[(h + AHEAD) % DN16_SLOTS], h + AHEAD);
     __builtin_amdgcn_sched_barrier(0);
-    const Gu16H& cur = wr[h % GU16_SLOTS];
+    const Gu16H& cur = wr[h % DN16_SLOTS];
     gu16_tile(cur.h, cur.q0, cur.q1, xs + h * XB, sxs + 16 * h, acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(acc[i]));
