@@ -149,6 +149,15 @@ struct SmemRoute {
   float sx[RT_MAX][GU_H_MAX / QK];
 };
 
+// One token gated in the block (RM_GATE, T = 1): the token's XQ record, copied into LDS at the
+// block's start so the dots do not wait for its reads after the weights (the spare tails take
+// the copies' clamped lanes).
+struct SmemXrec {
+  int8_t q[GU_H_MAX];
+  uint32_t pairs[128];  // [GU_H_MAX / QK][12]
+  float sx[64];         // [GU_H_MAX / QK]
+};
+
 __device__ void route_block(const float* __restrict__ Wr, const float* __restrict__ bias, const float* __restrict__ x,
                             int T, int H, int E, int K, bool global_out, RouteBufs rb, SmemRoute& sm,
                             uint64_t* exptab, uint64_t exp_e) {
@@ -343,6 +352,27 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   constexpr bool ROUTE = RM == RM_ROUTE;
   __shared__ __align__(16) typename std::conditional<ROUTE, SmemRoute, char>::type rt;
   __shared__ int32_t gsel[RM == RM_GATE ? RT_MAX * 8 : 1];
+  constexpr bool XREC = KIND == GEMV_GATEUP && RM == RM_GATE;
+  __shared__ __align__(16) typename std::conditional<XREC, SmemXrec, char>::type xr;
+  // (XREC, one token: waves 1-4, which gate nothing, read the token's XQ record while wave 0
+  // gates, and store it to LDS after; the barrier before the dots publishes it)
+  uint4 xr_q = {0, 0, 0, 0};
+  uint32_t xr_p0 = 0, xr_p1 = 0;
+  float xr_s = 0.0f;
+  const int xr_w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), xr_l = threadIdx.x & 63;
+  if constexpr (XREC) {
+    if (T == 1) {
+      const int nbq = H / QK;
+      if (xr_w == 1 || xr_w == 2) {
+        xr_q = reinterpret_cast<const uint4*>(xq_q)[min(64 * (xr_w - 1) + xr_l, H / 16 - 1)];
+      } else if (xr_w == 3) {
+        xr_p0 = xq_pairs[min(xr_l, 12 * nbq - 1)];
+        xr_p1 = xq_pairs[min(64 + xr_l, 12 * nbq - 1)];
+      } else if (xr_w == 4) {
+        xr_s = xq_sx[min(xr_l, nbq - 1)];
+      }
+    }
+  }
   if constexpr (ROUTE) {
     route_block(router, bias, x_in, T, H, E, K, blockIdx.x == 0, rb, rt, exptab, exp_e);
     sel = rt.sel;
@@ -355,6 +385,17 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   // expert, and its selections are in LDS, so every thread finds the block's experts and their
   // entries from them directly (no member lists and none of their barriers).
   const bool one = KIND == GEMV_GATEUP && RM != RM_NONE && T == 1;
+  if constexpr (XREC) {
+    if (one) {
+      if (xr_w == 1 || xr_w == 2) reinterpret_cast<uint4*>(xr.q)[64 * (xr_w - 1) + xr_l] = xr_q;
+      else if (xr_w == 3) {
+        xr.pairs[xr_l] = xr_p0;
+        xr.pairs[64 + xr_l] = xr_p1;
+      } else if (xr_w == 4) {
+        xr.sx[xr_l] = xr_s;
+      }
+    }
+  }
   auto entry_of = [&](int ex) {
     int k0 = 0;
     for (int k = 0; k < K; ++k) k0 = sel[k] == ex ? k : k0;
@@ -402,6 +443,7 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
   }
   typename R::Loaded L;
   if (has_blk) R::load(L, tile_addr(e, tile));
+  if (XREC && one) lds_barrier();  // the XQ record in LDS
   if (!one) {
     if (n_mem <= MST) stage(0, n_mem);
     lds_barrier();
@@ -431,6 +473,13 @@ __global__ void __launch_bounds__(512) k_experts(const uint8_t* __restrict__ wpk
             const int tok = one ? 0 : __builtin_amdgcn_readfirstlane(mem.list[c0 + m] / K);
             if constexpr (ROUTE) {
               tv.v[m][w][lane] = R::value(B, rt.q[tok] + w * QK, rt.pairs[tok][w], rt.sx[tok][w]);
+            } else if constexpr (XREC) {
+              if (one) {
+                tv.v[m][w][lane] = R::value(B, xr.q + w * QK, xr.pairs + 12 * w, xr.sx[w]);
+              } else {
+                const size_t xb = (size_t)tok * nb + w;
+                tv.v[m][w][lane] = R::value(B, xq_q + xb * QK, xq_pairs + xb * 12, xq_sx[xb]);
+              }
             } else {
               const size_t xb = (size_t)tok * nb + w;
               tv.v[m][w][lane] = R::value(B, xq_q + xb * QK, xq_pairs + xb * 12, xq_sx[xb]);
