@@ -808,6 +808,10 @@ __global__ void __launch_bounds__(256) k_residual_norm_route(const float* __rest
       hr[it] = h_in[row + min(tid + 256 * it, n - 1)];
       yr[it] = 0.0f;
     }
+    // the weights' loads complete here, behind the rows' (the compiler would otherwise issue
+    // each just before its use below, one round trip after another)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) asm volatile("" ::"s"(wk[k]));
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if (k < K) {
