@@ -1,11 +1,13 @@
-"""GPU parity of the Q4_K gate/up GEMM of decode batches (k_gateup16: at most 16 tokens, T*k <= 64,
-hidden 512 or 2048, member tiles of every token of the batch, weight rows streamed into registers,
-16-wave blocks over 256 outputs of one expert that also write the act rows' Q8 for the down GEMM)
-on the grouped path, against the CPU restatement of Model::moe_ffn_batch (model.rs:286-371):
-routing, weights and block outputs bit-identical. The cases reach its edges: a single expert,
-experts nobody chose (their blocks leave early), one-member experts (sums started at -0.0), k = 8
-with 8 tokens (64 entries), k = E, moe_ff of 1, 4, 5 and 7 act super-blocks, zero and scaled
-input rows (a zero act block quantises to scale 0).
+"""GPU parity of the Q4_K GEMMs of decode batches (at most 16 tokens, T*k <= 64) on the grouped
+path: the gate/up kernel k_gateup16 (hidden 512 or 2048, member tiles of every token of the batch,
+weight rows streamed into registers, 16-wave blocks over 256 outputs of one expert that also write
+the act rows' Q8) and, where the down experts are Q4_K, the down kernel k_down16 (the expert's at
+most 16 members, act Q8 rows at 16e + m, 16-wave blocks over 256 rows), against the CPU
+restatement of Model::moe_ffn_batch (model.rs:286-371): routing, weights and block outputs
+bit-identical. The cases reach their edges: a single expert, experts nobody chose (their blocks
+leave early), one-member experts (sums started at -0.0), k = 8 with 8 tokens (64 entries), k = E,
+moe_ff of 1, 3, 4, 5, 7 and 8 act super-blocks, zero and scaled input rows (a zero act block
+quantises to scale 0).
 """
 import numpy as np
 import pytest
@@ -36,6 +38,8 @@ CASES = [
     (6, 2048, 256, 5, 5, 12, Q6_K),    # k = E: every token chooses every expert
     (7, 512, 1280, 7, 2, 16, Q4_K),    # moe_ff 1280: 5 blocks per expert, 40 packed tiles
     (8, 2048, 1792, 32, 4, 2, Q6_K),
+    (9, 512, 2048, 16, 2, 16, Q4_K),   # moe_ff 2048: k_down16 over 8 act super-blocks, 2 blocks per expert
+    (10, 2048, 768, 32, 4, 16, Q4_K),  # moe_ff 768: k_down16 over 3, the padded act rows of 32 experts
 ]
 
 
